@@ -1,0 +1,219 @@
+// extern "C" entry points of libeinsum_ir_hip.so (declared in
+// include/einsum_ir_hip.h).  Thin: argument checks, plan ownership, error
+// strings; planning and kernels live in contract_plan.cpp / permute.hip.
+#include "etir_internal.h"
+#include <cstdio>
+#include <cstring>
+
+namespace etir {
+
+namespace {
+thread_local std::string t_last_error;
+}
+
+void set_error( std::string const & msg ) {
+  t_last_error = msg;
+}
+
+int fail( int code, std::string const & msg ) {
+  t_last_error = msg;
+  return code;
+}
+
+}  // namespace etir
+
+using etir::fail;
+
+extern "C" {
+
+int etir_hip_contraction_create( int64_t         num_loops,
+                                 int32_t const * dim_types,
+                                 int64_t const * sizes,
+                                 int64_t const * strides_left,
+                                 int64_t const * strides_right,
+                                 int64_t const * strides_out_aux,
+                                 int64_t const * strides_out,
+                                 int32_t         dtype_left,
+                                 int32_t         dtype_right,
+                                 int32_t         dtype_comp,
+                                 int32_t         dtype_out,
+                                 int32_t         ktype_first_touch,
+                                 int32_t         ktype_main,
+                                 int32_t         ktype_last_touch,
+                                 etir_plan_t   * plan ) {
+  if( plan == nullptr ) return fail( ETIR_UNDEFINED_ERROR, "plan output pointer is null" );
+  *plan = nullptr;
+  int l_device = 0;
+  ETIR_HIP_CHECK( hipGetDevice( &l_device ) );
+  etir_plan_s * l_plan = new etir_plan_s();
+  l_plan->kind = 1;
+  l_plan->device = l_device;
+  int l_err = etir::plan_contraction( num_loops, dim_types, sizes,
+                                      strides_left, strides_right, strides_out_aux, strides_out,
+                                      dtype_left, dtype_right, dtype_comp, dtype_out,
+                                      ktype_first_touch, ktype_main, ktype_last_touch,
+                                      l_plan->cont );
+  if( l_err != ETIR_SUCCESS ) {
+    if( l_plan->cont.d_tables != nullptr ) (void) hipFree( l_plan->cont.d_tables );
+    delete l_plan;
+    return l_err;
+  }
+  *plan = l_plan;
+  return ETIR_SUCCESS;
+}
+
+int etir_hip_contraction_execute( etir_plan_t  plan,
+                                  void const * left,
+                                  void const * right,
+                                  void const * out_aux,
+                                  void       * out,
+                                  void       * stream ) {
+  if( plan == nullptr || plan->kind != 1 ) {
+    return fail( ETIR_CALLED_BEFORE_COMPILATION, "not a contraction plan" );
+  }
+  return etir::launch_contraction( plan->cont, left, right, out_aux, out,
+                                   reinterpret_cast< hipStream_t >( stream ) );
+}
+
+int etir_hip_permute_create( int64_t         num_dims,
+                             int64_t const * sizes,
+                             int64_t const * strides_in,
+                             int64_t const * strides_out,
+                             int32_t         dtype_in,
+                             int32_t         dtype_comp,
+                             int32_t         dtype_out,
+                             int32_t         ktype_main,
+                             etir_plan_t   * plan ) {
+  if( plan == nullptr ) return fail( ETIR_UNDEFINED_ERROR, "plan output pointer is null" );
+  *plan = nullptr;
+  if( dtype_in != dtype_out || ( dtype_comp != dtype_in && dtype_comp != ETIR_UNDEFINED_DTYPE ) ) {
+    return fail( ETIR_INVALID_DTYPE, "permute: input, compute and output dtypes must match" );
+  }
+  int l_device = 0;
+  ETIR_HIP_CHECK( hipGetDevice( &l_device ) );
+  etir_plan_s * l_plan = new etir_plan_s();
+  l_plan->kind = 2;
+  l_plan->device = l_device;
+  int l_err = etir::plan_permute( num_dims, sizes, strides_in, strides_out,
+                                  dtype_in, ktype_main, l_plan->perm );
+  if( l_err != ETIR_SUCCESS ) {
+    delete l_plan;
+    return l_err;
+  }
+  *plan = l_plan;
+  return ETIR_SUCCESS;
+}
+
+int etir_hip_permute_execute( etir_plan_t  plan,
+                              void const * in,
+                              void       * out,
+                              void       * stream ) {
+  if( plan == nullptr || plan->kind != 2 ) {
+    return fail( ETIR_CALLED_BEFORE_COMPILATION, "not a permutation plan" );
+  }
+  return etir::launch_permute( plan->perm, in, out, reinterpret_cast< hipStream_t >( stream ) );
+}
+
+int etir_hip_plan_destroy( etir_plan_t plan ) {
+  if( plan == nullptr ) return ETIR_SUCCESS;
+  if( plan->kind == 1 && plan->cont.d_tables != nullptr ) {
+    ETIR_HIP_CHECK( hipFree( plan->cont.d_tables ) );
+  }
+  delete plan;
+  return ETIR_SUCCESS;
+}
+
+int etir_hip_plan_describe( etir_plan_t plan, char * buf, int64_t len ) {
+  if( plan == nullptr || buf == nullptr || len <= 0 ) {
+    return fail( ETIR_UNDEFINED_ERROR, "describe: invalid arguments" );
+  }
+  std::string l_s;
+  if( plan->kind == 1 ) {
+    l_s = plan->cont.desc;
+  }
+  else {
+    static char const * l_modes[] = { "fill", "transpose", "copy_vec", "gather" };
+    etir::PermutePlan const & p = plan->perm;
+    char l_tmp[256];
+    std::snprintf( l_tmp, sizeof( l_tmp ), "permute %s dims=%d elems=%lld vec=%d",
+                   l_modes[ (int) p.mode ], p.num_dims, (long long) p.num_elements, p.args.vec_ok );
+    l_s = l_tmp;
+  }
+  std::strncpy( buf, l_s.c_str(), (std::size_t) len - 1 );
+  buf[len - 1] = '\0';
+  return ETIR_SUCCESS;
+}
+
+int64_t etir_hip_plan_flops( etir_plan_t plan ) {
+  if( plan == nullptr || plan->kind != 1 ) return 0;
+  return plan->cont.flops;
+}
+
+int64_t etir_hip_plan_bytes( etir_plan_t plan ) {
+  if( plan == nullptr ) return 0;
+  if( plan->kind == 1 ) return plan->cont.bytes;
+  etir::PermutePlan const & p = plan->perm;
+  int64_t l_rw = ( p.ktype == ETIR_KTYPE_ZERO ) ? 1 : ( p.ktype == ETIR_KTYPE_ADD ? 3 : 2 );
+  return l_rw * p.elem_bytes * p.num_elements;
+}
+
+char const * etir_hip_last_error( void ) {
+  return etir::t_last_error.c_str();
+}
+
+int etir_hip_malloc( void ** ptr, int64_t num_bytes ) {
+  if( ptr == nullptr || num_bytes < 0 ) return fail( ETIR_UNDEFINED_ERROR, "malloc: invalid arguments" );
+  *ptr = nullptr;
+  if( num_bytes == 0 ) return ETIR_SUCCESS;
+  ETIR_HIP_CHECK( hipMalloc( ptr, (std::size_t) num_bytes ) );
+  return ETIR_SUCCESS;
+}
+
+int etir_hip_free( void * ptr ) {
+  if( ptr == nullptr ) return ETIR_SUCCESS;
+  ETIR_HIP_CHECK( hipFree( ptr ) );
+  return ETIR_SUCCESS;
+}
+
+int etir_hip_memcpy_h2d( void * dst, void const * src, int64_t num_bytes ) {
+  if( num_bytes <= 0 ) return ETIR_SUCCESS;
+  ETIR_HIP_CHECK( hipMemcpy( dst, src, (std::size_t) num_bytes, hipMemcpyHostToDevice ) );
+  return ETIR_SUCCESS;
+}
+
+int etir_hip_memcpy_d2h( void * dst, void const * src, int64_t num_bytes ) {
+  if( num_bytes <= 0 ) return ETIR_SUCCESS;
+  ETIR_HIP_CHECK( hipMemcpy( dst, src, (std::size_t) num_bytes, hipMemcpyDeviceToHost ) );
+  return ETIR_SUCCESS;
+}
+
+int etir_hip_memcpy_d2d( void * dst, void const * src, int64_t num_bytes, void * stream ) {
+  if( num_bytes <= 0 ) return ETIR_SUCCESS;
+  ETIR_HIP_CHECK( hipMemcpyAsync( dst, src, (std::size_t) num_bytes, hipMemcpyDeviceToDevice,
+                                  reinterpret_cast< hipStream_t >( stream ) ) );
+  return ETIR_SUCCESS;
+}
+
+int etir_hip_memset( void * dst, int32_t value, int64_t num_bytes ) {
+  if( num_bytes <= 0 ) return ETIR_SUCCESS;
+  ETIR_HIP_CHECK( hipMemset( dst, value, (std::size_t) num_bytes ) );
+  return ETIR_SUCCESS;
+}
+
+int etir_hip_synchronize( void * stream ) {
+  if( stream == nullptr ) {
+    ETIR_HIP_CHECK( hipDeviceSynchronize() );
+  }
+  else {
+    ETIR_HIP_CHECK( hipStreamSynchronize( reinterpret_cast< hipStream_t >( stream ) ) );
+  }
+  return ETIR_SUCCESS;
+}
+
+int etir_hip_device_count( void ) {
+  int l_n = 0;
+  if( hipGetDeviceCount( &l_n ) != hipSuccess ) return 0;
+  return l_n;
+}
+
+}  // extern "C"

@@ -1,0 +1,493 @@
+// Contraction planner: loop IR -> one kernel launch.
+//
+// Replaces the reference's loop-nest lowering and primitive choice
+//   BinaryContractionTpp::compile        reference src/backend/BinaryContractionTpp.cpp:4-127
+//   ContractionOptimizer::optimize       reference src/basic/binary/ContractionOptimizer.cpp:47-74
+//     (sort_and_fuse_iters :76-111, set_primitive_iters :232-584,
+//      reorder_and_parallelize_iters :586-679)
+//   ContractionBackend::set_kernel_shape reference src/basic/binary/ContractionBackend.cpp:518-678
+//
+// The reference picks a libxsmm GEMM/BRGEMM over the innermost unit-stride
+// loops and runs every other loop on the host.  Here all loops of one type are
+// flattened into a single kernel index (C -> grid batch, M -> MFMA rows,
+// N -> MFMA columns, K -> reduction) and described by offset tables, so the
+// whole contraction is one launch:
+//   1. size-1 loops are dropped (ContractionOptimizer::remove_empty_iters, :113-121);
+//   2. the kernel's column index (lanes 0..31 of a wave) is put on the
+//      output's unit-stride type, swapping the roles of left and right when
+//      the output is M-contiguous, so that epilogue stores coalesce;
+//   3. inside each type the loops are ordered so that the operand's
+//      unit-stride loop is innermost (the analogue of choosing the
+//      primitive's unit-stride m/k loops);
+//   4. the tables are enumerated and inspected: runs of consecutive offsets
+//      select 16-byte vector loads along M/N or along K; a single-loop K index
+//      becomes an affine offset (no table reads in the K loop);
+//   5. the tile shape is chosen from dtype and the number of output tiles.
+#include "etir_internal.h"
+#include <algorithm>
+#include <cstring>
+#include <limits>
+#include <sstream>
+
+namespace etir {
+
+int launch_contract_f32( int32_t tile, int32_t ma, int32_t mb, ContractArgs const & a,
+                         uint32_t grid, hipStream_t stream );
+int launch_contract_bf16( int32_t tile, int32_t ma, int32_t mb, ContractArgs const & a,
+                          uint32_t grid, hipStream_t stream );
+
+namespace {
+
+// tensor slots inside a loop
+enum { T_L = 0, T_R = 1, T_AUX = 2, T_OUT = 3 };
+
+struct Loop {
+  int32_t type;
+  int64_t size;
+  int64_t s[4];
+};
+
+// enumerates sum_d digit_d * stride_d over the mixed-radix index of dims
+// (outer -> inner)
+std::vector< int64_t > enumerate( std::vector< Loop > const & dims, int slot ) {
+  int64_t l_total = 1;
+  for( Loop const & l_d : dims ) l_total *= l_d.size;
+  std::vector< int64_t > l_tab( (std::size_t) l_total, 0 );
+  if( l_total == 0 ) return l_tab;
+  // fill from the innermost dim outwards: after processing a dim the first
+  // l_filled entries hold the offsets of all inner digits
+  int64_t l_filled = 1;
+  for( int64_t l_di = (int64_t) dims.size() - 1; l_di >= 0; l_di-- ) {
+    int64_t const l_sz = dims[l_di].size;
+    int64_t const l_st = dims[l_di].s[slot];
+    for( int64_t l_it = 1; l_it < l_sz; l_it++ ) {
+      for( int64_t l_e = 0; l_e < l_filled; l_e++ ) {
+        l_tab[l_it * l_filled + l_e] = l_tab[l_e] + l_it * l_st;
+      }
+    }
+    l_filled *= l_sz;
+  }
+  return l_tab;
+}
+
+// true if tab is made of aligned runs of length v with unit increments and
+// every run starts at a multiple of align
+bool runs_contiguous( std::vector< int64_t > const & tab, int64_t v, int64_t align ) {
+  if( (int64_t) tab.size() % v != 0 ) return false;
+  for( std::size_t l_g = 0; l_g < tab.size(); l_g += v ) {
+    if( tab[l_g] % align != 0 ) return false;
+    for( int64_t l_e = 1; l_e < v; l_e++ ) {
+      if( tab[l_g + l_e] != tab[l_g] + l_e ) return false;
+    }
+  }
+  return true;
+}
+
+bool all_multiple( std::vector< int64_t > const & tab, int64_t align ) {
+  for( int64_t l_v : tab ) if( l_v % align != 0 ) return false;
+  return true;
+}
+
+bool fits_i32( std::vector< int64_t > const & tab ) {
+  for( int64_t l_v : tab ) {
+    if( l_v < 0 || l_v > std::numeric_limits< int32_t >::max() ) return false;
+  }
+  return true;
+}
+
+// sorts dims by their stride in `slot`, largest stride (outermost) first
+void order_dims( std::vector< Loop > & dims, int slot ) {
+  std::stable_sort( dims.begin(), dims.end(),
+                    [slot]( Loop const & x, Loop const & y ) { return x.s[slot] > y.s[slot]; } );
+}
+
+// moves the first dim whose stride in `slot` is 1 to the innermost position;
+// returns true if such a dim exists
+bool unit_innermost( std::vector< Loop > & dims, int slot ) {
+  for( std::size_t l_i = 0; l_i < dims.size(); l_i++ ) {
+    if( dims[l_i].s[slot] == 1 ) {
+      Loop l_d = dims[l_i];
+      dims.erase( dims.begin() + l_i );
+      dims.push_back( l_d );
+      return true;
+    }
+  }
+  return false;
+}
+
+std::string dims_str( std::vector< Loop > const & dims ) {
+  std::ostringstream l_s;
+  l_s << "[";
+  for( std::size_t l_i = 0; l_i < dims.size(); l_i++ ) {
+    if( l_i ) l_s << ",";
+    l_s << dims[l_i].size;
+  }
+  l_s << "]";
+  return l_s.str();
+}
+
+char const * mode_str( int32_t m ) {
+  if( m == LOAD_VEC_MN ) return "vec_mn";
+  if( m == LOAD_VEC_K )  return "vec_k";
+  return "scalar";
+}
+
+char const * tile_str( int32_t t ) {
+  switch( t ) {
+    case TILE_F32_128x128:  return "f32_128x128x32";
+    case TILE_F32_64x64:    return "f32_64x64x32";
+    case TILE_BF16_256x256: return "bf16_256x256x64";
+    case TILE_BF16_128x128: return "bf16_128x128x64";
+    case TILE_BF16_64x64:   return "bf16_64x64x64";
+    default:                return "?";
+  }
+}
+
+void tile_shape( int32_t t, int64_t & bm, int64_t & bn ) {
+  switch( t ) {
+    case TILE_F32_128x128:  bm = 128; bn = 128; break;
+    case TILE_F32_64x64:    bm = 64;  bn = 64;  break;
+    case TILE_BF16_256x256: bm = 256; bn = 256; break;
+    case TILE_BF16_128x128: bm = 128; bn = 128; break;
+    default:                bm = 64;  bn = 64;  break;
+  }
+}
+
+}  // namespace
+
+int plan_contraction( int64_t            num_loops,
+                      int32_t const    * dim_types,
+                      int64_t const    * sizes,
+                      int64_t const    * strides_left,
+                      int64_t const    * strides_right,
+                      int64_t const    * strides_out_aux,
+                      int64_t const    * strides_out,
+                      int32_t            dtype_left,
+                      int32_t            dtype_right,
+                      int32_t            dtype_comp,
+                      int32_t            dtype_out,
+                      int32_t            ktype_first_touch,
+                      int32_t            ktype_main,
+                      int32_t            ktype_last_touch,
+                      ContractionPlan  & plan ) {
+  plan = ContractionPlan();
+
+  // ---------------------------------------------------------------- checks
+  bool const l_f32  = dtype_left == ETIR_FP32 && dtype_right == ETIR_FP32
+                   && dtype_comp == ETIR_FP32 && dtype_out == ETIR_FP32;
+  bool const l_bf16 = dtype_left == ETIR_BF16 && dtype_right == ETIR_BF16
+                   && dtype_comp == ETIR_FP32
+                   && ( dtype_out == ETIR_FP32 || dtype_out == ETIR_BF16 );
+  if( dtype_left == ETIR_FP64 || dtype_right == ETIR_FP64 || dtype_out == ETIR_FP64 ) {
+    return fail( ETIR_COMPILATION_FAILED, "contraction: FP64 is not supported by the HIP backend" );
+  }
+  if( !l_f32 && !l_bf16 ) {
+    return fail( ETIR_INVALID_DTYPE, "contraction: unsupported dtype combination" );
+  }
+  if( ktype_main != ETIR_KTYPE_MADD ) {
+    return fail( ETIR_INVALID_KTYPE, "contraction: main kernel must be MADD" );
+  }
+  if(    ktype_first_touch != ETIR_KTYPE_ZERO && ktype_first_touch != ETIR_KTYPE_COPY
+      && ktype_first_touch != ETIR_KTYPE_ADD  && ktype_first_touch != ETIR_KTYPE_UNDEFINED ) {
+    return fail( ETIR_COMPILATION_FAILED, "contraction: unsupported first-touch kernel" );
+  }
+  if(    ktype_last_touch != ETIR_KTYPE_RELU && ktype_last_touch != ETIR_KTYPE_ADD
+      && ktype_last_touch != ETIR_KTYPE_UNDEFINED ) {
+    return fail( ETIR_COMPILATION_FAILED, "contraction: unsupported last-touch kernel" );
+  }
+  if( num_loops < 0 || ( num_loops > 0 && ( dim_types == nullptr || sizes == nullptr
+                                            || strides_left == nullptr || strides_right == nullptr
+                                            || strides_out == nullptr ) ) ) {
+    return fail( ETIR_COMPILATION_FAILED, "contraction: invalid loop arrays" );
+  }
+
+  plan.dtype_in    = dtype_left;
+  plan.dtype_comp  = dtype_comp;
+  plan.dtype_out   = dtype_out;
+  plan.first_touch = ktype_first_touch;
+  plan.last_touch  = ktype_last_touch;
+  plan.needs_aux   =    ktype_first_touch == ETIR_KTYPE_COPY
+                     || ktype_first_touch == ETIR_KTYPE_ADD
+                     || ktype_last_touch  == ETIR_KTYPE_ADD;
+  // without explicit aux strides the aux tensor shares the output's layout
+  // (reference src/backend/BinaryContractionTpp.cpp:36-41)
+  int64_t const * l_s_aux = strides_out_aux != nullptr ? strides_out_aux : strides_out;
+
+  // ------------------------------------------------------------- loop sets
+  std::vector< Loop > l_c, l_m, l_n, l_k;
+  for( int64_t l_lo = 0; l_lo < num_loops; l_lo++ ) {
+    if( sizes[l_lo] < 0 ) return fail( ETIR_COMPILATION_FAILED, "contraction: negative loop size" );
+    if(    strides_left[l_lo] < 0 || strides_right[l_lo] < 0 || strides_out[l_lo] < 0
+        || l_s_aux[l_lo] < 0 ) {
+      return fail( ETIR_COMPILATION_FAILED, "contraction: negative stride" );
+    }
+    Loop l_lp{ dim_types[l_lo], sizes[l_lo],
+               { strides_left[l_lo], strides_right[l_lo], l_s_aux[l_lo], strides_out[l_lo] } };
+    if( l_lp.type == ETIR_DIM_I || l_lp.type == ETIR_DIM_J ) continue;
+    if( l_lp.size == 1 ) continue;
+    if(      l_lp.type == ETIR_DIM_C ) l_c.push_back( l_lp );
+    else if( l_lp.type == ETIR_DIM_M ) l_m.push_back( l_lp );
+    else if( l_lp.type == ETIR_DIM_N ) l_n.push_back( l_lp );
+    else if( l_lp.type == ETIR_DIM_K ) l_k.push_back( l_lp );
+    else return fail( ETIR_COMPILATION_FAILED, "contraction: invalid dimension type" );
+  }
+
+  auto prod = []( std::vector< Loop > const & d ) {
+    int64_t l_p = 1;
+    for( Loop const & l_x : d ) l_p *= l_x.size;
+    return l_p;
+  };
+  int64_t const l_size_c = prod( l_c );
+  int64_t const l_size_m = prod( l_m );
+  int64_t const l_size_n = prod( l_n );
+  int64_t const l_size_k = prod( l_k );
+
+  // ------------------------------------------------------------ role swap
+  // kernel columns (lane index) go to the output's unit-stride type
+  bool l_swap = false;
+  for( Loop const & l_x : l_m ) if( l_x.s[T_OUT] == 1 ) l_swap = true;
+  plan.swapped = l_swap;
+
+  // kernel operand slots: A (rows), B (columns)
+  int const l_sa = l_swap ? T_R : T_L;
+  int const l_sb = l_swap ? T_L : T_R;
+  std::vector< Loop > l_km = l_swap ? l_n : l_m;   // kernel-M loops (A, aux, out)
+  std::vector< Loop > l_kn = l_swap ? l_m : l_n;   // kernel-N loops (B, aux, out)
+  int64_t const l_kern_m = l_swap ? l_size_n : l_size_m;
+  int64_t const l_kern_n = l_swap ? l_size_m : l_size_n;
+
+  int64_t const l_esz = ( dtype_left == ETIR_BF16 ) ? 2 : 4;
+  int64_t const l_vk  = 16 / l_esz;   // elements per 16-byte vector along K
+  int64_t const l_vr  = 4;            // rows per vector along M/N
+
+  // ordering
+  order_dims( l_km, l_sa );
+  unit_innermost( l_km, l_sa );
+  order_dims( l_kn, T_OUT );
+  if( !unit_innermost( l_kn, T_OUT ) ) unit_innermost( l_kn, l_sb );
+  // K: the operand whose unit-stride loop is a K loop decides the order
+  bool l_a_unit_k = false, l_b_unit_k = false;
+  for( Loop const & l_x : l_k ) {
+    if( l_x.s[l_sa] == 1 ) l_a_unit_k = true;
+    if( l_x.s[l_sb] == 1 ) l_b_unit_k = true;
+  }
+  int const l_k_slot = l_a_unit_k ? l_sa : ( l_b_unit_k ? l_sb : l_sa );
+  order_dims( l_k, l_k_slot );
+  unit_innermost( l_k, l_k_slot );
+  order_dims( l_c, T_OUT );
+
+  // --------------------------------------------------------------- tables
+  std::vector< int64_t > l_tc_a   = enumerate( l_c, l_sa );
+  std::vector< int64_t > l_tc_b   = enumerate( l_c, l_sb );
+  std::vector< int64_t > l_tc_aux = enumerate( l_c, T_AUX );
+  std::vector< int64_t > l_tc_out = enumerate( l_c, T_OUT );
+  std::vector< int64_t > l_tm_a   = enumerate( l_km, l_sa );
+  std::vector< int64_t > l_tm_aux = enumerate( l_km, T_AUX );
+  std::vector< int64_t > l_tm_out = enumerate( l_km, T_OUT );
+  std::vector< int64_t > l_tn_b   = enumerate( l_kn, l_sb );
+  std::vector< int64_t > l_tn_aux = enumerate( l_kn, T_AUX );
+  std::vector< int64_t > l_tn_out = enumerate( l_kn, T_OUT );
+  std::vector< int64_t > l_tk_a   = enumerate( l_k, l_sa );
+  std::vector< int64_t > l_tk_b   = enumerate( l_k, l_sb );
+
+  int64_t const l_max_i32 = std::numeric_limits< int32_t >::max();
+  if(    l_size_m > l_max_i32 || l_size_n > l_max_i32 || l_size_k > l_max_i32
+      || l_size_c > l_max_i32 ) {
+    return fail( ETIR_COMPILATION_FAILED, "contraction: flattened index exceeds int32" );
+  }
+  if(    !fits_i32( l_tm_a ) || !fits_i32( l_tm_aux ) || !fits_i32( l_tm_out )
+      || !fits_i32( l_tn_b ) || !fits_i32( l_tn_aux ) || !fits_i32( l_tn_out )
+      || !fits_i32( l_tk_a ) || !fits_i32( l_tk_b ) ) {
+    return fail( ETIR_COMPILATION_FAILED, "contraction: per-type offsets exceed int32" );
+  }
+  int64_t const l_total_entries = 4 * l_size_c + 3 * ( l_size_m + l_size_n ) + 2 * l_size_k;
+  if( l_total_entries > ( int64_t( 1 ) << 27 ) ) {
+    return fail( ETIR_COMPILATION_FAILED, "contraction: offset tables too large" );
+  }
+
+  // ------------------------------------------------------- load modes
+  auto pick_mode = [&]( std::vector< int64_t > const & rows,
+                        std::vector< int64_t > const & tk,
+                        std::vector< int64_t > const & tc ) -> int32_t {
+    // vectors of 4 consecutive rows: 16 B (fp32) / 8 B (bf16)
+    if(    rows.size() > 0 && runs_contiguous( rows, l_vr, l_vr )
+        && all_multiple( tk, l_vr ) && all_multiple( tc, l_vr ) ) {
+      return LOAD_VEC_MN;
+    }
+    // 16-byte vectors along K
+    if(    tk.size() > 0 && runs_contiguous( tk, l_vk, l_vk )
+        && all_multiple( rows, l_vk ) && all_multiple( tc, l_vk ) ) {
+      return LOAD_VEC_K;
+    }
+    return LOAD_SCALAR;
+  };
+  plan.mode_a = pick_mode( l_tm_a, l_tk_a, l_tc_a );
+  plan.mode_b = pick_mode( l_tn_b, l_tk_b, l_tc_b );
+
+  bool l_k_affine = true;
+  int64_t l_sk_a = l_tk_a.size() > 1 ? l_tk_a[1] : 0;
+  int64_t l_sk_b = l_tk_b.size() > 1 ? l_tk_b[1] : 0;
+  for( std::size_t l_i = 0; l_i < l_tk_a.size(); l_i++ ) {
+    if( l_tk_a[l_i] != int64_t( l_i ) * l_sk_a || l_tk_b[l_i] != int64_t( l_i ) * l_sk_b ) {
+      l_k_affine = false;
+      break;
+    }
+  }
+
+  // ---------------------------------------------------------- tile choice
+  auto n_tiles = [&]( int32_t t ) {
+    int64_t l_bm, l_bn;
+    tile_shape( t, l_bm, l_bn );
+    return ( ( l_kern_m + l_bm - 1 ) / l_bm ) * ( ( l_kern_n + l_bn - 1 ) / l_bn ) * l_size_c;
+  };
+  int64_t const l_cus = 256;
+  if( l_f32 ) {
+    plan.tile = ( n_tiles( TILE_F32_128x128 ) >= l_cus ) ? TILE_F32_128x128 : TILE_F32_64x64;
+  }
+  else {
+    if(      n_tiles( TILE_BF16_256x256 ) >= l_cus ) plan.tile = TILE_BF16_256x256;
+    else if( n_tiles( TILE_BF16_128x128 ) >= l_cus ) plan.tile = TILE_BF16_128x128;
+    else                                             plan.tile = TILE_BF16_64x64;
+  }
+  int64_t l_bm, l_bn;
+  tile_shape( plan.tile, l_bm, l_bn );
+
+  plan.C = l_size_c;
+  plan.M = l_kern_m;
+  plan.N = l_kern_n;
+  plan.K = l_size_k;
+  plan.flops = 2 * l_size_c * l_size_m * l_size_n * l_size_k;
+  int64_t const l_esz_out = ( dtype_out == ETIR_BF16 ) ? 2 : 4;
+  bool const l_read_out = ktype_first_touch == ETIR_KTYPE_ADD || ktype_first_touch == ETIR_KTYPE_UNDEFINED;
+  plan.bytes =   l_esz * l_size_c * ( l_size_m + l_size_n ) * l_size_k
+               + l_esz_out * l_size_c * l_size_m * l_size_n * ( 1 + ( l_read_out ? 1 : 0 )
+                                                                  + ( plan.needs_aux ? 1 : 0 ) );
+
+  std::ostringstream l_d;
+  l_d << "contract " << tile_str( plan.tile )
+      << " C=" << l_size_c << dims_str( l_c )
+      << " M=" << plan.M << dims_str( l_km )
+      << " N=" << plan.N << dims_str( l_kn )
+      << " K=" << plan.K << dims_str( l_k )
+      << " A=" << ( l_swap ? "right" : "left" ) << ":" << mode_str( plan.mode_a )
+      << " B=" << ( l_swap ? "left" : "right" ) << ":" << mode_str( plan.mode_b )
+      << " k_affine=" << ( l_k_affine ? 1 : 0 );
+  plan.desc = l_d.str();
+
+  // ------------------------------------------------------ device tables
+  // layout: int64 C tables first (8-byte aligned), then int32 tables
+  std::vector< int64_t > l_c64;
+  l_c64.insert( l_c64.end(), l_tc_a.begin(),   l_tc_a.end() );
+  l_c64.insert( l_c64.end(), l_tc_b.begin(),   l_tc_b.end() );
+  l_c64.insert( l_c64.end(), l_tc_aux.begin(), l_tc_aux.end() );
+  l_c64.insert( l_c64.end(), l_tc_out.begin(), l_tc_out.end() );
+  std::vector< int32_t > l_t32;
+  auto app32 = [&]( std::vector< int64_t > const & t ) {
+    for( int64_t l_v : t ) l_t32.push_back( (int32_t) l_v );
+  };
+  std::size_t const l_o_tm_a = l_t32.size(); app32( l_tm_a );
+  std::size_t const l_o_tm_x = l_t32.size(); app32( l_tm_aux );
+  std::size_t const l_o_tm_o = l_t32.size(); app32( l_tm_out );
+  std::size_t const l_o_tn_b = l_t32.size(); app32( l_tn_b );
+  std::size_t const l_o_tn_x = l_t32.size(); app32( l_tn_aux );
+  std::size_t const l_o_tn_o = l_t32.size(); app32( l_tn_out );
+  std::size_t const l_o_tk_a = l_t32.size(); app32( l_tk_a );
+  std::size_t const l_o_tk_b = l_t32.size(); app32( l_tk_b );
+
+  std::size_t const l_bytes64 = l_c64.size() * sizeof( int64_t );
+  std::size_t const l_bytes32 = l_t32.size() * sizeof( int32_t );
+  std::size_t const l_total = l_bytes64 + l_bytes32 + 256;
+  ETIR_HIP_CHECK( hipMalloc( &plan.d_tables, l_total ) );
+  char * l_base = reinterpret_cast< char * >( plan.d_tables );
+  hipError_t l_e1 = hipMemcpy( l_base, l_c64.data(), l_bytes64, hipMemcpyHostToDevice );
+  hipError_t l_e2 = l_bytes32 > 0
+                  ? hipMemcpy( l_base + l_bytes64, l_t32.data(), l_bytes32, hipMemcpyHostToDevice )
+                  : hipSuccess;
+  if( l_e1 != hipSuccess || l_e2 != hipSuccess ) {
+    (void) hipFree( plan.d_tables );
+    plan.d_tables = nullptr;
+    return fail( ETIR_UNDEFINED_ERROR, "contraction: copying offset tables to the device failed" );
+  }
+
+  ContractArgs & a = plan.args;
+  a = ContractArgs();
+  int64_t const * l_p64 = reinterpret_cast< int64_t const * >( l_base );
+  a.tc_a   = l_p64;
+  a.tc_b   = l_p64 + l_size_c;
+  a.tc_aux = l_p64 + 2 * l_size_c;
+  a.tc_out = l_p64 + 3 * l_size_c;
+  int32_t const * l_p32 = reinterpret_cast< int32_t const * >( l_base + l_bytes64 );
+  a.tm_a   = l_p32 + l_o_tm_a;
+  a.tm_aux = l_p32 + l_o_tm_x;
+  a.tm_out = l_p32 + l_o_tm_o;
+  a.tn_b   = l_p32 + l_o_tn_b;
+  a.tn_aux = l_p32 + l_o_tn_x;
+  a.tn_out = l_p32 + l_o_tn_o;
+  a.tk_a   = l_p32 + l_o_tk_a;
+  a.tk_b   = l_p32 + l_o_tk_b;
+  a.M = (int32_t) l_kern_m;
+  a.N = (int32_t) l_kern_n;
+  a.K = (int32_t) l_size_k;
+  a.C = (int32_t) l_size_c;
+  a.tiles_m = (int32_t) ( ( l_kern_m + l_bm - 1 ) / l_bm );
+  a.tiles_n = (int32_t) ( ( l_kern_n + l_bn - 1 ) / l_bn );
+  a.k_affine = l_k_affine ? 1 : 0;
+  a.sk_a = (int32_t) l_sk_a;
+  a.sk_b = (int32_t) l_sk_b;
+  a.first_touch = ktype_first_touch;
+  a.last_touch  = ktype_last_touch;
+  a.out_bf16 = ( dtype_out == ETIR_BF16 ) ? 1 : 0;
+  return ETIR_SUCCESS;
+}
+
+int launch_contraction( ContractionPlan const & plan,
+                        void const            * left,
+                        void const            * right,
+                        void const            * out_aux,
+                        void                  * out,
+                        hipStream_t             stream ) {
+  if( plan.C == 0 || plan.M == 0 || plan.N == 0 ) return ETIR_SUCCESS;
+  if( out == nullptr || ( plan.K > 0 && ( left == nullptr || right == nullptr ) ) ) {
+    return fail( ETIR_NO_DATA_PTR_PROVIDED, "contraction: null tensor pointer" );
+  }
+  if( plan.needs_aux && out_aux == nullptr ) {
+    return fail( ETIR_NO_DATA_PTR_PROVIDED, "contraction: touch kernel needs the auxiliary tensor" );
+  }
+  ContractArgs a = plan.args;
+  a.a   = plan.swapped ? right : left;
+  a.b   = plan.swapped ? left : right;
+  a.aux = plan.needs_aux ? out_aux : nullptr;
+  a.out = out;
+
+  // vector paths need aligned base pointers; otherwise fall back to gathers
+  int32_t l_ma = plan.mode_a;
+  int32_t l_mb = plan.mode_b;
+  int64_t const l_esz = ( plan.dtype_in == ETIR_BF16 ) ? 2 : 4;
+  auto align_of = [&]( int32_t mode ) -> uintptr_t {
+    if( mode == LOAD_VEC_K )  return 16;
+    if( mode == LOAD_VEC_MN ) return uintptr_t( 4 * l_esz );
+    return uintptr_t( l_esz );
+  };
+  if( uintptr_t( a.a ) % align_of( l_ma ) != 0 ) l_ma = LOAD_SCALAR;
+  if( uintptr_t( a.b ) % align_of( l_mb ) != 0 ) l_mb = LOAD_SCALAR;
+
+  int64_t const l_grid = int64_t( a.tiles_m ) * a.tiles_n * a.C;
+  if( l_grid > 0x7fffffffLL ) {
+    return fail( ETIR_UNDEFINED_ERROR, "contraction: grid too large" );
+  }
+  int l_err;
+  if( plan.dtype_in == ETIR_BF16 ) {
+    l_err = launch_contract_bf16( plan.tile, l_ma, l_mb, a, (uint32_t) l_grid, stream );
+  }
+  else {
+    l_err = launch_contract_f32( plan.tile, l_ma, l_mb, a, (uint32_t) l_grid, stream );
+  }
+  if( l_err != ETIR_SUCCESS ) return l_err;
+  hipError_t l_he = hipGetLastError();
+  if( l_he != hipSuccess ) {
+    return fail( ETIR_UNDEFINED_ERROR, std::string( "contraction launch failed: " ) + hipGetErrorString( l_he ) );
+  }
+  return ETIR_SUCCESS;
+}
+
+}  // namespace etir

@@ -1,0 +1,196 @@
+// Internal declarations shared by the planner, the kernels and the C ABI of
+// libeinsum_ir_hip.so.  Host-only structures; the kernels receive the *Args
+// structs by value.
+#ifndef ETIR_INTERNAL_H
+#define ETIR_INTERNAL_H
+
+#include <cstdint>
+#include <string>
+#include <vector>
+#include <hip/hip_runtime.h>
+#include "../../../include/einsum_ir_hip.h"
+
+namespace etir {
+
+// ---------------------------------------------------------------------------
+// error handling
+// ---------------------------------------------------------------------------
+void set_error( std::string const & msg );
+int  fail( int code, std::string const & msg );
+
+#define ETIR_HIP_CHECK( expr )                                                  \
+  do {                                                                          \
+    hipError_t l_e = ( expr );                                                  \
+    if( l_e != hipSuccess ) {                                                   \
+      return ::etir::fail( ETIR_UNDEFINED_ERROR,                                \
+                           std::string( #expr " failed: " ) +                   \
+                           hipGetErrorString( l_e ) );                          \
+    }                                                                           \
+  } while( 0 )
+
+inline int64_t dtype_bytes( int32_t dt ) {
+  if( dt == ETIR_FP32 ) return 4;
+  if( dt == ETIR_FP64 ) return 8;
+  if( dt == ETIR_BF16 ) return 2;
+  return -1;
+}
+
+// ---------------------------------------------------------------------------
+// permutation
+// ---------------------------------------------------------------------------
+constexpr int kPermMaxDims = 12;
+
+enum class PermMode : int32_t {
+  FILL      = 0,  // ZERO: out = 0 over the output's strides
+  TRANSPOSE = 1,  // LDS-tiled 2-D transpose of (in-unit dim, out-unit dim) + batch
+  COPY_VEC  = 2,  // both innermost dims unit-stride: vectorised strided copy
+  GATHER    = 3   // anything else: one thread per output element
+};
+
+struct PermArgs {
+  void const * in;
+  void       * out;
+  int32_t  num_batch;                   // number of batch dims (outer -> inner)
+  int64_t  batch_size[kPermMaxDims];
+  int64_t  batch_s_in[kPermMaxDims];
+  int64_t  batch_s_out[kPermMaxDims];
+  int64_t  size_i;    // TRANSPOSE: unit-stride dim of the input; COPY_VEC: the common inner dim
+  int64_t  size_o;    // TRANSPOSE: unit-stride dim of the output
+  int64_t  s_in_o;    // input stride of the o dim
+  int64_t  s_out_i;   // output stride of the i dim
+  int64_t  tiles_i;
+  int64_t  tiles_o;
+  int64_t  num_batch_total;
+  int64_t  num_elements;
+  int32_t  add;       // ktype ADD: out += in
+  int32_t  vec_ok;    // 16-byte vector accesses are legal (sizes/strides/alignment)
+};
+
+struct PermutePlan {
+  PermMode mode = PermMode::GATHER;
+  int32_t  dtype = ETIR_FP32;
+  int32_t  ktype = ETIR_KTYPE_COPY;
+  int64_t  elem_bytes = 4;
+  int64_t  num_elements = 0;
+  int32_t  num_dims = 0;                 // fused dims (output order)
+  int64_t  size[kPermMaxDims];
+  int64_t  s_in[kPermMaxDims];
+  int64_t  s_out[kPermMaxDims];
+  PermArgs args{};                       // pointers filled at execute time
+};
+
+int  plan_permute( int64_t         num_dims,
+                   int64_t const * sizes,
+                   int64_t const * strides_in,
+                   int64_t const * strides_out,
+                   int32_t         dtype,
+                   int32_t         ktype,
+                   PermutePlan   & plan );
+int  launch_permute( PermutePlan const & plan,
+                     void const        * in,
+                     void              * out,
+                     hipStream_t         stream );
+
+// ---------------------------------------------------------------------------
+// contraction
+// ---------------------------------------------------------------------------
+// Operand load modes of the contraction kernel.  "A" is the operand whose
+// dimension indexes the MFMA rows (kernel-M), "B" the MFMA columns (kernel-N).
+enum LoadMode : int32_t {
+  LOAD_SCALAR = 0,   // element gathers through the offset tables
+  LOAD_VEC_MN = 1,   // 16-byte vectors along the operand's M (or N) index
+  LOAD_VEC_K  = 2    // 16-byte vectors along K
+};
+
+enum TileCfg : int32_t {
+  TILE_F32_128x128 = 0,
+  TILE_F32_64x64   = 1,
+  TILE_BF16_256x256 = 2,
+  TILE_BF16_128x128 = 3,
+  TILE_BF16_64x64  = 4,
+  TILE_F64_64x64   = 5
+};
+
+struct ContractArgs {
+  void const * a;
+  void const * b;
+  void const * aux;
+  void       * out;
+  // C (batch) offsets per tensor, int64, C entries each
+  int64_t const * tc_a;
+  int64_t const * tc_b;
+  int64_t const * tc_aux;
+  int64_t const * tc_out;
+  // kernel-M offsets (A, aux, out), kernel-N offsets (B, aux, out), K offsets (A, B)
+  int32_t const * tm_a;
+  int32_t const * tm_aux;
+  int32_t const * tm_out;
+  int32_t const * tn_b;
+  int32_t const * tn_aux;
+  int32_t const * tn_out;
+  int32_t const * tk_a;
+  int32_t const * tk_b;
+  int32_t M, N, K, C;
+  int32_t tiles_m, tiles_n;
+  // affine K: offset = k * stride (when the K index is one fused dim)
+  int32_t k_affine;
+  int32_t sk_a, sk_b;
+  int32_t first_touch;    // ETIR_KTYPE_{ZERO,COPY,ADD,UNDEFINED}
+  int32_t last_touch;     // ETIR_KTYPE_{RELU,ADD,UNDEFINED}
+  int32_t k_full;         // K % BK == 0: no K masking needed
+  int32_t out_bf16;       // output stored as bf16 (RNE)
+};
+
+struct ContractionPlan {
+  int32_t dtype_in   = ETIR_FP32;
+  int32_t dtype_comp = ETIR_FP32;
+  int32_t dtype_out  = ETIR_FP32;
+  int32_t first_touch = ETIR_KTYPE_UNDEFINED;
+  int32_t last_touch  = ETIR_KTYPE_UNDEFINED;
+  bool    swapped = false;       // kernel A = right tensor, kernel B = left tensor
+  bool    needs_aux = false;
+  int64_t C = 1, M = 1, N = 1, K = 1;
+  int32_t mode_a = LOAD_SCALAR;
+  int32_t mode_b = LOAD_SCALAR;
+  int32_t tile = TILE_F32_128x128;
+  int64_t flops = 0;
+  int64_t bytes = 0;
+  // fused loops per kernel role (outer -> inner) for diagnostics
+  std::string desc;
+  // device blob with all tables
+  void *  d_tables = nullptr;
+  ContractArgs args{};          // table pointers + sizes; tensor pointers set at execute
+};
+
+int  plan_contraction( int64_t            num_loops,
+                       int32_t const    * dim_types,
+                       int64_t const    * sizes,
+                       int64_t const    * strides_left,
+                       int64_t const    * strides_right,
+                       int64_t const    * strides_out_aux,
+                       int64_t const    * strides_out,
+                       int32_t            dtype_left,
+                       int32_t            dtype_right,
+                       int32_t            dtype_comp,
+                       int32_t            dtype_out,
+                       int32_t            ktype_first_touch,
+                       int32_t            ktype_main,
+                       int32_t            ktype_last_touch,
+                       ContractionPlan  & plan );
+int  launch_contraction( ContractionPlan const & plan,
+                         void const            * left,
+                         void const            * right,
+                         void const            * out_aux,
+                         void                  * out,
+                         hipStream_t             stream );
+
+}  // namespace etir
+
+struct etir_plan_s {
+  int32_t kind = 0;              // 1 contraction, 2 permutation
+  int32_t device = 0;
+  etir::ContractionPlan cont;
+  etir::PermutePlan     perm;
+};
+
+#endif
