@@ -1,0 +1,269 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X einsum_ir backend (one GPU).
+
+Prints ONE JSON line.  The headline `value` is the binary-contraction
+throughput of BASELINE config 3 -- the large bf16 batched multi-mode
+contraction  zakm,zbkn->zabmn  (z8 a64 m64 b64 n64 k1024, bf16 inputs, fp32
+accumulate and output) -- in GFLOP/s, with inputs resident in HBM.  A "step"
+is one execution of that contraction (one kernel launch).  The other configs
+(permute abcd->dbca in GB/s, the fp32 contraction of config 1, the 4-layer
+MLP tree of config 4) are reported under "extra".
+
+`roofline` is for the dominant kernel (the config-3 contraction kernel):
+achieved = 2*C*M*N*K FLOP per launch / average launch duration, measured with
+HIP events recorded on the stream the kernel is launched on; peak = MI355X
+dense bf16 MFMA 2516.6 TFLOP/s.  `traffic` (HBM bytes per launch) comes from
+the committed rocprofv3 --pmc summary under profiles/ when present.
+
+`cpu_baseline` times the CPU restatement of the reference algorithm
+(oracle/oracle.c: fused loops, OpenMP tasks, packed fp32 blocked GEMM) on a
+bounded sample of the same workload on the host cores.
+"""
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2516.6
+PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--only", default="", help="comma list of configs to run (c1,c2,c3,c4)")
+    return p.parse_args()
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def time_launches(torch, stream, fn, steps, warmup):
+    """Runs fn() warmup times untimed, then steps times between HIP events on
+    `stream`; returns (total seconds by host clock, average seconds per launch
+    by device events)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    return t1 - t0, start.elapsed_time(end) * 1e-3 / steps
+
+
+def traffic_from_profile(name):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary (FETCH_SIZE /
+    WRITE_SIZE in KiB, scaled by the copy-kernel calibration factor)."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"^hbm_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def bench_c3(torch, eir, stream, steps, warmup):
+    sizes = dict(z=8, a=64, m=64, b=64, n=64, k=1024)
+    loops = eir.binary_loops("zakm,zbkn->zabmn", sizes)
+    g = torch.Generator(device="cuda").manual_seed(3)
+    n_in = 8 * 64 * 1024 * 64
+    left = (torch.rand(n_in, device="cuda", generator=g) * 2 - 1).to(torch.bfloat16)
+    right = (torch.rand(n_in, device="cuda", generator=g) * 2 - 1).to(torch.bfloat16)
+    out = torch.empty(8 * 64 * 64 * 64 * 64, device="cuda", dtype=torch.float32)
+    plan = eir.ContractionPlan(loops["dim_types"], loops["sizes"], loops["strides_left"],
+                               loops["strides_right"], loops["strides_out"],
+                               dtype_left=eir.BF16, dtype_right=eir.BF16, dtype_comp=eir.FP32,
+                               dtype_out=eir.FP32)
+    flops = plan.flops
+    fn = lambda: plan.execute(left, right, out, stream=stream)
+    wall, per_launch = time_launches(torch, stream, fn, steps, warmup)
+    res = dict(flops=flops, wall=wall, per_launch=per_launch, desc=plan.describe(), bytes=plan.bytes)
+    plan.close()
+    del left, right, out
+    return res
+
+
+def bench_c2(torch, eir, stream, steps, warmup):
+    sizes = dict(a=64, b=64, c=64, d=64)
+    u = eir.unary_dims("abcd->dbca", sizes)
+    g = torch.Generator(device="cuda").manual_seed(2)
+    x = torch.rand(64 ** 4, device="cuda", generator=g) * 2 - 1
+    y = torch.empty_like(x)
+    plan = eir.PermutePlan(u["sizes"], u["strides_in"], u["strides_out"], dtype=eir.FP32, ktype=eir.COPY)
+    fn = lambda: plan.execute(x, y, stream=stream)
+    wall, per_launch = time_launches(torch, stream, fn, steps, warmup)
+    res = dict(bytes=plan.bytes, wall=wall, per_launch=per_launch, desc=plan.describe())
+    plan.close()
+    return res
+
+
+def bench_c1(torch, eir, stream, steps, warmup):
+    sizes = dict(a=32, b=16, c=32, d=16, k=32, l=16)
+    loops = eir.binary_loops("abkl,cdkl->abcd", sizes)
+    g = torch.Generator(device="cuda").manual_seed(1)
+    left = torch.rand(512 * 512, device="cuda", generator=g) * 2 - 1
+    right = torch.rand(512 * 512, device="cuda", generator=g) * 2 - 1
+    out = torch.empty(512 * 512, device="cuda")
+    plan = eir.ContractionPlan(loops["dim_types"], loops["sizes"], loops["strides_left"],
+                               loops["strides_right"], loops["strides_out"])
+    fn = lambda: plan.execute(left, right, out, stream=stream)
+    wall, per_launch = time_launches(torch, stream, fn, steps, warmup)
+    res = dict(flops=plan.flops, wall=wall, per_launch=per_launch, desc=plan.describe())
+    plan.close()
+    return res
+
+
+def bench_c4(torch, eir, stream, steps, warmup):
+    """4-layer MLP tree bi,ih,hj,jk,ko->bo along the left-to-right path; every
+    node is one contraction with its output kept in HBM (the tree's node order
+    after the reference's swap_inputs: left = weight, right = activation)."""
+    b, w = 4096, 2048
+    g = torch.Generator(device="cuda").manual_seed(4)
+    x = torch.randn(b * w, device="cuda", generator=g)
+    ws = [torch.randn(w * w, device="cuda", generator=g) / (w ** 0.5) for _ in range(4)]
+    acts = [torch.empty(b * w, device="cuda") for _ in range(4)]
+    names = ["i", "h", "j", "k", "o"]
+    plans = []
+    for layer in range(4):
+        p_in, p_out = names[layer], names[layer + 1]
+        expr = f"{p_in}{p_out},b{p_in}->b{p_out}"
+        loops = eir.binary_loops(expr, {"b": b, p_in: w, p_out: w})
+        plans.append(eir.ContractionPlan(loops["dim_types"], loops["sizes"], loops["strides_left"],
+                                         loops["strides_right"], loops["strides_out"]))
+    flops = sum(p.flops for p in plans)
+
+    def fn():
+        cur = x
+        for layer in range(4):
+            plans[layer].execute(ws[layer], cur, acts[layer], stream=stream)
+            cur = acts[layer]
+    wall, per_step = time_launches(torch, stream, fn, steps, warmup)
+    res = dict(flops=flops, wall=wall, per_launch=per_step, desc=plans[0].describe())
+    for p in plans:
+        p.close()
+    return res
+
+
+def cpu_baseline_c3():
+    """CPU restatement of the reference algorithm on a bounded sample of config 3:
+    one batch (z=1), a=16 of 64 (M = 16*64 = 1024), all of N = 4096 and K = 1024."""
+    import numpy as np
+    from oracle import py_oracle as orc
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    sizes = dict(z=1, a=16, m=64, b=64, n=64, k=1024)
+    import einsum_ir_amd as eir
+    loops = eir.binary_loops("zakm,zbkn->zabmn", sizes)
+    rng = np.random.default_rng(3)
+    a = orc.bf16_to_f32(orc.f32_to_bf16(rng.uniform(-1, 1, 16 * 1024 * 64).astype(np.float32)))
+    b = orc.bf16_to_f32(orc.f32_to_bf16(rng.uniform(-1, 1, 64 * 1024 * 64).astype(np.float32)))
+    out = np.empty(16 * 64 * 64 * 64, dtype=np.float32)
+    flops = 2 * 1024 * 4096 * 1024
+    orc.contract_blocked(loops, a, b, out, num_threads=threads)   # warm-up
+    reps, t = 0, 0.0
+    while t < 10.0 and reps < 50:
+        t0 = time.perf_counter()
+        orc.contract_blocked(loops, a, b, out, num_threads=threads)
+        t += time.perf_counter() - t0
+        reps += 1
+    return dict(value=round(flops * reps / t * 1e-9, 2), unit="GFLOP/s", cores=threads, kind="port",
+                sample=f"config-3 slice z=1,a=16 (M=1024,N=4096,K=1024; {flops/1e9:.2f} GFLOP) x{reps}, "
+                       "fp32 math on the bf16-rounded inputs (the reference has no bf16 path); "
+                       "oracle/oracle.c oracle_contract_blocked, OpenMP")
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no "
+              "multi-GPU path. Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import einsum_ir_amd as eir
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    stream = torch.cuda.current_stream()
+    only = set(x for x in args.only.split(",") if x)
+    run = lambda name: (not only) or (name in only)
+
+    extra = {}
+    c3 = None
+    if run("c3"):
+        c3 = bench_c3(torch, eir, stream, args.steps, args.warmup)
+        log(f"c3: {c3['desc']}  {c3['per_launch']*1e6:.1f} us/launch")
+    if run("c2"):
+        c2 = bench_c2(torch, eir, stream, max(args.steps, 20), args.warmup)
+        gbs = c2["bytes"] / c2["per_launch"] * 1e-9
+        extra["c2_permute_abcd_dbca_64^4_fp32"] = dict(
+            value=round(gbs, 1), unit="GB/s", us_per_launch=round(c2["per_launch"] * 1e6, 2),
+            frac_hbm_peak=round(gbs / PEAK_HBM_GBS, 4), bytes_per_launch=c2["bytes"], kernel=c2["desc"])
+        log(f"c2: {c2['desc']}  {c2['per_launch']*1e6:.2f} us/launch  {gbs:.0f} GB/s")
+    if run("c1"):
+        c1 = bench_c1(torch, eir, stream, max(args.steps, 20), args.warmup)
+        gf = c1["flops"] / c1["per_launch"] * 1e-9
+        extra["c1_abkl_cdkl_fp32"] = dict(value=round(gf, 1), unit="GFLOP/s",
+                                          us_per_launch=round(c1["per_launch"] * 1e6, 2),
+                                          frac_fp32_peak=round(gf / (PEAK_FP32_TFLOPS * 1e3), 4),
+                                          kernel=c1["desc"])
+        log(f"c1: {c1['desc']}  {c1['per_launch']*1e6:.2f} us/launch")
+    if run("c4"):
+        c4 = bench_c4(torch, eir, stream, max(5, args.steps // 5), min(args.warmup, 2))
+        gf = c4["flops"] / c4["per_launch"] * 1e-9
+        extra["c4_mlp_tree_fp32"] = dict(value=round(gf, 1), unit="GFLOP/s",
+                                         ms_per_eval=round(c4["per_launch"] * 1e3, 3),
+                                         frac_fp32_peak=round(gf / (PEAK_FP32_TFLOPS * 1e3), 4),
+                                         kernel=c4["desc"])
+        log(f"c4: {c4['per_launch']*1e3:.3f} ms/eval")
+
+    cpu = None
+    if not args.no_cpu_baseline and run("c3"):
+        cpu = cpu_baseline_c3()
+        log(f"cpu baseline: {cpu}")
+
+    if c3 is None:
+        print(json.dumps({"extra": extra}))
+        return
+    value = c3["flops"] * args.steps / c3["wall"] * 1e-9
+    achieved = c3["flops"] / c3["per_launch"] * 1e-12
+    line = {
+        "metric": "binary-contraction GFLOP/s & % MFMA peak; permute GB/s & % HBM peak (1 GPU)",
+        "value": round(value, 1),
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c3["wall"] / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (uniform[-1,1], seeded torch generator, device-resident)",
+        "config": {"workload": "zakm,zbkn->zabmn z=8 a=64 m=64 b=64 n=64 k=1024, bf16 in, fp32 acc+out "
+                               "(BASELINE config 3)",
+                   "C": 8, "M": 4096, "N": 4096, "K": 1024, "flops_per_step": c3["flops"],
+                   "kernel": c3["desc"]},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic_from_profile("contract_bf16_c3_pmc.txt")},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

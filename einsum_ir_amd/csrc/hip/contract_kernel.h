@@ -62,6 +62,17 @@ template< int DT > struct InType;
 template<> struct InType< ETIR_FP32 > { typedef float    T; };
 template<> struct InType< ETIR_BF16 > { typedef uint16_t T; };
 
+// Pitch (elements) of the [k][row] LDS layout.  bf16: 2*PK = 64 (mod 256) so
+// the four k rows of one transpose read land in disjoint bank ranges; fp32:
+// 4*PK = 32 (mod 64) so rows k and k+4 (the two lane groups) do not collide.
+template< int R, int ESZ >
+struct KmPitch {
+  static constexpr int bytes_raw = R * ESZ;
+  static constexpr int pad = ( ESZ == 2 ) ? ( ( 64 - bytes_raw % 256 + 256 ) % 256 )
+                                          : ( ( 32 - bytes_raw % 64 + 64 ) % 64 );
+  static constexpr int value = ( bytes_raw + pad ) / ESZ;
+};
+
 // ---------------------------------------------------------------------------
 // Operand loader: global -> registers -> LDS ([row][k], pitch LDK elements)
 // ---------------------------------------------------------------------------
@@ -93,13 +104,14 @@ struct Loader< R, BK, T, ESZ, LOAD_VEC_K > {
     }
   }
 
-  template< typename TE >
+  template< bool KAFF, typename TE >
   __device__ inline void load( TE const * base, int32_t k0, int32_t K,
-                               int32_t const * tab_k, int32_t k_affine, int32_t sk ) {
+                               int32_t const * tab_k, int32_t sk ) {
     int32_t const l_k = k0 + m_kv;
     bool const l_kok = l_k < K;
     int32_t l_koff = 0;
-    if( l_kok ) l_koff = k_affine ? l_k * sk : tab_k[l_k];
+    if( KAFF ) l_koff = l_k * sk;
+    else if( l_kok ) l_koff = tab_k[l_k];
 #pragma unroll
     for( int l_i = 0; l_i < NV; l_i++ ) {
       if( l_kok && m_row_off[l_i] >= 0 ) {
@@ -150,9 +162,10 @@ struct Loader< R, BK, T, ESZ, LOAD_SCALAR > {
     }
   }
 
-  template< typename TE >
+  template< bool KAFF, typename TE >
   __device__ inline void load( TE const * base, int32_t k0, int32_t K,
-                               int32_t const * tab_k, int32_t k_affine, int32_t sk ) {
+                               int32_t const * tab_k, int32_t sk ) {
+    // all table reads first, then all data reads: one wait for the tables
     int32_t l_koff[V];
     bool    l_kok[V];
 #pragma unroll
@@ -160,7 +173,8 @@ struct Loader< R, BK, T, ESZ, LOAD_SCALAR > {
       int32_t const l_k = k0 + m_kv + l_e;
       l_kok[l_e] = l_k < K;
       l_koff[l_e] = 0;
-      if( l_kok[l_e] ) l_koff[l_e] = k_affine ? l_k * sk : tab_k[l_k];
+      if( KAFF ) l_koff[l_e] = l_k * sk;
+      else if( l_kok[l_e] ) l_koff[l_e] = tab_k[l_k];
     }
 #pragma unroll
     for( int l_i = 0; l_i < NV; l_i++ ) {
@@ -188,54 +202,53 @@ struct Loader< R, BK, T, ESZ, LOAD_SCALAR > {
   }
 };
 
-// vectors of VR=4 consecutive rows (unit stride along M/N); each thread loads a
-// VK x 4 micro-block (VK consecutive k) and transposes it in registers into
-// 4 K-contiguous 16-byte LDS rows.
+// 16-byte vectors of consecutive rows (unit stride along M or N) at one k,
+// stored as loaded: LDS layout [k][row] with pitch PK elements.  The MFMA
+// fragments (consecutive k for one row) are read back with the gfx950 LDS
+// transpose read (bf16) or one 4-byte read per MFMA step (fp32), so no
+// register transpose is needed and both the LDS writes (32 lanes cover one
+// 512-byte row) and the reads are free of bank conflicts.
 template< int R, int BK, int T, int ESZ >
 struct Loader< R, BK, T, ESZ, LOAD_VEC_MN > {
-  static constexpr int VR     = 4;                  // rows per global vector
-  static constexpr int VK     = 16 / ESZ;           // k per LDS vector
-  static constexpr int RG     = R / VR;             // row groups
-  static constexpr int COUNT  = RG * ( BK / VK );
-  static constexpr int NB     = ( COUNT + T - 1 ) / T;
-  static constexpr int LDK    = BK + 16 / ESZ;
-  // fp32: 16-byte row vectors, bf16: 8-byte row vectors
-  typedef typename std::conditional< ESZ == 4, u32x4, u32x2 >::type RowVec;
+  static constexpr int V      = 16 / ESZ;           // rows per vector
+  static constexpr int VPK    = R / V;              // vectors per k row
+  static constexpr int COUNT  = BK * VPK;
+  static constexpr int NV     = COUNT / T;
+  static constexpr int PK     = KmPitch< R, ESZ >::value;
+  static_assert( COUNT % T == 0 && T % VPK == 0, "VEC_MN loader: tile/threads mismatch" );
 
-  RowVec  m_reg[NB][VK];
-  int32_t m_row_off[NB];
-  int     m_rg[NB];
-  int     m_kg[NB];
+  u32x4   m_reg[NV];
+  int32_t m_row_off;
+  int     m_mv;
+  int     m_k;
 
   __device__ inline void init( int32_t const * tab_rows, int32_t rows, int32_t row0 ) {
     int const l_t = threadIdx.x;
-#pragma unroll
-    for( int l_i = 0; l_i < NB; l_i++ ) {
-      int const l_idx = l_t + l_i * T;
-      m_rg[l_i] = l_idx % RG;
-      m_kg[l_i] = l_idx / RG;
-      int const l_g = row0 + m_rg[l_i] * VR;
-      m_row_off[l_i] = ( l_idx < COUNT && l_g < rows ) ? tab_rows[l_g] : -1;
-    }
+    m_mv = l_t % VPK;
+    m_k  = l_t / VPK;
+    int const l_g = row0 + m_mv * V;
+    m_row_off = ( l_g < rows ) ? tab_rows[l_g] : -1;
   }
 
-  template< typename TE >
+  template< bool KAFF, typename TE >
   __device__ inline void load( TE const * base, int32_t k0, int32_t K,
-                               int32_t const * tab_k, int32_t k_affine, int32_t sk ) {
+                               int32_t const * tab_k, int32_t sk ) {
+    int32_t l_koff[NV];
 #pragma unroll
-    for( int l_i = 0; l_i < NB; l_i++ ) {
-      int32_t const l_kb = k0 + m_kg[l_i] * VK;
+    for( int l_i = 0; l_i < NV; l_i++ ) {
+      int32_t const l_k = k0 + m_k + l_i * ( T / VPK );
+      l_koff[l_i] = 0;
+      if( KAFF ) l_koff[l_i] = l_k * sk;
+      else if( l_k < K ) l_koff[l_i] = tab_k[l_k];
+    }
 #pragma unroll
-      for( int l_j = 0; l_j < VK; l_j++ ) {
-        int32_t const l_k = l_kb + l_j;
-        bool const l_ok = ( l_k < K ) && m_row_off[l_i] >= 0;
-        if( l_ok ) {
-          int32_t const l_koff = k_affine ? l_k * sk : tab_k[l_k];
-          m_reg[l_i][l_j] = *reinterpret_cast< RowVec const * >( base + m_row_off[l_i] + l_koff );
-        }
-        else {
-          m_reg[l_i][l_j] = RowVec( 0u );
-        }
+    for( int l_i = 0; l_i < NV; l_i++ ) {
+      int32_t const l_k = k0 + m_k + l_i * ( T / VPK );
+      if( l_k < K && m_row_off >= 0 ) {
+        m_reg[l_i] = *reinterpret_cast< u32x4 const * >( base + m_row_off + l_koff[l_i] );
+      }
+      else {
+        m_reg[l_i] = u32x4{ 0u, 0u, 0u, 0u };
       }
     }
   }
@@ -243,61 +256,117 @@ struct Loader< R, BK, T, ESZ, LOAD_VEC_MN > {
   template< typename TE >
   __device__ inline void store( TE * lds ) {
 #pragma unroll
-    for( int l_i = 0; l_i < NB; l_i++ ) {
-      if( COUNT % T == 0 || ( int( threadIdx.x ) + l_i * T ) < COUNT ) {
-        TE * l_dst = lds + ( m_rg[l_i] * VR ) * LDK + m_kg[l_i] * VK;
-        if constexpr( ESZ == 4 ) {
-          // 4x4 fp32 transpose: register renaming only
-#pragma unroll
-          for( int l_r = 0; l_r < 4; l_r++ ) {
-            u32x4 l_w = u32x4{ m_reg[l_i][0][l_r], m_reg[l_i][1][l_r],
-                               m_reg[l_i][2][l_r], m_reg[l_i][3][l_r] };
-            *reinterpret_cast< u32x4 * >( l_dst + l_r * LDK ) = l_w;
-          }
-        }
-        else {
-          // 8(k) x 4(row) bf16 block: m_reg[k] = {row0|row1<<16, row2|row3<<16}
-#pragma unroll
-          for( int l_r = 0; l_r < 4; l_r++ ) {
-            u32x4 l_w;
-#pragma unroll
-            for( int l_p = 0; l_p < 4; l_p++ ) {
-              uint32_t const l_lo = m_reg[l_i][2 * l_p    ][l_r >> 1];
-              uint32_t const l_hi = m_reg[l_i][2 * l_p + 1][l_r >> 1];
-              l_w[l_p] = ( l_r & 1 ) ? ( ( l_lo >> 16 ) | ( l_hi & 0xffff0000u ) )
-                                     : ( ( l_lo & 0xffffu ) | ( l_hi << 16 ) );
-            }
-            *reinterpret_cast< u32x4 * >( l_dst + l_r * LDK ) = l_w;
-          }
-        }
-      }
+    for( int l_i = 0; l_i < NV; l_i++ ) {
+      int const l_k = m_k + l_i * ( T / VPK );
+      *reinterpret_cast< u32x4 * >( lds + l_k * PK + m_mv * V ) = m_reg[l_i];
     }
   }
 };
 
 // ---------------------------------------------------------------------------
+// MFMA fragment reads from LDS
+//   fp32, v_mfma_f32_32x32x2_f32: step s (0..BK/2-1), lane group g = lane/32
+//         feeds k = 8*(s/4) + 4*g + s%4
+//   bf16, v_mfma_f32_32x32x16_bf16: step s (0..BK/16-1), lane group g feeds
+//         k = 16*s + 8*g + (0..7)
+// Both operands use the same assignment, so the sum over k is unchanged.
+// ---------------------------------------------------------------------------
+template< int ESZ, int MODE, int R, int BK >
+struct Frag;
+
+// [row][k] layout (LOAD_SCALAR, LOAD_VEC_K), fp32: one 16-byte read = 4 steps
+template< int MODE, int R, int BK >
+struct Frag< 4, MODE, R, BK > {
+  static constexpr int LDK = BK + 4;
+  __device__ static inline f32x4 read4( float const * lds, int row, int s4, int lane ) {
+    return *reinterpret_cast< f32x4 const * >( lds + row * LDK + 8 * s4 + 4 * ( lane >> 5 ) );
+  }
+};
+
+// [k][row] layout (LOAD_VEC_MN), fp32: one 4-byte read per step
+template< int R, int BK >
+struct Frag< 4, LOAD_VEC_MN, R, BK > {
+  static constexpr int PK = KmPitch< R, 4 >::value;
+  __device__ static inline f32x4 read4( float const * lds, int row, int s4, int lane ) {
+    float const * l_p = lds + ( 8 * s4 + 4 * ( lane >> 5 ) ) * PK + row;
+    return f32x4{ l_p[0], l_p[PK], l_p[2 * PK], l_p[3 * PK] };
+  }
+};
+
+// [row][k] layout, bf16: one 16-byte read per step
+template< int MODE, int R, int BK >
+struct Frag< 2, MODE, R, BK > {
+  static constexpr int LDK = BK + 8;
+  __device__ static inline bf16x8 read8( uint16_t const * lds, int row, int s, int lane ) {
+    return *reinterpret_cast< bf16x8 const * >( lds + row * LDK + 16 * s + 8 * ( lane >> 5 ) );
+  }
+};
+
+// [k][row] layout, bf16: two transpose reads per step.  Within each group of
+// 16 lanes, ds_read_b64_tr_b16 hands lane i element i%4 of the 8-byte chunks
+// read by lanes 4j + i/4 (j = 0..3); lane L of the group therefore addresses
+// row k = kb + L/4, columns 4*(L%4)..+3 of its 16-row slice, and receives the
+// 4 consecutive k of row L.
+template< int R, int BK >
+struct Frag< 2, LOAD_VEC_MN, R, BK > {
+  static constexpr int PK = KmPitch< R, 2 >::value;
+  typedef short v4i16 __attribute__( ( ext_vector_type( 4 ) ) );
+  typedef __attribute__( ( address_space( 3 ) ) ) v4i16 lds_v4i16;
+  __device__ static inline bf16x8 read8( uint16_t const * lds, int row_base, int s, int lane ) {
+    int const l_q   = lane >> 4;           // 16-lane group
+    int const l_L   = lane & 15;
+    int const l_row = row_base + 16 * ( l_q & 1 ) + 4 * ( l_L & 3 );
+    int const l_kb  = 16 * s + 8 * ( l_q >> 1 ) + ( l_L >> 2 );
+    uint16_t const * l_p0 = lds + l_kb * PK + l_row;
+    uint16_t const * l_p1 = l_p0 + 4 * PK;
+    v4i16 l_lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16( (lds_v4i16 *) ( l_p0 ) );
+    v4i16 l_hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16( (lds_v4i16 *) ( l_p1 ) );
+    typedef short v8i16 __attribute__( ( ext_vector_type( 8 ) ) );
+    v8i16 l_all = __builtin_shufflevector( l_lo, l_hi, 0, 1, 2, 3, 4, 5, 6, 7 );
+    return __builtin_bit_cast( bf16x8, l_all );
+  }
+};
+
+template< int ESZ, int MODE, int R, int BK >
+struct LdsSize {
+  static constexpr int value = ( MODE == LOAD_VEC_MN ) ? BK * KmPitch< R, ESZ >::value
+                                                       : R * ( BK + 16 / ESZ );
+};
+
+// ---------------------------------------------------------------------------
 // the kernel
 // ---------------------------------------------------------------------------
-template< int DT, int BM, int BN, int BK, int WM, int WN, int MA, int MB >
+template< int DT, int BM, int BN, int BK, int WM, int WN, int MA, int MB, bool KAFF >
 __global__ __launch_bounds__( 64 * WM * WN )
 void contract_kernel( ContractArgs a ) {
   typedef typename InType< DT >::T TE;
   constexpr int T    = 64 * WM * WN;
   constexpr int ESZ  = sizeof( TE );
-  constexpr int LDK  = BK + 16 / ESZ;
   constexpr int TM   = BM / WM / 32;
   constexpr int TN   = BN / WN / 32;
+  constexpr int SZA  = LdsSize< ESZ, MA, BM, BK >::value;
+  constexpr int SZB  = LdsSize< ESZ, MB, BN, BK >::value;
   static_assert( TM >= 1 && TN >= 1, "wave tile must hold at least one 32x32 block" );
 
-  __shared__ __attribute__( ( aligned( 16 ) ) ) TE l_lds_a[2][BM * LDK];
-  __shared__ __attribute__( ( aligned( 16 ) ) ) TE l_lds_b[2][BN * LDK];
+  __shared__ __attribute__( ( aligned( 16 ) ) ) TE l_lds_a[2][SZA];
+  __shared__ __attribute__( ( aligned( 16 ) ) ) TE l_lds_b[2][SZB];
 
+  // XCD-aware order: consecutive workgroup ids are dispatched round-robin over
+  // the 8 XCDs; remap so that each XCD works on one contiguous range of tiles
+  // (sharing its L2), then walk tiles in groups of kGroupM tile rows.
   int32_t const l_ntiles = a.tiles_m * a.tiles_n;
-  int32_t const l_bid    = blockIdx.x;
+  int32_t const l_nblk   = gridDim.x;
+  int32_t l_bid = blockIdx.x;
+  if( ( l_nblk & 7 ) == 0 ) l_bid = ( l_bid & 7 ) * ( l_nblk >> 3 ) + ( l_bid >> 3 );
   int32_t const l_c      = l_bid / l_ntiles;
   int32_t const l_tile   = l_bid - l_c * l_ntiles;
-  int32_t const l_tm     = l_tile / a.tiles_n;
-  int32_t const l_tn     = l_tile - l_tm * a.tiles_n;
+  constexpr int32_t kGroupM = 8;
+  int32_t const l_in_grp = kGroupM * a.tiles_n;
+  int32_t const l_grp    = l_tile / l_in_grp;
+  int32_t const l_fm     = l_grp * kGroupM;
+  int32_t const l_gsz    = min( a.tiles_m - l_fm, kGroupM );
+  int32_t const l_tm     = l_fm + ( l_tile - l_grp * l_in_grp ) % l_gsz;
+  int32_t const l_tn     = ( l_tile - l_grp * l_in_grp ) / l_gsz;
   int32_t const l_m0     = l_tm * BM;
   int32_t const l_n0     = l_tn * BN;
 
@@ -314,7 +383,6 @@ void contract_kernel( ContractArgs a ) {
   int const l_wm   = l_wave / WN;
   int const l_wn   = l_wave - l_wm * WN;
   int const l_lr   = l_lane & 31;    // row (A) / column (B) inside a 32x32 block
-  int const l_lg   = l_lane >> 5;    // lane group: which k slice this lane feeds
 
   f32x16 l_acc[TM][TN];
 #pragma unroll
@@ -326,8 +394,8 @@ void contract_kernel( ContractArgs a ) {
   int32_t const l_nk = ( a.K + BK - 1 ) / BK;
 
   if( l_nk > 0 ) {
-    l_ld_a.load( l_a, 0, a.K, a.tk_a, a.k_affine, a.sk_a );
-    l_ld_b.load( l_b, 0, a.K, a.tk_b, a.k_affine, a.sk_b );
+    l_ld_a.template load< KAFF >( l_a, 0, a.K, a.tk_a, a.sk_a );
+    l_ld_b.template load< KAFF >( l_b, 0, a.K, a.tk_b, a.sk_b );
     l_ld_a.store( l_lds_a[0] );
     l_ld_b.store( l_lds_b[0] );
     __syncthreads();
@@ -336,25 +404,29 @@ void contract_kernel( ContractArgs a ) {
       int const l_cur = l_kt & 1;
       bool const l_more = ( l_kt + 1 ) < l_nk;
       if( l_more ) {
-        l_ld_a.load( l_a, ( l_kt + 1 ) * BK, a.K, a.tk_a, a.k_affine, a.sk_a );
-        l_ld_b.load( l_b, ( l_kt + 1 ) * BK, a.K, a.tk_b, a.k_affine, a.sk_b );
+        l_ld_a.template load< KAFF >( l_a, ( l_kt + 1 ) * BK, a.K, a.tk_a, a.sk_a );
+        l_ld_b.template load< KAFF >( l_b, ( l_kt + 1 ) * BK, a.K, a.tk_b, a.sk_b );
       }
 
-      TE const * l_sa = l_lds_a[l_cur] + ( l_wm * TM * 32 + l_lr ) * LDK;
-      TE const * l_sb = l_lds_b[l_cur] + ( l_wn * TN * 32 + l_lr ) * LDK;
+      TE const * l_sa = l_lds_a[l_cur];
+      TE const * l_sb = l_lds_b[l_cur];
+      // rows of this wave's blocks; VEC_MN readers take the block base row
+      int const l_ra = l_wm * TM * 32 + ( MA == LOAD_VEC_MN ? 0 : l_lr );
+      int const l_rb = l_wn * TN * 32 + ( MB == LOAD_VEC_MN ? 0 : l_lr );
 
       if constexpr( DT == ETIR_FP32 ) {
-        // v_mfma_f32_32x32x2_f32: lane group g feeds k = g*BK/2 + s for step s
 #pragma unroll
         for( int l_s4 = 0; l_s4 < BK / 8; l_s4++ ) {
           f32x4 l_fa[TM];
           f32x4 l_fb[TN];
 #pragma unroll
           for( int l_i = 0; l_i < TM; l_i++ )
-            l_fa[l_i] = *reinterpret_cast< f32x4 const * >( l_sa + l_i * 32 * LDK + l_lg * ( BK / 2 ) + 4 * l_s4 );
+            l_fa[l_i] = Frag< 4, MA, BM, BK >::read4( l_sa, l_ra + l_i * 32 + ( MA == LOAD_VEC_MN ? l_lr : 0 ),
+                                                      l_s4, l_lane );
 #pragma unroll
           for( int l_j = 0; l_j < TN; l_j++ )
-            l_fb[l_j] = *reinterpret_cast< f32x4 const * >( l_sb + l_j * 32 * LDK + l_lg * ( BK / 2 ) + 4 * l_s4 );
+            l_fb[l_j] = Frag< 4, MB, BN, BK >::read4( l_sb, l_rb + l_j * 32 + ( MB == LOAD_VEC_MN ? l_lr : 0 ),
+                                                      l_s4, l_lane );
 #pragma unroll
           for( int l_e = 0; l_e < 4; l_e++ )
 #pragma unroll
@@ -366,17 +438,16 @@ void contract_kernel( ContractArgs a ) {
         }
       }
       else {
-        // v_mfma_f32_32x32x16_bf16: lane group g feeds k = 16*s + 8*g + (0..7)
 #pragma unroll
         for( int l_s = 0; l_s < BK / 16; l_s++ ) {
           bf16x8 l_fa[TM];
           bf16x8 l_fb[TN];
 #pragma unroll
           for( int l_i = 0; l_i < TM; l_i++ )
-            l_fa[l_i] = *reinterpret_cast< bf16x8 const * >( l_sa + l_i * 32 * LDK + 16 * l_s + 8 * l_lg );
+            l_fa[l_i] = Frag< 2, MA, BM, BK >::read8( l_sa, l_ra + l_i * 32, l_s, l_lane );
 #pragma unroll
           for( int l_j = 0; l_j < TN; l_j++ )
-            l_fb[l_j] = *reinterpret_cast< bf16x8 const * >( l_sb + l_j * 32 * LDK + 16 * l_s + 8 * l_lg );
+            l_fb[l_j] = Frag< 2, MB, BN, BK >::read8( l_sb, l_rb + l_j * 32, l_s, l_lane );
 #pragma unroll
           for( int l_i = 0; l_i < TM; l_i++ )
 #pragma unroll
@@ -395,34 +466,62 @@ void contract_kernel( ContractArgs a ) {
   }
 
   // ---------------------------------------------------------------- epilogue
+  // The tile's output (and aux) row/column offsets are staged in LDS first:
+  // table reads from global memory between the stores would make every store
+  // wait for all earlier ones (one vector-memory counter on gfx9).
   // 32x32 accumulator layout: register r of lane l holds
   //   row = 8*(r/4) + 4*(l/32) + r%4,  column = l%32
+  static_assert( ( 2 * ( BM + BN ) ) * 4 <= ( SZA + SZB ) * ESZ * 2, "LDS too small for the epilogue tables" );
+  int32_t * l_s_m_out = reinterpret_cast< int32_t * >( &l_lds_a[0][0] );
+  int32_t * l_s_m_aux = l_s_m_out + BM;
+  int32_t * l_s_n_out = l_s_m_aux + BM;
+  int32_t * l_s_n_aux = l_s_n_out + BN;
+  bool const l_has_aux = ( a.aux != nullptr );
+  for( int l_x = threadIdx.x; l_x < BM; l_x += T ) {
+    int32_t const l_m = l_m0 + l_x;
+    l_s_m_out[l_x] = ( l_m < a.M ) ? a.tm_out[l_m] : 0;
+    l_s_m_aux[l_x] = ( l_has_aux && l_m < a.M ) ? a.tm_aux[l_m] : 0;
+  }
+  for( int l_x = threadIdx.x; l_x < BN; l_x += T ) {
+    int32_t const l_n = l_n0 + l_x;
+    l_s_n_out[l_x] = ( l_n < a.N ) ? a.tn_out[l_n] : 0;
+    l_s_n_aux[l_x] = ( l_has_aux && l_n < a.N ) ? a.tn_aux[l_n] : 0;
+  }
+  __syncthreads();
+
+  int const l_lg = l_lane >> 5;
   int64_t const l_coff_out = a.tc_out[l_c];
-  int64_t const l_coff_aux = ( a.aux != nullptr ) ? a.tc_aux[l_c] : 0;
-  float const * l_aux_f = reinterpret_cast< float const * >( a.aux );
-  uint16_t const * l_aux_h = reinterpret_cast< uint16_t const * >( a.aux );
-  float * l_out_f = reinterpret_cast< float * >( a.out );
-  uint16_t * l_out_h = reinterpret_cast< uint16_t * >( a.out );
+  int64_t const l_coff_aux = l_has_aux ? a.tc_aux[l_c] : 0;
+  float const * l_aux_f = reinterpret_cast< float const * >( a.aux ) + l_coff_aux;
+  uint16_t const * l_aux_h = reinterpret_cast< uint16_t const * >( a.aux ) + l_coff_aux;
+  float * l_out_f = reinterpret_cast< float * >( a.out ) + l_coff_out;
+  uint16_t * l_out_h = reinterpret_cast< uint16_t * >( a.out ) + l_coff_out;
   bool const l_read_out = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_UNDEFINED );
   bool const l_aux_first = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_COPY );
+  bool const l_need_aux = l_has_aux && ( l_aux_first || a.last_touch == ETIR_KTYPE_ADD );
+  bool const l_plain = !l_read_out && !l_need_aux && a.last_touch == ETIR_KTYPE_UNDEFINED && !a.out_bf16;
 
 #pragma unroll
   for( int l_j = 0; l_j < TN; l_j++ ) {
-    int32_t const l_n = l_n0 + ( l_wn * TN + l_j ) * 32 + l_lr;
-    if( l_n >= a.N ) continue;
-    int64_t const l_noff_out = l_coff_out + a.tn_out[l_n];
-    int64_t const l_noff_aux = ( a.aux != nullptr ) ? l_coff_aux + a.tn_aux[l_n] : 0;
+    int32_t const l_nl = ( l_wn * TN + l_j ) * 32 + l_lr;
+    bool const l_nok = ( l_n0 + l_nl ) < a.N;
+    int32_t const l_noff_out = l_s_n_out[l_nl];
+    int32_t const l_noff_aux = l_s_n_aux[l_nl];
 #pragma unroll
     for( int l_i = 0; l_i < TM; l_i++ ) {
 #pragma unroll
       for( int l_r = 0; l_r < 16; l_r++ ) {
-        int32_t const l_m = l_m0 + ( l_wm * TM + l_i ) * 32 + 8 * ( l_r >> 2 ) + 4 * l_lg + ( l_r & 3 );
-        if( l_m >= a.M ) continue;
-        int64_t const l_off = l_noff_out + a.tm_out[l_m];
+        int32_t const l_ml = ( l_wm * TM + l_i ) * 32 + 8 * ( l_r >> 2 ) + 4 * l_lg + ( l_r & 3 );
+        if( !l_nok || ( l_m0 + l_ml ) >= a.M ) continue;
+        int64_t const l_off = int64_t( l_noff_out ) + l_s_m_out[l_ml];
         float l_v = l_acc[l_i][l_j][l_r];
+        if( l_plain ) {
+          l_out_f[l_off] = l_v;
+          continue;
+        }
         float l_aux = 0.0f;
-        if( a.aux != nullptr && ( l_aux_first || a.last_touch == ETIR_KTYPE_ADD ) ) {
-          int64_t const l_aoff = l_noff_aux + a.tm_aux[l_m];
+        if( l_need_aux ) {
+          int64_t const l_aoff = int64_t( l_noff_aux ) + l_s_m_aux[l_ml];
           l_aux = a.out_bf16 ? bf16_to_f32( l_aux_h[l_aoff] ) : l_aux_f[l_aoff];
         }
         if( l_read_out ) {

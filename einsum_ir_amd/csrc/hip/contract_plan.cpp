@@ -31,10 +31,16 @@
 
 namespace etir {
 
-int launch_contract_f32( int32_t tile, int32_t ma, int32_t mb, ContractArgs const & a,
-                         uint32_t grid, hipStream_t stream );
-int launch_contract_bf16( int32_t tile, int32_t ma, int32_t mb, ContractArgs const & a,
-                          uint32_t grid, hipStream_t stream );
+int launch_contract_f32_128x128( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
+                                 uint32_t grid, hipStream_t stream );
+int launch_contract_f32_64x64( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
+                               uint32_t grid, hipStream_t stream );
+int launch_contract_bf16_256x256( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
+                                  uint32_t grid, hipStream_t stream );
+int launch_contract_bf16_128x128( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
+                                  uint32_t grid, hipStream_t stream );
+int launch_contract_bf16_64x64( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
+                                uint32_t grid, hipStream_t stream );
 
 namespace {
 
@@ -257,8 +263,7 @@ int plan_contraction( int64_t            num_loops,
   int64_t const l_kern_n = l_swap ? l_size_m : l_size_n;
 
   int64_t const l_esz = ( dtype_left == ETIR_BF16 ) ? 2 : 4;
-  int64_t const l_vk  = 16 / l_esz;   // elements per 16-byte vector along K
-  int64_t const l_vr  = 4;            // rows per vector along M/N
+  int64_t const l_vk  = 16 / l_esz;   // elements per 16-byte vector
 
   // ordering
   order_dims( l_km, l_sa );
@@ -309,9 +314,9 @@ int plan_contraction( int64_t            num_loops,
   auto pick_mode = [&]( std::vector< int64_t > const & rows,
                         std::vector< int64_t > const & tk,
                         std::vector< int64_t > const & tc ) -> int32_t {
-    // vectors of 4 consecutive rows: 16 B (fp32) / 8 B (bf16)
-    if(    rows.size() > 0 && runs_contiguous( rows, l_vr, l_vr )
-        && all_multiple( tk, l_vr ) && all_multiple( tc, l_vr ) ) {
+    // 16-byte vectors of consecutive rows (4 fp32 / 8 bf16)
+    if(    rows.size() > 0 && runs_contiguous( rows, l_vk, l_vk )
+        && all_multiple( tk, l_vk ) && all_multiple( tc, l_vk ) ) {
       return LOAD_VEC_MN;
     }
     // 16-byte vectors along K
@@ -464,8 +469,7 @@ int launch_contraction( ContractionPlan const & plan,
   int32_t l_mb = plan.mode_b;
   int64_t const l_esz = ( plan.dtype_in == ETIR_BF16 ) ? 2 : 4;
   auto align_of = [&]( int32_t mode ) -> uintptr_t {
-    if( mode == LOAD_VEC_K )  return 16;
-    if( mode == LOAD_VEC_MN ) return uintptr_t( 4 * l_esz );
+    if( mode == LOAD_VEC_K || mode == LOAD_VEC_MN ) return 16;
     return uintptr_t( l_esz );
   };
   if( uintptr_t( a.a ) % align_of( l_ma ) != 0 ) l_ma = LOAD_SCALAR;
@@ -475,12 +479,16 @@ int launch_contraction( ContractionPlan const & plan,
   if( l_grid > 0x7fffffffLL ) {
     return fail( ETIR_UNDEFINED_ERROR, "contraction: grid too large" );
   }
+  bool const l_kaff = ( a.k_affine != 0 );
+  uint32_t const l_g = (uint32_t) l_grid;
   int l_err;
-  if( plan.dtype_in == ETIR_BF16 ) {
-    l_err = launch_contract_bf16( plan.tile, l_ma, l_mb, a, (uint32_t) l_grid, stream );
-  }
-  else {
-    l_err = launch_contract_f32( plan.tile, l_ma, l_mb, a, (uint32_t) l_grid, stream );
+  switch( plan.tile ) {
+    case TILE_F32_128x128:  l_err = launch_contract_f32_128x128( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
+    case TILE_F32_64x64:    l_err = launch_contract_f32_64x64( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
+    case TILE_BF16_256x256: l_err = launch_contract_bf16_256x256( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
+    case TILE_BF16_128x128: l_err = launch_contract_bf16_128x128( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
+    case TILE_BF16_64x64:   l_err = launch_contract_bf16_64x64( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
+    default: return fail( ETIR_COMPILATION_FAILED, "contraction: unknown tile configuration" );
   }
   if( l_err != ETIR_SUCCESS ) return l_err;
   hipError_t l_he = hipGetLastError();
