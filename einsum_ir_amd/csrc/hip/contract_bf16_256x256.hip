@@ -7,92 +7,92 @@ namespace etir {
 int launch_contract_bf16_256x256( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
                    uint32_t grid, hipStream_t stream ) {
   if( ma == LOAD_SCALAR && mb == LOAD_SCALAR && kaff == false ) {
-    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_SCALAR, LOAD_SCALAR, false > ),
+    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_SCALAR, LOAD_SCALAR, false, 2 > ),
                         dim3( grid ), dim3( 512 ), 0, stream, a );
     return ETIR_SUCCESS;
   }
   if( ma == LOAD_SCALAR && mb == LOAD_VEC_MN && kaff == false ) {
-    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_SCALAR, LOAD_VEC_MN, false > ),
+    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_SCALAR, LOAD_VEC_MN, false, 2 > ),
                         dim3( grid ), dim3( 512 ), 0, stream, a );
     return ETIR_SUCCESS;
   }
   if( ma == LOAD_SCALAR && mb == LOAD_VEC_K && kaff == false ) {
-    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_SCALAR, LOAD_VEC_K, false > ),
+    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_SCALAR, LOAD_VEC_K, false, 2 > ),
                         dim3( grid ), dim3( 512 ), 0, stream, a );
     return ETIR_SUCCESS;
   }
   if( ma == LOAD_VEC_MN && mb == LOAD_SCALAR && kaff == false ) {
-    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_MN, LOAD_SCALAR, false > ),
+    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_MN, LOAD_SCALAR, false, 2 > ),
                         dim3( grid ), dim3( 512 ), 0, stream, a );
     return ETIR_SUCCESS;
   }
   if( ma == LOAD_VEC_MN && mb == LOAD_VEC_MN && kaff == false ) {
-    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_MN, LOAD_VEC_MN, false > ),
+    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_MN, LOAD_VEC_MN, false, 2 > ),
                         dim3( grid ), dim3( 512 ), 0, stream, a );
     return ETIR_SUCCESS;
   }
   if( ma == LOAD_VEC_MN && mb == LOAD_VEC_K && kaff == false ) {
-    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_MN, LOAD_VEC_K, false > ),
+    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_MN, LOAD_VEC_K, false, 2 > ),
                         dim3( grid ), dim3( 512 ), 0, stream, a );
     return ETIR_SUCCESS;
   }
   if( ma == LOAD_VEC_K && mb == LOAD_SCALAR && kaff == false ) {
-    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_K, LOAD_SCALAR, false > ),
+    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_K, LOAD_SCALAR, false, 2 > ),
                         dim3( grid ), dim3( 512 ), 0, stream, a );
     return ETIR_SUCCESS;
   }
   if( ma == LOAD_VEC_K && mb == LOAD_VEC_MN && kaff == false ) {
-    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_K, LOAD_VEC_MN, false > ),
+    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_K, LOAD_VEC_MN, false, 2 > ),
                         dim3( grid ), dim3( 512 ), 0, stream, a );
     return ETIR_SUCCESS;
   }
   if( ma == LOAD_VEC_K && mb == LOAD_VEC_K && kaff == false ) {
-    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_K, LOAD_VEC_K, false > ),
+    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_K, LOAD_VEC_K, false, 2 > ),
                         dim3( grid ), dim3( 512 ), 0, stream, a );
     return ETIR_SUCCESS;
   }
   if( ma == LOAD_SCALAR && mb == LOAD_SCALAR && kaff == true ) {
-    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_SCALAR, LOAD_SCALAR, true > ),
+    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_SCALAR, LOAD_SCALAR, true, 2 > ),
                         dim3( grid ), dim3( 512 ), 0, stream, a );
     return ETIR_SUCCESS;
   }
   if( ma == LOAD_SCALAR && mb == LOAD_VEC_MN && kaff == true ) {
-    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_SCALAR, LOAD_VEC_MN, true > ),
+    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_SCALAR, LOAD_VEC_MN, true, 2 > ),
                         dim3( grid ), dim3( 512 ), 0, stream, a );
     return ETIR_SUCCESS;
   }
   if( ma == LOAD_SCALAR && mb == LOAD_VEC_K && kaff == true ) {
-    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_SCALAR, LOAD_VEC_K, true > ),
+    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_SCALAR, LOAD_VEC_K, true, 2 > ),
                         dim3( grid ), dim3( 512 ), 0, stream, a );
     return ETIR_SUCCESS;
   }
   if( ma == LOAD_VEC_MN && mb == LOAD_SCALAR && kaff == true ) {
-    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_MN, LOAD_SCALAR, true > ),
+    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_MN, LOAD_SCALAR, true, 2 > ),
                         dim3( grid ), dim3( 512 ), 0, stream, a );
     return ETIR_SUCCESS;
   }
   if( ma == LOAD_VEC_MN && mb == LOAD_VEC_MN && kaff == true ) {
-    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_MN, LOAD_VEC_MN, true > ),
+    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_MN, LOAD_VEC_MN, true, 2 > ),
                         dim3( grid ), dim3( 512 ), 0, stream, a );
     return ETIR_SUCCESS;
   }
   if( ma == LOAD_VEC_MN && mb == LOAD_VEC_K && kaff == true ) {
-    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_MN, LOAD_VEC_K, true > ),
+    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_MN, LOAD_VEC_K, true, 2 > ),
                         dim3( grid ), dim3( 512 ), 0, stream, a );
     return ETIR_SUCCESS;
   }
   if( ma == LOAD_VEC_K && mb == LOAD_SCALAR && kaff == true ) {
-    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_K, LOAD_SCALAR, true > ),
+    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_K, LOAD_SCALAR, true, 2 > ),
                         dim3( grid ), dim3( 512 ), 0, stream, a );
     return ETIR_SUCCESS;
   }
   if( ma == LOAD_VEC_K && mb == LOAD_VEC_MN && kaff == true ) {
-    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_K, LOAD_VEC_MN, true > ),
+    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_K, LOAD_VEC_MN, true, 2 > ),
                         dim3( grid ), dim3( 512 ), 0, stream, a );
     return ETIR_SUCCESS;
   }
   if( ma == LOAD_VEC_K && mb == LOAD_VEC_K && kaff == true ) {
-    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_K, LOAD_VEC_K, true > ),
+    hipLaunchKernelGGL( ( kern::contract_kernel< ETIR_BF16, 256, 256, 64, 2, 4, LOAD_VEC_K, LOAD_VEC_K, true, 2 > ),
                         dim3( grid ), dim3( 512 ), 0, stream, a );
     return ETIR_SUCCESS;
   }

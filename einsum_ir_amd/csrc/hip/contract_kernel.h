@@ -336,8 +336,8 @@ struct LdsSize {
 // ---------------------------------------------------------------------------
 // the kernel
 // ---------------------------------------------------------------------------
-template< int DT, int BM, int BN, int BK, int WM, int WN, int MA, int MB, bool KAFF >
-__global__ __launch_bounds__( 64 * WM * WN )
+template< int DT, int BM, int BN, int BK, int WM, int WN, int MA, int MB, bool KAFF, int WPE >
+__global__ __launch_bounds__( 64 * WM * WN, WPE )
 void contract_kernel( ContractArgs a ) {
   typedef typename InType< DT >::T TE;
   constexpr int T    = 64 * WM * WN;

@@ -25,6 +25,7 @@
 //   5. the tile shape is chosen from dtype and the number of output tiles.
 #include "etir_internal.h"
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <limits>
 #include <sstream>
@@ -36,6 +37,8 @@ int launch_contract_f32_128x128( int32_t ma, int32_t mb, bool kaff, ContractArgs
 int launch_contract_f32_64x64( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
                                uint32_t grid, hipStream_t stream );
 int launch_contract_bf16_256x256( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
+                                  uint32_t grid, hipStream_t stream );
+int launch_contract_bf16_256x128( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
                                   uint32_t grid, hipStream_t stream );
 int launch_contract_bf16_128x128( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
                                   uint32_t grid, hipStream_t stream );
@@ -143,6 +146,7 @@ char const * tile_str( int32_t t ) {
     case TILE_F32_128x128:  return "f32_128x128x32";
     case TILE_F32_64x64:    return "f32_64x64x32";
     case TILE_BF16_256x256: return "bf16_256x256x64";
+    case TILE_BF16_256x128: return "bf16_256x128x32";
     case TILE_BF16_128x128: return "bf16_128x128x64";
     case TILE_BF16_64x64:   return "bf16_64x64x64";
     default:                return "?";
@@ -154,6 +158,7 @@ void tile_shape( int32_t t, int64_t & bm, int64_t & bn ) {
     case TILE_F32_128x128:  bm = 128; bn = 128; break;
     case TILE_F32_64x64:    bm = 64;  bn = 64;  break;
     case TILE_BF16_256x256: bm = 256; bn = 256; break;
+    case TILE_BF16_256x128: bm = 256; bn = 128; break;
     case TILE_BF16_128x128: bm = 128; bn = 128; break;
     default:                bm = 64;  bn = 64;  break;
   }
@@ -350,9 +355,15 @@ int plan_contraction( int64_t            num_loops,
     plan.tile = ( n_tiles( TILE_F32_128x128 ) >= l_cus ) ? TILE_F32_128x128 : TILE_F32_64x64;
   }
   else {
-    if(      n_tiles( TILE_BF16_256x256 ) >= l_cus ) plan.tile = TILE_BF16_256x256;
+    if(      n_tiles( TILE_BF16_256x128 ) >= 2 * l_cus ) plan.tile = TILE_BF16_256x128;
     else if( n_tiles( TILE_BF16_128x128 ) >= l_cus ) plan.tile = TILE_BF16_128x128;
     else                                             plan.tile = TILE_BF16_64x64;
+  }
+  if( char const * l_env = std::getenv( "ETIR_TILE" ) ) {
+    // diagnostic override of the tile heuristic (must match the dtype)
+    int32_t l_t = std::atoi( l_env );
+    bool const l_t_f32 = ( l_t == TILE_F32_128x128 || l_t == TILE_F32_64x64 );
+    if( l_t >= 0 && l_t <= TILE_BF16_256x128 && l_t != TILE_F64_64x64 && l_t_f32 == l_f32 ) plan.tile = l_t;
   }
   int64_t l_bm, l_bn;
   tile_shape( plan.tile, l_bm, l_bn );
@@ -486,6 +497,7 @@ int launch_contraction( ContractionPlan const & plan,
     case TILE_F32_128x128:  l_err = launch_contract_f32_128x128( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_F32_64x64:    l_err = launch_contract_f32_64x64( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_BF16_256x256: l_err = launch_contract_bf16_256x256( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
+    case TILE_BF16_256x128: l_err = launch_contract_bf16_256x128( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_BF16_128x128: l_err = launch_contract_bf16_128x128( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_BF16_64x64:   l_err = launch_contract_bf16_64x64( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     default: return fail( ETIR_COMPILATION_FAILED, "contraction: unknown tile configuration" );

@@ -108,7 +108,8 @@ enum TileCfg : int32_t {
   TILE_BF16_256x256 = 2,
   TILE_BF16_128x128 = 3,
   TILE_BF16_64x64  = 4,
-  TILE_F64_64x64   = 5
+  TILE_F64_64x64   = 5,
+  TILE_BF16_256x128 = 6
 };
 
 struct ContractArgs {

@@ -1,0 +1,59 @@
+// BinaryContraction on the MI355X: compile() lowers the contraction to the
+// loop IR and creates one device plan through the C ABI
+// (etir_hip_contraction_create); contract() launches it.
+//
+// Sibling of the reference's BinaryContractionTpp
+// (reference src/backend/BinaryContractionTpp.{h,cpp}); the lowering follows
+// BinaryContractionTpp::compile (reference src/backend/BinaryContractionTpp.cpp:4-127).
+// All tensor pointers are device pointers.  contract() is synchronous like
+// the reference's; contract_async() only enqueues on the plan's stream (used
+// by EinsumNode to run a whole tree on one stream).
+#ifndef EINSUM_IR_BACKEND_BINARY_CONTRACTION_HIP
+#define EINSUM_IR_BACKEND_BINARY_CONTRACTION_HIP
+
+#include "BinaryContraction.h"
+#include "einsum_ir_hip.h"
+
+namespace einsum_ir {
+  namespace backend {
+    class BinaryContractionHip;
+  }
+}
+
+class einsum_ir::backend::BinaryContractionHip : public BinaryContraction {
+  private:
+    etir_plan_t m_plan = nullptr;
+    void * m_stream = nullptr;
+    err_t m_last_error = err_t::SUCCESS;
+
+  public:
+    ~BinaryContractionHip();
+
+    err_t compile();
+
+    /** Selects the HIP stream (hipStream_t as void*, nullptr = null stream). **/
+    void set_stream( void * i_stream ) { m_stream = i_stream; }
+
+    void contract( void const * i_tensor_left,
+                   void const * i_tensor_right,
+                   void       * io_tensor_out );
+
+    void contract( void const * i_tensor_left,
+                   void const * i_tensor_right,
+                   void const * i_tensor_out_aux,
+                   void       * io_tensor_out );
+
+    /** Enqueues the contraction on the stream without waiting. **/
+    err_t contract_async( void const * i_tensor_left,
+                          void const * i_tensor_right,
+                          void const * i_tensor_out_aux,
+                          void       * io_tensor_out );
+
+    /** Error of the last contract() call (contract() itself returns void). **/
+    err_t last_error() const { return m_last_error; }
+
+    /** The device plan (diagnostics: etir_hip_plan_describe). **/
+    etir_plan_t plan() const { return m_plan; }
+};
+
+#endif

@@ -1,0 +1,97 @@
+// Dimension-ordering primitives of the tree path (drop-in for the parts of
+// reference src/backend/BinaryPrimitives.h that EinsumNode uses):
+//   swap_inputs  -- which child becomes the left operand
+//                   (reference src/backend/BinaryPrimitives.cpp:87-134);
+//   init         -- block-size targets per dtype/backend (:25-85; HIP added);
+//   reorder      -- internal dimension order of both children for a tensor
+//                   ordering (:833-1711) or a backend (:1713-1768).
+// The blocking_* routines and compileLoopOrder of the reference are not part
+// of the tree path and are not provided.
+#ifndef EINSUM_IR_BACKEND_BINARY_PRIMITIVES
+#define EINSUM_IR_BACKEND_BINARY_PRIMITIVES
+
+#include <cstdint>
+#include <map>
+#include <vector>
+#include "../constants.h"
+
+namespace einsum_ir {
+  namespace backend {
+    class BinaryPrimitives;
+  }
+}
+
+class einsum_ir::backend::BinaryPrimitives {
+  public:
+    int64_t m_size_cb_min = 0;
+    int64_t m_size_cb_max = 0;
+    int64_t m_size_mb_min = 0;
+    int64_t m_size_mb_max = 0;
+    int64_t m_size_nb_min = 0;
+    int64_t m_size_nb_max = 0;
+    int64_t m_size_kb_min = 0;
+    int64_t m_size_kb_max = 0;
+
+    //! placement of the blocked C dims inside the inputs
+    enum class CBlock { NONE, INNER, OUTER };
+
+    /**
+     * Generic reorder used by the three tensor orderings: classifies the
+     * trailing output dims into blocked C (per `i_cblock`), blocked M and
+     * blocked N groups (size targets min/max), blocks the largest K dims,
+     * and writes the new dim orders of the left/right inputs; the output
+     * keeps its order.
+     **/
+    static err_t reorder_generic( CBlock                               i_cblock,
+                                  int64_t                              i_size_cb_min,
+                                  int64_t                              i_size_cb_max,
+                                  int64_t                              i_size_mb_min,
+                                  int64_t                              i_size_mb_max,
+                                  int64_t                              i_size_nb_min,
+                                  int64_t                              i_size_nb_max,
+                                  int64_t                              i_size_kb_min,
+                                  int64_t                              i_size_kb_max,
+                                  int64_t                              i_num_dims_left,
+                                  int64_t                              i_num_dims_right,
+                                  int64_t                              i_num_dims_out,
+                                  std::map< int64_t, int64_t > const * i_dim_sizes,
+                                  int64_t                            * io_dim_ids_left,
+                                  int64_t                            * io_dim_ids_right,
+                                  int64_t                            * io_dim_ids_out );
+
+    void init( int64_t i_size_cb_min, int64_t i_size_cb_max,
+               int64_t i_size_mb_min, int64_t i_size_mb_max,
+               int64_t i_size_nb_min, int64_t i_size_nb_max,
+               int64_t i_size_kb_min, int64_t i_size_kb_max );
+
+    err_t init( data_t    i_data_type,
+                backend_t i_backend_type );
+
+    /** True if the inputs have to be swapped so that the output's fastest non-C dim is M. **/
+    static bool swap_inputs( int64_t         i_num_dims_left,
+                             int64_t         i_num_dims_right,
+                             int64_t         i_num_dims_out,
+                             int64_t const * i_dim_ids_left,
+                             int64_t const * i_dim_ids_right,
+                             int64_t const * i_dim_ids_out );
+
+    err_t reorder( tenord_t                             i_primitive_ordering,
+                   int64_t                              i_num_dims_left,
+                   int64_t                              i_num_dims_right,
+                   int64_t                              i_num_dims_out,
+                   std::map< int64_t, int64_t > const * i_dim_sizes,
+                   int64_t                            * io_dim_ids_left,
+                   int64_t                            * io_dim_ids_right,
+                   int64_t                            * io_dim_ids_out ) const;
+
+    err_t reorder( backend_t                            i_backend_type,
+                   int64_t                              i_num_dims_left,
+                   int64_t                              i_num_dims_right,
+                   int64_t                              i_num_dims_out,
+                   std::map< int64_t, int64_t > const * i_dim_sizes,
+                   int64_t                            * io_dim_ids_left,
+                   int64_t                            * io_dim_ids_right,
+                   int64_t                            * io_dim_ids_out ) const;
+};
+
+#endif

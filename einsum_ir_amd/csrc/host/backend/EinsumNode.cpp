@@ -1,0 +1,406 @@
+// Behaviour follows the reference's EinsumNode (reference src/backend/EinsumNode.cpp):
+//   init overloads          :21-190  (environment switches EINSUM_IR_BACKEND,
+//                                     EINSUM_IR_REORDER_DIMS, EINSUM_IR_PACK_INPUTS)
+//   compile_recursive       :204-454 (swap_inputs, reorder, contraction, unary
+//                                     copy, offsets, memory need, child order)
+//   store_and_lock_data     :458-479
+//   eval                    :496-540
+//   compile_memory_usage    :560-578, requires_permutation :580-593
+// Device-specific: one stream for the tree, device arena and device copies.
+#include <stdexcept>
+#include "EinsumNode.h"
+#include "BinaryContractionFactory.h"
+#include "BinaryContractionHip.h"
+#include "BinaryPrimitives.h"
+#include "Tensor.h"
+#include "UnaryHip.h"
+#include "einsum_ir_hip.h"
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
+namespace {
+  bool env_flag( char const * i_name, bool i_default ) {
+    char const * l_v = std::getenv( i_name );
+    if( l_v == nullptr ) return i_default;
+    return std::strcmp( l_v, "1" ) == 0 || std::strcmp( l_v, "true" ) == 0;
+  }
+}
+
+einsum_ir::backend::EinsumNode::~EinsumNode() {
+  delete m_unary;
+  delete m_cont;
+  if( m_data_ptr_int != nullptr ) {
+    etir_hip_free( m_data_ptr_int );
+  }
+}
+
+void einsum_ir::backend::EinsumNode::init( int64_t                              i_num_dims,
+                                           int64_t                      const * i_dim_ids,
+                                           std::map< int64_t, int64_t > const * i_dim_sizes_inner,
+                                           std::map< int64_t, int64_t > const * i_dim_sizes_outer,
+                                           data_t                               i_dtype,
+                                           void                               * i_data_ptr,
+                                           MemoryManager                      * i_memory ) {
+  m_dtype = i_dtype;
+  m_ktype_first_touch = kernel_t::UNDEFINED_KTYPE;
+  m_ktype_main        = kernel_t::UNDEFINED_KTYPE;
+  m_ktype_last_touch  = kernel_t::UNDEFINED_KTYPE;
+  m_size = 0;
+  m_num_dims = i_num_dims;
+  m_dim_ids_ext = i_dim_ids;
+  m_dim_ids_int.assign( i_dim_ids, i_dim_ids + i_num_dims );
+  m_dim_sizes_inner = i_dim_sizes_inner;
+  m_dim_sizes_outer = ( i_dim_sizes_outer != nullptr ) ? i_dim_sizes_outer : i_dim_sizes_inner;
+  m_dim_sizes_aux_outer = nullptr;
+  m_offsets_aux_ext = nullptr;
+  m_offsets_ext = nullptr;
+  m_children.clear();
+  m_data_ptr_int = nullptr;
+  m_data_ptr_active = nullptr;
+  m_data_ptr_ext = i_data_ptr;
+  m_data_ptr_aux_ext = nullptr;
+
+  // backend selection: the reference's variable, with HIP as this library's backend
+  m_btype_unary  = backend_t::HIP;
+  m_btype_binary = backend_t::AUTO;
+  if( char const * l_bt = std::getenv( "EINSUM_IR_BACKEND" ) ) {
+    if(      std::strcmp( l_bt, "AUTO" )   == 0 ) m_btype_binary = backend_t::AUTO;
+    else if( std::strcmp( l_bt, "HIP" )    == 0 ) m_btype_binary = backend_t::HIP;
+    else if( std::strcmp( l_bt, "TPP" )    == 0 ) m_btype_binary = backend_t::TPP;
+    else if( std::strcmp( l_bt, "BLAS" )   == 0 ) m_btype_binary = backend_t::BLAS;
+    else if( std::strcmp( l_bt, "TBLIS" )  == 0 ) m_btype_binary = backend_t::TBLIS;
+    else if( std::strcmp( l_bt, "SCALAR" ) == 0 ) m_btype_binary = backend_t::SCALAR;
+  }
+  m_reorder_dims = env_flag( "EINSUM_IR_REORDER_DIMS", true );
+  m_pack_inputs  = env_flag( "EINSUM_IR_PACK_INPUTS", false );
+
+  m_unary = nullptr;
+  m_cont = nullptr;
+  m_num_ops_node = 0;
+  m_num_ops_children = 0;
+  m_num_tasks_intra_op = 1;
+  m_memory = i_memory;
+  m_mem_id = 0;
+  m_count_mem_users = 1;
+  m_active_mem_users = 0;
+  m_req_mem = 0;
+  m_mem_subtree = 0;
+  m_compiled = false;
+  m_data_locked = false;
+}
+
+void einsum_ir::backend::EinsumNode::init( int64_t                              i_num_dims,
+                                           int64_t                      const * i_dim_ids,
+                                           std::map< int64_t, int64_t > const * i_dim_sizes_inner,
+                                           std::map< int64_t, int64_t > const * i_dim_sizes_outer,
+                                           data_t                               i_dtype,
+                                           void                               * i_data_ptr,
+                                           EinsumNode                         * i_child,
+                                           MemoryManager                      * i_memory,
+                                           int64_t                              i_num_threads ) {
+  init( i_num_dims, i_dim_ids, i_dim_sizes_inner, i_dim_sizes_outer, i_dtype, i_data_ptr, i_memory );
+  m_children.assign( 1, i_child );
+  m_num_threads = i_num_threads;
+}
+
+void einsum_ir::backend::EinsumNode::init( int64_t                              i_num_dims,
+                                           int64_t                      const * i_dim_ids,
+                                           std::map< int64_t, int64_t > const * i_dim_sizes_inner,
+                                           std::map< int64_t, int64_t > const * i_dim_sizes_aux_outer,
+                                           std::map< int64_t, int64_t > const * i_dim_sizes_outer,
+                                           std::map< int64_t, int64_t > const * i_offsets_aux,
+                                           std::map< int64_t, int64_t > const * i_offsets,
+                                           data_t                               i_dtype,
+                                           void                               * i_data_ptr_aux,
+                                           void                               * i_data_ptr,
+                                           kernel_t                             i_ktype_first_touch,
+                                           kernel_t                             i_ktype_main,
+                                           kernel_t                             i_ktype_last_touch,
+                                           EinsumNode                         * i_left,
+                                           EinsumNode                         * i_right,
+                                           MemoryManager                      * i_memory,
+                                           int64_t                              i_num_threads ) {
+  init( i_num_dims, i_dim_ids, i_dim_sizes_inner, i_dim_sizes_outer, i_dtype, i_data_ptr, i_memory );
+  m_dim_sizes_aux_outer = i_dim_sizes_aux_outer;
+  m_offsets_aux_ext     = i_offsets_aux;
+  m_offsets_ext         = i_offsets;
+  m_data_ptr_aux_ext    = i_data_ptr_aux;
+  m_ktype_first_touch   = i_ktype_first_touch;
+  m_ktype_main          = i_ktype_main;
+  m_ktype_last_touch    = i_ktype_last_touch;
+  m_children = { i_left, i_right };
+  m_num_threads = i_num_threads;
+}
+
+void einsum_ir::backend::EinsumNode::set_stream( void * i_stream ) {
+  m_stream = i_stream;
+  for( EinsumNode * l_ch : m_children ) l_ch->set_stream( i_stream );
+}
+
+einsum_ir::err_t einsum_ir::backend::EinsumNode::compile() {
+  err_t l_err = compile_recursive();
+  if( l_err != err_t::SUCCESS ) return l_err;
+  if( m_memory == nullptr ) return err_t::UNDEFINED_ERROR;
+  compile_memory_usage();
+  return m_memory->alloc_all_memory();
+}
+
+einsum_ir::err_t einsum_ir::backend::EinsumNode::compile_recursive() {
+  err_t l_err = err_t::UNDEFINED_ERROR;
+
+  // backend of the contraction: AUTO resolves to HIP unless the kernels are
+  // complex (the reference sends those to BLAS, which this build lacks)
+  if( m_btype_binary == backend_t::AUTO ) {
+    bool l_cpx = ce_cpx_op( m_ktype_first_touch ) || ce_cpx_op( m_ktype_main ) || ce_cpx_op( m_ktype_last_touch );
+    m_btype_binary = l_cpx ? backend_t::BLAS : backend_t::HIP;
+  }
+  if( !BinaryContractionFactory::supports( m_btype_binary ) ) {
+    return err_t::INVALID_BACKEND;
+  }
+
+  try {
+    m_size = Tensor::size( ce_n_bytes( m_dtype ), m_num_dims, m_dim_ids_ext, *m_dim_sizes_outer );
+  }
+  catch( std::out_of_range const & ) {
+    return err_t::COMPILATION_FAILED;
+  }
+
+  if( m_children.size() == 2 ) {
+    // the left operand must provide the output's fastest non-C dim
+    if( BinaryPrimitives::swap_inputs( m_children[0]->m_num_dims, m_children[1]->m_num_dims, m_num_dims,
+                                       m_children[0]->m_dim_ids_ext, m_children[1]->m_dim_ids_ext,
+                                       m_dim_ids_int.data() ) ) {
+      std::swap( m_children[0], m_children[1] );
+    }
+
+    // internal dim orders of the children for the backend's tensor ordering
+    if( m_reorder_dims ) {
+      BinaryPrimitives l_prims;
+      l_prims.init( m_dtype, m_btype_binary );
+      l_err = l_prims.reorder( m_btype_binary,
+                               m_children[0]->m_num_dims, m_children[1]->m_num_dims, m_num_dims,
+                               m_dim_sizes_inner,
+                               m_children[0]->m_dim_ids_int.data(),
+                               m_children[1]->m_dim_ids_int.data(),
+                               m_dim_ids_int.data() );
+      if( l_err != err_t::SUCCESS ) return l_err;
+    }
+
+    delete m_cont;
+    m_cont = BinaryContractionFactory::create( m_btype_binary );
+    m_cont->init( m_children[0]->m_num_dims, m_children[1]->m_num_dims, m_num_dims,
+                  m_dim_sizes_inner,
+                  m_children[0]->m_dim_sizes_outer, m_children[1]->m_dim_sizes_outer,
+                  m_dim_sizes_aux_outer, m_dim_sizes_outer,
+                  nullptr,
+                  m_children[0]->m_dim_ids_int.data(), m_children[1]->m_dim_ids_int.data(),
+                  m_dim_ids_int.data(),
+                  nullptr, nullptr,
+                  m_memory,
+                  m_children[0]->m_dtype, m_children[1]->m_dtype,
+                  ( m_dtype == data_t::BF16 ) ? data_t::FP32 : m_dtype,
+                  m_dtype,
+                  m_ktype_first_touch, m_ktype_main, m_ktype_last_touch,
+                  m_num_threads );
+    static_cast< BinaryContractionHip * >( m_cont )->set_stream( m_stream );
+    l_err = m_cont->compile();
+    if( l_err != err_t::SUCCESS ) return l_err;
+  }
+
+  // unary copy: external layout -> internal layout (leaves), or the child's
+  // layout -> this node's layout (one child)
+  delete m_unary;
+  UnaryHip * l_unary = new UnaryHip();
+  m_unary = l_unary;
+  l_unary->set_stream( m_stream );
+  if( m_children.size() != 1 ) {
+    m_unary->init( m_num_dims, m_dim_sizes_outer, m_dim_ids_ext, m_dim_ids_int.data(),
+                   m_dtype, m_dtype, m_dtype, kernel_t::COPY, 1 );
+  }
+  else {
+    // the child's data is in its internal layout; the parent reads this node's
+    // data in this node's internal layout (both equal the external ones unless
+    // a binary parent reordered them)
+    m_unary->init( m_num_dims, m_dim_sizes_outer, m_children[0]->m_dim_ids_int.data(), m_dim_ids_int.data(),
+                   m_dtype, m_dtype, m_dtype, kernel_t::COPY, 1 );
+  }
+  l_err = m_unary->compile();
+  if( l_err != err_t::SUCCESS ) return l_err;
+
+  // byte offsets of the node's data inside larger (outer) tensors
+  auto offset_bytes = [this]( std::map< int64_t, int64_t > const * i_offsets,
+                              std::map< int64_t, int64_t > const * i_outer ) -> int64_t {
+    int64_t l_off = 0;
+    int64_t l_stride = 1;
+    for( int64_t l_di = m_num_dims - 1; l_di >= 0; l_di-- ) {
+      int64_t const l_id = m_dim_ids_int[l_di];
+      auto l_it = i_offsets->find( l_id );
+      if( l_it != i_offsets->end() ) l_off += l_stride * l_it->second;
+      l_stride *= i_outer->at( l_id );
+    }
+    return l_off * ce_n_bytes( m_dtype );
+  };
+  if( m_offsets_aux_ext != nullptr && m_dim_sizes_aux_outer != nullptr ) {
+    m_offset_aux_bytes = offset_bytes( m_offsets_aux_ext, m_dim_sizes_aux_outer );
+  }
+  if( m_offsets_ext != nullptr ) {
+    m_offset_bytes = offset_bytes( m_offsets_ext, m_dim_sizes_outer );
+  }
+
+  // memory need: intermediates and permuted inputs live in the arena
+  m_req_mem = ( m_data_ptr_ext == nullptr || requires_permutation() ) ? m_size : 0;
+
+  // children, and the order that minimises the peak memory of the subtree
+  if( m_children.size() > 1 ) {
+    for( EinsumNode * l_ch : m_children ) {
+      l_err = l_ch->compile_recursive();
+      if( l_err != err_t::SUCCESS ) return l_err;
+    }
+    int64_t const l_m0 = m_children[0]->m_mem_subtree;
+    int64_t const l_m1 = m_children[1]->m_mem_subtree;
+    int64_t const l_first0 = std::max( l_m0, l_m1 + m_children[0]->m_req_mem );
+    int64_t const l_first1 = std::max( l_m1, l_m0 + m_children[1]->m_req_mem );
+    if( l_first0 <= l_first1 ) {
+      m_mem_subtree = l_first0;
+      m_exec_order = { 0, 1 };
+    }
+    else {
+      m_mem_subtree = l_first1;
+      m_exec_order = { 1, 0 };
+    }
+    m_mem_subtree = std::max( m_mem_subtree,
+                              m_req_mem + m_children[0]->m_req_mem + m_children[1]->m_req_mem );
+  }
+  else if( m_children.size() == 1 ) {
+    l_err = m_children[0]->compile_recursive();
+    if( l_err != err_t::SUCCESS ) return l_err;
+    m_exec_order = { 0 };
+    m_mem_subtree = std::max( m_children[0]->m_mem_subtree, m_req_mem + m_children[0]->m_req_mem );
+  }
+  else {
+    m_mem_subtree = m_req_mem;
+  }
+
+  m_num_ops_node = ( m_children.size() > 1 ) ? m_cont->num_ops() : 0;
+  m_num_ops_children = 0;
+  for( EinsumNode * l_ch : m_children ) {
+    m_num_ops_children += l_ch->m_num_ops_node + l_ch->m_num_ops_children;
+  }
+
+  m_compiled = true;
+  return err_t::SUCCESS;
+}
+
+einsum_ir::err_t einsum_ir::backend::EinsumNode::store_and_lock_data() {
+  if( !m_compiled ) return err_t::CALLED_BEFORE_COMPILATION;
+  if( m_data_ptr_ext == nullptr ) return err_t::NO_DATA_PTR_PROVIDED;
+  if( m_data_ptr_int == nullptr ) {
+    if( etir_hip_malloc( &m_data_ptr_int, m_size ) != ETIR_SUCCESS ) return err_t::UNDEFINED_ERROR;
+  }
+  UnaryHip * l_unary = static_cast< UnaryHip * >( m_unary );
+  err_t l_err = l_unary->eval_async( m_data_ptr_ext, m_data_ptr_int );
+  if( l_err != err_t::SUCCESS ) return l_err;
+  if( etir_hip_synchronize( m_stream ) != ETIR_SUCCESS ) return err_t::UNDEFINED_ERROR;
+  m_data_locked = true;
+  return err_t::SUCCESS;
+}
+
+einsum_ir::err_t einsum_ir::backend::EinsumNode::unlock_data() {
+  if( m_data_ptr_ext == nullptr ) return err_t::NO_DATA_PTR_PROVIDED;
+  if( m_data_ptr_int != nullptr ) {
+    etir_hip_free( m_data_ptr_int );
+    m_data_ptr_int = nullptr;
+  }
+  m_data_locked = false;
+  return err_t::SUCCESS;
+}
+
+einsum_ir::err_t einsum_ir::backend::EinsumNode::eval_async() {
+  if( !m_compiled ) return err_t::CALLED_BEFORE_COMPILATION;
+  for( std::size_t l_ch = 0; l_ch < m_children.size(); l_ch++ ) {
+    err_t l_err = m_children[ m_exec_order[l_ch] ]->eval_async();
+    if( l_err != err_t::SUCCESS ) return l_err;
+  }
+
+  if( m_data_locked ) {
+    m_data_ptr_active = m_data_ptr_int;
+  }
+  else if( m_mem_id ) {
+    m_data_ptr_active = m_memory->get_mem_ptr( m_mem_id );
+    m_active_mem_users = m_count_mem_users;
+  }
+  else {
+    m_data_ptr_active = m_data_ptr_ext;
+  }
+
+  UnaryHip * l_unary = static_cast< UnaryHip * >( m_unary );
+  if( m_children.size() != 1 ) {
+    if( !m_data_locked && m_data_ptr_ext != nullptr && m_req_mem != 0 ) {
+      err_t l_err = l_unary->eval_async( m_data_ptr_ext, m_data_ptr_active );
+      if( l_err != err_t::SUCCESS ) return l_err;
+    }
+  }
+  else {
+    err_t l_err = l_unary->eval_async( m_children[0]->m_data_ptr_active, m_data_ptr_active );
+    if( l_err != err_t::SUCCESS ) return l_err;
+  }
+
+  if( m_children.size() == 2 ) {
+    void const * l_aux = ( m_data_ptr_aux_int != nullptr ) ? m_data_ptr_aux_int : m_data_ptr_aux_ext;
+    if( l_aux != nullptr ) l_aux = static_cast< char const * >( l_aux ) + m_offset_aux_bytes;
+    void * l_out = static_cast< char * >( m_data_ptr_active ) + m_offset_bytes;
+    err_t l_err = static_cast< BinaryContractionHip * >( m_cont )->contract_async( m_children[0]->m_data_ptr_active,
+                                                                                   m_children[1]->m_data_ptr_active,
+                                                                                   l_aux, l_out );
+    if( l_err != err_t::SUCCESS ) return l_err;
+  }
+  return err_t::SUCCESS;
+}
+
+void einsum_ir::backend::EinsumNode::eval() {
+  err_t l_err = eval_async();
+  if( l_err == err_t::SUCCESS && etir_hip_synchronize( m_stream ) != ETIR_SUCCESS ) {
+    l_err = err_t::UNDEFINED_ERROR;
+  }
+  if( l_err != err_t::SUCCESS ) {
+    std::fprintf( stderr, "einsum_ir: tree evaluation failed (%d): %s\n", (int) l_err, etir_hip_last_error() );
+  }
+}
+
+int64_t einsum_ir::backend::EinsumNode::num_ops( bool i_children ) {
+  return m_num_ops_node + ( i_children ? m_num_ops_children : 0 );
+}
+
+void einsum_ir::backend::EinsumNode::cancel_memory_reservation() {
+  m_active_mem_users--;
+  if( m_active_mem_users <= 0 && m_mem_id ) {
+    m_memory->remove_reservation( m_mem_id );
+  }
+}
+
+void einsum_ir::backend::EinsumNode::compile_memory_usage() {
+  m_memory->m_layer_id++;
+  for( std::size_t l_ch = 0; l_ch < m_children.size(); l_ch++ ) {
+    m_children[ m_exec_order[l_ch] ]->compile_memory_usage();
+  }
+  m_memory->m_layer_id--;
+
+  if( m_req_mem ) {
+    m_mem_id = m_memory->reserve_memory( m_req_mem );
+  }
+  // planning walk: the children's data is released once this node is planned
+  for( EinsumNode * l_ch : m_children ) {
+    l_ch->m_active_mem_users = l_ch->m_count_mem_users;
+    l_ch->cancel_memory_reservation();
+  }
+}
+
+bool einsum_ir::backend::EinsumNode::requires_permutation() {
+  if( m_dim_ids_ext == m_dim_ids_int.data() || m_data_ptr_ext == nullptr ) return false;
+  for( int64_t l_di = 0; l_di < m_num_dims; l_di++ ) {
+    if( m_dim_ids_ext[l_di] != m_dim_ids_int[l_di] ) return true;
+  }
+  return false;
+}

@@ -1,0 +1,160 @@
+// Node of an einsum tree, executed device-resident on one HIP stream.
+//
+// Drop-in for the reference's einsum_ir::backend::EinsumNode
+// (reference src/backend/EinsumNode.h:16-270): same three init overloads,
+// compile / store_and_lock_data / unlock_data / eval / num_ops.  Differences:
+//   - all data pointers are device pointers; intermediates live in the
+//     MemoryManager's single HBM arena; locked data is a device copy;
+//   - eval() enqueues the whole tree (permutes and contractions, post-order)
+//     on one stream and synchronises once, at the end;
+//   - the backend is HIP (EINSUM_IR_BACKEND unset, AUTO or HIP).
+#ifndef EINSUM_IR_BACKEND_EINSUM_NODE
+#define EINSUM_IR_BACKEND_EINSUM_NODE
+
+#include <vector>
+#include "BinaryContraction.h"
+#include "MemoryManager.h"
+#include "Unary.h"
+#include "../constants.h"
+
+namespace einsum_ir {
+  namespace backend {
+    class EinsumNode;
+    class BinaryContractionHip;
+    class UnaryHip;
+  }
+}
+
+class einsum_ir::backend::EinsumNode {
+  public:
+    data_t m_dtype = data_t::UNDEFINED_DTYPE;
+
+    kernel_t m_ktype_first_touch = kernel_t::UNDEFINED_KTYPE;
+    kernel_t m_ktype_main = kernel_t::UNDEFINED_KTYPE;
+    kernel_t m_ktype_last_touch = kernel_t::UNDEFINED_KTYPE;
+
+    //! bytes of the node's tensor
+    int64_t m_size = 0;
+
+    int64_t m_num_dims = 0;
+    int64_t const * m_dim_ids_ext = nullptr;
+    std::vector< int64_t > m_dim_ids_int;
+
+    std::map< int64_t, int64_t > const * m_dim_sizes_inner = nullptr;
+    std::map< int64_t, int64_t > const * m_dim_sizes_aux_outer = nullptr;
+    std::map< int64_t, int64_t > const * m_dim_sizes_outer = nullptr;
+
+    std::vector< EinsumNode * > m_children;
+
+    void * m_data_ptr_int = nullptr;
+    void * m_data_ptr_ext = nullptr;
+    void * m_data_ptr_active = nullptr;
+    void * m_data_ptr_aux_int = nullptr;
+    void * m_data_ptr_aux_ext = nullptr;
+
+    std::map< int64_t, int64_t > const * m_offsets_aux_ext = nullptr;
+    std::map< int64_t, int64_t > const * m_offsets_ext = nullptr;
+    int64_t m_offset_aux_bytes = 0;
+    int64_t m_offset_bytes = 0;
+
+    bool m_reorder_dims = false;
+    bool m_pack_inputs = false;
+
+    backend_t m_btype_unary  = backend_t::UNDEFINED_BACKEND;
+    backend_t m_btype_binary = backend_t::UNDEFINED_BACKEND;
+
+    Unary * m_unary = nullptr;
+    BinaryContraction * m_cont = nullptr;
+
+    MemoryManager * m_memory = nullptr;
+    int64_t m_mem_id = 0;
+    int64_t m_count_mem_users = 0;
+    int64_t m_active_mem_users = 0;
+    int64_t m_req_mem = 0;
+    int64_t m_mem_subtree = 0;
+
+    std::vector< int64_t > m_exec_order;
+
+    int64_t m_num_ops_node = 0;
+    int64_t m_num_ops_children = 0;
+
+    int64_t m_num_tasks_intra_op = 1;
+
+    bool m_compiled = false;
+    bool m_data_locked = false;
+
+    int64_t m_num_threads = 1;
+
+    //! HIP stream of the whole tree (hipStream_t as void*, nullptr = null stream)
+    void * m_stream = nullptr;
+
+    ~EinsumNode();
+
+    /** Leaf node (reference EinsumNode.h:141-157). **/
+    void init( int64_t                              i_num_dims,
+               int64_t                      const * i_dim_ids,
+               std::map< int64_t, int64_t > const * i_dim_sizes_inner,
+               std::map< int64_t, int64_t > const * i_dim_sizes_outer,
+               data_t                               i_dtype,
+               void                               * i_data_ptr,
+               MemoryManager                      * i_memory );
+
+    /** Node with one child: a permutation of the child's tensor. **/
+    void init( int64_t                              i_num_dims,
+               int64_t                      const * i_dim_ids,
+               std::map< int64_t, int64_t > const * i_dim_sizes_inner,
+               std::map< int64_t, int64_t > const * i_dim_sizes_outer,
+               data_t                               i_dtype,
+               void                               * i_data_ptr,
+               EinsumNode                         * i_child,
+               MemoryManager                      * i_memory,
+               int64_t                              i_num_threads );
+
+    /** Node with two children: a binary contraction. **/
+    void init( int64_t                              i_num_dims,
+               int64_t                      const * i_dim_ids,
+               std::map< int64_t, int64_t > const * i_dim_sizes_inner,
+               std::map< int64_t, int64_t > const * i_dim_sizes_aux_outer,
+               std::map< int64_t, int64_t > const * i_dim_sizes_outer,
+               std::map< int64_t, int64_t > const * i_offsets_aux,
+               std::map< int64_t, int64_t > const * i_offsets,
+               data_t                               i_dtype,
+               void                               * i_data_ptr_aux,
+               void                               * i_data_ptr,
+               kernel_t                             i_ktype_first_touch,
+               kernel_t                             i_ktype_main,
+               kernel_t                             i_ktype_last_touch,
+               EinsumNode                         * i_left,
+               EinsumNode                         * i_right,
+               MemoryManager                      * i_memory,
+               int64_t                              i_num_threads );
+
+    /** Compiles the tree below this node, plans and allocates the arena. **/
+    err_t compile();
+
+    err_t compile_recursive();
+
+    /** Copies (and permutes) the external input once into device memory owned by the node. **/
+    err_t store_and_lock_data();
+
+    err_t unlock_data();
+
+    /** Evaluates the tree and waits for the result. **/
+    void eval();
+
+    /** Enqueues the evaluation of the tree on the stream without waiting. **/
+    err_t eval_async();
+
+    /** Sets the stream of this node and its subtree (before compile()). **/
+    void set_stream( void * i_stream );
+
+    int64_t num_ops( bool i_children = true );
+
+    void cancel_memory_reservation();
+
+    void compile_memory_usage();
+
+    bool requires_permutation();
+};
+
+#endif

@@ -1,0 +1,46 @@
+#include "UnaryHip.h"
+#include <cstdio>
+
+einsum_ir::backend::UnaryHip::~UnaryHip() {
+  if( m_plan != nullptr ) {
+    etir_hip_plan_destroy( m_plan );
+  }
+}
+
+einsum_ir::err_t einsum_ir::backend::UnaryHip::compile() {
+  if( compile_base() != err_t::SUCCESS ) {
+    return err_t::COMPILATION_FAILED;
+  }
+  if( m_plan != nullptr ) {
+    etir_hip_plan_destroy( m_plan );
+    m_plan = nullptr;
+  }
+  int l_rc = etir_hip_permute_create( m_num_dims, m_sizes_out.data(), m_strides_in.data(),
+                                      m_strides_out.data(), m_dtype_in, m_dtype_comp, m_dtype_out,
+                                      m_ktype_main, &m_plan );
+  if( l_rc != ETIR_SUCCESS ) {
+    return static_cast< err_t >( l_rc );
+  }
+  m_compiled = true;
+  return err_t::SUCCESS;
+}
+
+einsum_ir::err_t einsum_ir::backend::UnaryHip::eval_async( void const * i_tensor_in,
+                                                           void       * io_tensor_out ) {
+  if( !m_compiled ) {
+    return err_t::CALLED_BEFORE_COMPILATION;
+  }
+  return static_cast< err_t >( etir_hip_permute_execute( m_plan, i_tensor_in, io_tensor_out, m_stream ) );
+}
+
+void einsum_ir::backend::UnaryHip::eval( void const * i_tensor_in,
+                                         void       * io_tensor_out ) {
+  m_last_error = eval_async( i_tensor_in, io_tensor_out );
+  if( m_last_error == err_t::SUCCESS && etir_hip_synchronize( m_stream ) != ETIR_SUCCESS ) {
+    m_last_error = err_t::UNDEFINED_ERROR;
+  }
+  if( m_last_error != err_t::SUCCESS ) {
+    std::fprintf( stderr, "einsum_ir: permutation failed (%d): %s\n", (int) m_last_error,
+                  etir_hip_last_error() );
+  }
+}

@@ -1,0 +1,42 @@
+// Unary operator on the MI355X: one device permutation plan per operator
+// (etir_hip_permute_create), sibling of the reference's UnaryTpp
+// (reference src/backend/UnaryTpp.cpp:4-54).  eval() is synchronous;
+// eval_async() only enqueues on the stream.  Pointers are device pointers.
+#ifndef EINSUM_IR_BACKEND_UNARY_HIP
+#define EINSUM_IR_BACKEND_UNARY_HIP
+
+#include "Unary.h"
+#include "einsum_ir_hip.h"
+
+namespace einsum_ir {
+  namespace backend {
+    class UnaryHip;
+  }
+}
+
+class einsum_ir::backend::UnaryHip : public Unary {
+  private:
+    etir_plan_t m_plan = nullptr;
+    void * m_stream = nullptr;
+    bool m_compiled = false;
+    err_t m_last_error = err_t::SUCCESS;
+
+  public:
+    ~UnaryHip();
+
+    err_t compile();
+
+    void set_stream( void * i_stream ) { m_stream = i_stream; }
+
+    void eval( void const * i_tensor_in,
+               void       * io_tensor_out );
+
+    err_t eval_async( void const * i_tensor_in,
+                      void       * io_tensor_out );
+
+    err_t last_error() const { return m_last_error; }
+
+    etir_plan_t plan() const { return m_plan; }
+};
+
+#endif

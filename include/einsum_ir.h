@@ -1,0 +1,104 @@
+/*
+ * einsum_ir.h -- C ABI of the operator layer of libeinsum_ir.so.
+ *
+ * The C++ classes (einsum_ir::backend::BinaryContractionHip, UnaryHip,
+ * EinsumNode, einsum_ir::frontend::EinsumExpression, EinsumTree) are the
+ * drop-in for the reference's operator API.  These functions expose the same
+ * operators to callers that can only bind C (ctypes, other languages): each
+ * one builds the objects the reference's bench harnesses build from the same
+ * string inputs (reference src/bench_binary.cpp:212-402,
+ * src/bench_unary.cpp:55-216, src/bench_expression.cpp:8-291,
+ * src/bench_tree.cpp:8-140) and forwards to their init/compile/eval calls.
+ *
+ * Dimension ids are the positions of the sorted dimension names
+ * (EinsumExpressionAscii::parse_dim_ids, reference
+ * src/frontend/EinsumExpressionAscii.cpp:267-303); `dim_sizes` lists the sizes
+ * in ascending id order, as the reference harnesses expect.  Tensor pointers
+ * are device pointers.  Return values are einsum_ir::err_t codes.
+ */
+#ifndef EINSUM_IR_H
+#define EINSUM_IR_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct etir_binary_s     * etir_binary_t;
+typedef struct etir_unary_s      * etir_unary_t;
+typedef struct etir_expression_s * etir_expression_t;
+typedef struct etir_tree_s       * etir_tree_t;
+
+/* BinaryContraction (reference src/backend/BinaryContraction.h:279-391)
+ * through BinaryContractionHip: `expr` is "abkl,cdkl->abcd" or the bracketed
+ * form; outer sizes (NULL = inner sizes) describe views into larger tensors;
+ * aux_outer_sizes (NULL allowed) is the auxiliary tensor's outer size per id. */
+int etir_binary_create( char const    * expr,
+                        int64_t const * dim_sizes,
+                        int64_t         num_dim_sizes,
+                        int64_t const * aux_outer_sizes,
+                        int32_t         dtype_left,
+                        int32_t         dtype_right,
+                        int32_t         dtype_comp,
+                        int32_t         dtype_out,
+                        int32_t         ktype_first_touch,
+                        int32_t         ktype_main,
+                        int32_t         ktype_last_touch,
+                        etir_binary_t * handle );
+/* BinaryContraction::contract with auxiliary tensor (synchronous). */
+int etir_binary_contract( etir_binary_t handle, void const * left, void const * right,
+                          void const * out_aux, void * out );
+/* BinaryContraction::num_ops */
+int64_t etir_binary_num_ops( etir_binary_t handle );
+/* m_num_dims_{c,m,n,k} and the products of m_sizes_{c,m,n,k} (read by the harnesses) */
+int etir_binary_sizes( etir_binary_t handle, int64_t * num_dims_cmnk, int64_t * sizes_cmnk );
+int etir_binary_destroy( etir_binary_t handle );
+
+/* Unary (reference src/backend/Unary.h:98-157) through UnaryHip:
+ * `expr` is "abcd->dbca"; ktype COPY, ZERO or ADD. */
+int etir_unary_create( char const * expr, int64_t const * dim_sizes, int64_t num_dim_sizes,
+                       int32_t dtype, int32_t ktype, etir_unary_t * handle );
+int etir_unary_eval( etir_unary_t handle, void const * in, void * out );
+int etir_unary_destroy( etir_unary_t handle );
+
+/* EinsumExpression (reference src/frontend/EinsumExpression.h:148-201):
+ * `expr` with n inputs, `path` the 2*(n-1) ids of opt_einsum's standard
+ * contraction path, data_ptrs the n inputs followed by the output.
+ * stream: hipStream_t as void* (NULL = null stream). */
+int etir_expression_create( char const        * expr,
+                            int64_t const     * dim_sizes,
+                            int64_t             num_dim_sizes,
+                            int64_t const     * path,
+                            int64_t             path_len,
+                            int32_t             dtype,
+                            void * const      * data_ptrs,
+                            void              * stream,
+                            etir_expression_t * handle );
+/* EinsumExpression::eval: enqueues the tree and waits for it. */
+int etir_expression_eval( etir_expression_t handle );
+/* Enqueues the tree on the stream without waiting. */
+int etir_expression_eval_async( etir_expression_t handle );
+int64_t etir_expression_num_ops( etir_expression_t handle );
+/* EinsumExpression::store_and_lock_data / unlock_data for input tensor `tensor_id`. */
+int etir_expression_store_and_lock_data( etir_expression_t handle, int64_t tensor_id );
+int etir_expression_unlock_data( etir_expression_t handle, int64_t tensor_id );
+/* Bytes of the device arena planned for the intermediates. */
+int64_t etir_expression_arena_bytes( etir_expression_t handle );
+int etir_expression_destroy( etir_expression_t handle );
+
+/* EinsumTree (reference src/frontend/EinsumTree.h:46-60) from the bracketed
+ * tree format of bench_tree; `data_ptrs` holds one pointer per node in
+ * post-order (leaves' inputs, NULL for intermediates, the root's output). */
+int64_t etir_tree_count_nodes( char const * tree );
+int etir_tree_create( char const * tree, char const * dim_sizes, int32_t dtype,
+                      void * const * data_ptrs, void * stream, etir_tree_t * handle );
+int etir_tree_eval( etir_tree_t handle );
+int64_t etir_tree_num_ops( etir_tree_t handle );
+int etir_tree_destroy( etir_tree_t handle );
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

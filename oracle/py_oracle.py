@@ -122,3 +122,51 @@ def bf16_to_f32(b):
     out = np.empty(b.shape, dtype=np.float32)
     lib().oracle_bf16_to_f32(b.ctypes.data, out.ctypes.data, b.size)
     return out
+
+
+def _names_sorted(names):
+    def key(n):
+        try:
+            return (0, int(n), "")
+        except ValueError:
+            return (1, 0, n)
+    return sorted(names, key=key)
+
+
+def contract_path(expr, sizes, path, arrays, dtype=FP64):
+    """Einsum expression evaluated pairwise along a contraction path
+    (opt_einsum standard form) with oracle_contract for every step; each
+    intermediate keeps the dims still needed later in ascending name order,
+    as EinsumExpression::substring_out does (reference
+    src/frontend/EinsumExpression.cpp:25-70).  Returns the output as float64.
+
+    arrays: flat numpy arrays of the inputs in their expression layouts."""
+    lhs, out = expr.replace(" ", "").split("->")
+    live = [(list(t), np.ascontiguousarray(a, dtype=np.float64)) for t, a in zip(lhs.split(","), arrays)]
+
+    def strides_of(dims):
+        st, acc = {}, 1
+        for d in reversed(dims):
+            st[d] = acc if sizes[d] >= 2 else 0
+            acc *= sizes[d]
+        return st
+
+    for step, (i, j) in enumerate(path):
+        (dl, al), (dr, ar) = live[i], live[j]
+        rest = [d for k, (t, _) in enumerate(live) if k not in (i, j) for d in t] + list(out)
+        last = step == len(path) - 1
+        res = list(out) if last else _names_sorted(set(d for d in dl + dr if d in rest))
+        sl, sr, so = strides_of(dl), strides_of(dr), strides_of(res)
+        alld = list(dict.fromkeys(res + dl + dr))
+        types = []
+        for d in alld:
+            in_l, in_r, in_o = d in dl, d in dr, d in res
+            types.append(0 if (in_l and in_r and in_o) else 1 if (in_l and in_o) else
+                         2 if (in_r and in_o) else 3 if (in_l and in_r) else 5 if in_l else 6)
+        loops = dict(dim_types=types, sizes=[sizes[d] for d in alld],
+                     strides_left=[sl.get(d, 0) for d in alld], strides_right=[sr.get(d, 0) for d in alld],
+                     strides_out=[so.get(d, 0) for d in alld])
+        o = np.zeros(int(np.prod([sizes[d] for d in res])) if res else 1, dtype=np.float64)
+        contract(loops, al, ar, o, dtype_left=FP64, dtype_right=FP64, dtype_out=FP64)
+        live = [t for k, t in enumerate(live) if k not in (i, j)] + [(res, o)]
+    return live[0][1]

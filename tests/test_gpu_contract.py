@@ -193,3 +193,26 @@ def test_missing_aux_is_an_error(torch_cuda):
         plan.execute(t, t, t)
     assert e.value.code == eir.NO_DATA_PTR_PROVIDED
     plan.close()
+
+
+# every tile configuration on layouts that exercise all load modes, ragged edges
+# and the affine / table K paths (ETIR_TILE overrides the planner's tile choice)
+TILES_F32 = [0, 1]
+TILES_BF16 = [2, 6, 3, 4]
+TILE_SHAPES = [
+    ("zakm,zbkn->zabmn", dict(z=2, a=3, m=64, b=2, n=64, k=96)),   # vec_mn x vec_mn, affine K
+    ("mk,nk->mn", dict(m=300, k=72, n=260)),                       # vec_k x vec_k, ragged
+    ("km,nk->nm", dict(k=40, m=136, n=200)),                       # vec_mn x vec_k
+    ("akbl,cldk->abcd", dict(a=5, b=7, c=6, d=9, k=12, l=8)),      # table K, scalar loads
+]
+
+
+@pytest.mark.parametrize("tile", TILES_F32 + TILES_BF16)
+@pytest.mark.parametrize("expr,sizes", TILE_SHAPES)
+def test_every_tile(torch_cuda, oracle, monkeypatch, tile, expr, sizes):
+    monkeypatch.setenv("ETIR_TILE", str(tile))
+    dtype = eir.FP32 if tile in TILES_F32 else eir.BF16
+    _, desc = run_case(torch_cuda, oracle, expr, sizes, dtype=dtype, seed=tile * 7 + len(expr))
+    names = {0: "f32_128x128", 1: "f32_64x64", 2: "bf16_256x256", 6: "bf16_256x128",
+             3: "bf16_128x128", 4: "bf16_64x64"}
+    assert names[tile] in desc

@@ -216,3 +216,15 @@ def test_blocked_baseline_matches_exact(oracle, expr, sizes, first, last):
     oracle.contract(loops, a, b, o1, aux=x, first_touch=first, last_touch=last)
     oracle.contract_blocked(loops, a, b, o2, aux=x, first_touch=first, last_touch=last, num_threads=2)
     assert rel_frobenius(o1, o2) < 1e-6
+
+
+def test_contract_path_matches_numpy(oracle):
+    # the tree oracle along a path equals numpy.einsum in float64
+    expr = "da,dce,bec->abc"
+    sizes = dict(a=3, b=4, c=5, d=2, e=3)
+    rng = np.random.default_rng(11)
+    ins = expr.split("->")[0].split(",")
+    arrs = [rng.uniform(-1, 1, tensor_numel(t, sizes)) for t in ins]
+    got = oracle.contract_path(expr, sizes, [(1, 2), (0, 1)], arrs)
+    ref = np.einsum(expr, *[a.reshape([sizes[d] for d in t]) for a, t in zip(arrs, ins)])
+    np.testing.assert_allclose(got, ref.ravel(), rtol=1e-12, atol=1e-12)
