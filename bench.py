@@ -40,7 +40,9 @@ def parse_args():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", default="", help="comma list of configs to run (c1,c2,c3,c4)")
+    p.add_argument("--only", default="", help="comma list of configs to run (c1,c2,c3,c4,c5)")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="also time a plain 512 MiB device copy (reference for the PMC byte counters)")
     return p.parse_args()
 
 
@@ -129,33 +131,40 @@ def bench_c1(torch, eir, stream, steps, warmup):
 
 
 def bench_c4(torch, eir, stream, steps, warmup):
-    """4-layer MLP tree bi,ih,hj,jk,ko->bo along the left-to-right path; every
-    node is one contraction with its output kept in HBM (the tree's node order
-    after the reference's swap_inputs: left = weight, right = activation)."""
+    """the 4-layer MLP tree bi,ih,hj,jk,ko->bo through
+    EinsumExpression (left-to-right path, intermediates in the HBM arena, all
+    nodes on one stream)."""
+    from einsum_ir_amd import host
     b, w = 4096, 2048
     g = torch.Generator(device="cuda").manual_seed(4)
     x = torch.randn(b * w, device="cuda", generator=g)
     ws = [torch.randn(w * w, device="cuda", generator=g) / (w ** 0.5) for _ in range(4)]
-    acts = [torch.empty(b * w, device="cuda") for _ in range(4)]
-    names = ["i", "h", "j", "k", "o"]
-    plans = []
-    for layer in range(4):
-        p_in, p_out = names[layer], names[layer + 1]
-        expr = f"{p_in}{p_out},b{p_in}->b{p_out}"
-        loops = eir.binary_loops(expr, {"b": b, p_in: w, p_out: w})
-        plans.append(eir.ContractionPlan(loops["dim_types"], loops["sizes"], loops["strides_left"],
-                                         loops["strides_right"], loops["strides_out"]))
-    flops = sum(p.flops for p in plans)
+    out = torch.empty(b * w, device="cuda")
+    sizes = dict(b=b, i=w, h=w, j=w, k=w, o=w)
+    e = host.Expression("bi,ih,hj,jk,ko->bo", sizes, [(0, 1), (0, 3), (0, 2), (0, 1)], [x] + ws + [out],
+                        stream=stream)
+    flops = 4 * 2 * b * w * w
+    wall, per_eval = time_launches(torch, stream, e.eval_async, steps, warmup)
+    res = dict(flops=flops, wall=wall, per_launch=per_eval, num_ops=e.num_ops(), arena=e.arena_bytes())
+    e.close()
+    return res
 
-    def fn():
-        cur = x
-        for layer in range(4):
-            plans[layer].execute(ws[layer], cur, acts[layer], stream=stream)
-            cur = acts[layer]
-    wall, per_step = time_launches(torch, stream, fn, steps, warmup)
-    res = dict(flops=flops, wall=wall, per_launch=per_step, desc=plans[0].describe())
-    for p in plans:
-        p.close()
+
+def bench_c5(torch, eir, stream, steps, warmup):
+    """the committed random tensor network (~50 GFLOP) through
+    EinsumExpression along its greedy path."""
+    from einsum_ir_amd import host
+    fx = json.load(open(os.path.join(ROOT, "tests", "golden", "c5_network.json")))
+    expr, sizes, path = fx["expr"], fx["sizes"], [tuple(p) for p in fx["path"]]
+    ins, out = expr.split("->")
+    g = torch.Generator(device="cuda").manual_seed(5)
+    numel = lambda t: int(__import__("math").prod(sizes[d] for d in t))
+    tensors = [torch.rand(numel(t), device="cuda", generator=g) * 2 - 1 for t in ins.split(",")]
+    tensors.append(torch.empty(numel(out), device="cuda"))
+    e = host.Expression(expr, sizes, path, tensors, stream=stream)
+    wall, per_eval = time_launches(torch, stream, e.eval_async, steps, warmup)
+    res = dict(flops=fx["flops"], wall=wall, per_launch=per_eval, num_ops=e.num_ops())
+    e.close()
     return res
 
 
@@ -202,6 +211,15 @@ def main():
 
     extra = {}
     c3 = None
+    if args.calibrate_copy:
+        n = 128 * 2 ** 20   # 512 MiB of fp32
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty_like(src)
+        wall, per = time_launches(torch, stream, lambda: dst.copy_(src), 5, 2)
+        extra["copy_512MiB"] = dict(value=round(2 * 4 * n / per * 1e-9, 1), unit="GB/s",
+                                    us_per_launch=round(per * 1e6, 2), bytes_per_launch=2 * 4 * n)
+        log(f"copy: {per*1e6:.1f} us, {2 * 4 * n / per * 1e-9:.0f} GB/s")
+        del src, dst
     if run("c3"):
         c3 = bench_c3(torch, eir, stream, args.steps, args.warmup)
         log(f"c3: {c3['desc']}  {c3['per_launch']*1e6:.1f} us/launch")
@@ -226,8 +244,18 @@ def main():
         extra["c4_mlp_tree_fp32"] = dict(value=round(gf, 1), unit="GFLOP/s",
                                          ms_per_eval=round(c4["per_launch"] * 1e3, 3),
                                          frac_fp32_peak=round(gf / (PEAK_FP32_TFLOPS * 1e3), 4),
-                                         kernel=c4["desc"])
+                                         path="EinsumExpression (4 contraction nodes, HBM arena "
+                                              f"{c4['arena'] / 2**20:.0f} MiB)")
         log(f"c4: {c4['per_launch']*1e3:.3f} ms/eval")
+    if run("c5"):
+        c5 = bench_c5(torch, eir, stream, max(5, args.steps // 5), min(args.warmup, 2))
+        gf = c5["flops"] / c5["per_launch"] * 1e-9
+        extra["c5_tensor_network_fp32"] = dict(value=round(gf, 1), unit="GFLOP/s",
+                                               ms_per_eval=round(c5["per_launch"] * 1e3, 3),
+                                               frac_fp32_peak=round(gf / (PEAK_FP32_TFLOPS * 1e3), 4),
+                                               flops_per_eval=c5["flops"],
+                                               path="EinsumExpression, tests/golden/c5_network.json")
+        log(f"c5: {c5['per_launch']*1e3:.3f} ms/eval")
 
     cpu = None
     if not args.no_cpu_baseline and run("c3"):
