@@ -1,0 +1,30 @@
+// Instantiations of the direct-to-LDS bf16 contraction kernel: 256 x 256
+// tiles, 4 waves, one per (A load mode, B load mode) in {VEC_MN, VEC_K}.
+#include "contract_dma.h"
+
+namespace etir {
+
+namespace {
+
+template< int MA, int MB, int BK, int STAGES >
+int launch_one( ContractArgs const & a, uint32_t grid, hipStream_t stream ) {
+  hipLaunchKernelGGL( ( kern::contract_dma_kernel< 256, 256, BK, 2, 2, MA, MB, STAGES > ),
+                      dim3( grid ), dim3( 256 ), 0, stream, a );
+  return ETIR_SUCCESS;
+}
+
+}  // namespace
+
+int launch_contract_bf16_dma( int32_t ma, int32_t mb, int32_t variant, ContractArgs const & a,
+                              uint32_t grid, hipStream_t stream ) {
+  if( ma == LOAD_VEC_MN && mb == LOAD_VEC_MN ) {
+    if( variant == 1 ) return launch_one< LOAD_VEC_MN, LOAD_VEC_MN, 32, 4 >( a, grid, stream );
+    return launch_one< LOAD_VEC_MN, LOAD_VEC_MN, 64, 2 >( a, grid, stream );
+  }
+  if( ma == LOAD_VEC_MN && mb == LOAD_VEC_K ) return launch_one< LOAD_VEC_MN, LOAD_VEC_K, 64, 2 >( a, grid, stream );
+  if( ma == LOAD_VEC_K && mb == LOAD_VEC_MN ) return launch_one< LOAD_VEC_K, LOAD_VEC_MN, 64, 2 >( a, grid, stream );
+  if( ma == LOAD_VEC_K && mb == LOAD_VEC_K )  return launch_one< LOAD_VEC_K, LOAD_VEC_K, 64, 2 >( a, grid, stream );
+  return fail( ETIR_COMPILATION_FAILED, "no direct-to-LDS bf16 kernel for this load-mode combination" );
+}
+
+}  // namespace etir

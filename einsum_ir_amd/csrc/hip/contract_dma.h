@@ -1,0 +1,394 @@
+// gfx950 bf16 contraction kernel with direct-to-LDS operand loads.
+//
+// Same contraction and epilogue as contract_kernel.h
+//   out[c][m][n] = touch( sum_k A[c][m][k] * B[c][n][k] )
+// (first/last-touch semantics of reference src/basic/binary/
+// ContractionBackendTpp.cpp:15-49,127-163, applied once per output element),
+// specialised for the large, compute-bound case:
+//
+// * bf16 operands, fp32 accumulation, v_mfma_f32_32x32x16_bf16;
+// * one workgroup of 4 waves per CU computes a BM x BN = 256 x 256 tile, each
+//   wave a 128 x 128 block (16 accumulator tiles of 32 x 32 = 256 registers),
+//   which keeps the LDS read traffic at (128 + 128) rows per wave and k;
+// * operands go global -> LDS with buffer_load_dwordx4 ... lds (no VGPR
+//   staging, no ds_write): one instruction moves 64 x 16 bytes into one
+//   contiguous KiB of LDS, lane i into bytes [16 i, 16 i + 16).  Each lane
+//   chooses WHICH 16 global bytes it fetches, which is how the XOR swizzle
+//   below is applied.  Out-of-range rows and k read as zero through the
+//   buffer's range check (offset >= num_records), so edge tiles need no
+//   branches;
+// * STAGES LDS buffers: the loads for k-step t + STAGES - 1 are issued at the
+//   start of step t, so a load has STAGES - 1 steps of MFMA work to land.
+//
+// Operand layouts in LDS (per stage), both read with conflict-free patterns:
+//
+// VEC_MN (16-byte runs along the operand's rows, e.g. M-contiguous A):
+//   [k][R] bf16, R*2 bytes per k row, 16-byte segment g of k row k stored at
+//   segment g ^ swz(k & 3), swz = {0, 6, 10, 12}.  MFMA fragments are read with
+//   ds_read_b64_tr_b16 (the LDS transpose read of gfx950); one such read
+//   touches 4 k rows x 64 bytes, which the swizzle spreads over disjoint bank
+//   ranges for 16-lane (128 B/clk) and 32-lane (256 B/clk) service groups.
+// VEC_K (16-byte runs along K, K-contiguous operand):
+//   [R][BK] bf16, segment g (8 k) of row r stored at g ^ swz(r),
+//   swz(r) = (r & 7) ^ ((r >> 3) & 1); fragments are ds_read_b128.
+#ifndef ETIR_CONTRACT_DMA_H
+#define ETIR_CONTRACT_DMA_H
+
+#include "contract_kernel.h"
+
+namespace etir {
+namespace kern {
+
+typedef int32_t i32x4 __attribute__( ( ext_vector_type( 4 ) ) );
+
+// buffer resource of a raw (stride 0) buffer: base address, num_records
+// bytes, gfx9 word-3 format bits for untyped dword access
+__device__ inline i32x4 make_rsrc( void const * base, uint32_t num_records ) {
+  uint64_t const l_b = reinterpret_cast< uint64_t >( base );
+  i32x4 l_r;
+  l_r[0] = int32_t( uint32_t( l_b ) );
+  l_r[1] = int32_t( uint32_t( l_b >> 32 ) & 0xffffu );
+  l_r[2] = int32_t( num_records );
+  l_r[3] = 0x00020000;
+  return l_r;
+}
+
+// 64 lanes x 16 bytes global -> LDS: lane i's bytes at buffer offset voff go
+// to LDS byte lds_addr + 16 i.  Written as inline assembly so that the
+// compiler neither tracks these loads (it would otherwise wait for all of
+// them before any LDS read, which defeats the prefetch) nor moves them across
+// the explicit waits and barriers of the main loop; M0 carries the LDS base
+// and is not used by anything else in these kernels.  gfx9 needs one wait
+// state between an SALU write of M0 and an LDS-DMA instruction reading it
+// (the compiler's hazard recognizer does not look inside inline assembly).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ inline void dma16( i32x4 rsrc, uint32_t voff, uint32_t lds_addr ) {
+  asm volatile( "s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                :: "v"( voff ), "s"( rsrc ), "s"( lds_addr ) : "m0" );
+}
+#pragma clang diagnostic pop
+
+// LDS byte address of a generic pointer into a __shared__ array
+__device__ inline uint32_t lds_addr( void const * p ) {
+  return uint32_t( reinterpret_cast< uintptr_t >( (__attribute__( ( address_space( 3 ) ) ) char const *) p ) );
+}
+
+// wait until at most N vector-memory operations of this wave are in flight
+template< int N >
+__device__ inline void wait_vmcnt() {
+  static_assert( N >= 0 && N < 64, "vmcnt out of range" );
+  if constexpr( N == 0 )      asm volatile( "s_waitcnt vmcnt(0)" ::: "memory" );
+  else if constexpr( N == 8 ) asm volatile( "s_waitcnt vmcnt(8)" ::: "memory" );
+  else if constexpr( N == 16 ) asm volatile( "s_waitcnt vmcnt(16)" ::: "memory" );
+  else if constexpr( N == 24 ) asm volatile( "s_waitcnt vmcnt(24)" ::: "memory" );
+  else if constexpr( N == 32 ) asm volatile( "s_waitcnt vmcnt(32)" ::: "memory" );
+  else if constexpr( N == 48 ) asm volatile( "s_waitcnt vmcnt(48)" ::: "memory" );
+  else static_assert( N == 0, "add the vmcnt value" );
+}
+
+// workgroup barrier that also orders LDS accesses around it (no waitcnt)
+__device__ inline void barrier_lds() {
+  asm volatile( "s_barrier" ::: "memory" );
+}
+
+__device__ inline void wait_lgkmcnt0() {
+  asm volatile( "s_waitcnt lgkmcnt(0)" ::: "memory" );
+}
+
+// byte offset used for lanes whose row or k is out of range: at or above the
+// buffer's num_records, so the load returns zeros
+constexpr uint32_t kDmaOob = 0x80000000u;
+
+__device__ inline uint32_t swz_mn( int k ) {
+  return ( 0xCA60u >> ( 4 * ( k & 3 ) ) ) & 0xFu;
+}
+
+__device__ inline uint32_t swz_k( int r ) {
+  return uint32_t( ( r & 7 ) ^ ( ( r >> 3 ) & 1 ) );
+}
+
+// ---------------------------------------------------------------------------
+// DMA loaders: precomputed per-lane byte offsets (row part + local k part);
+// the k-step part is added per issue.
+// ---------------------------------------------------------------------------
+template< int R, int BK, int W, int MODE >
+struct DmaLoader;
+
+template< int R, int BK, int W >
+struct DmaLoader< R, BK, W, LOAD_VEC_MN > {
+  static constexpr int SEGS  = R / 8;          // 16-byte segments per k row
+  static constexpr int KPC   = 64 / SEGS;      // k rows per KiB chunk
+  static constexpr int NCH   = BK / KPC;       // chunks per stage
+  static constexpr int NJ    = NCH / W;        // chunks per wave
+  static constexpr int STAGE_BYTES = BK * R * 2;
+  static_assert( SEGS >= 16 && SEGS <= 64 && 64 % SEGS == 0, "VEC_MN DMA: R must be 128..512" );
+  static_assert( NCH % W == 0, "VEC_MN DMA: chunks must divide over the waves" );
+
+  uint32_t m_off[NJ];
+  int32_t  m_kk[NJ];
+
+  __device__ inline void init( int32_t const * tab_rows, int32_t rows, int32_t row0, int32_t sk,
+                               int wave, int lane ) {
+#pragma unroll
+    for( int l_j = 0; l_j < NJ; l_j++ ) {
+      int const l_chunk = wave * NJ + l_j;
+      int const l_kk = l_chunk * KPC + lane / SEGS;
+      int const l_p  = lane % SEGS;
+      int const l_g  = l_p ^ int( swz_mn( l_kk ) );
+      int32_t const l_row = row0 + 8 * l_g;
+      m_kk[l_j] = l_kk;
+      m_off[l_j] = ( l_row < rows ) ? uint32_t( 2 * ( tab_rows[l_row] + l_kk * sk ) ) : kDmaOob;
+    }
+  }
+
+  // k0: first k of the step; kstep_bytes = 2 * k0 * sk.  Lanes whose k is at
+  // or past K (partial last step, prefetches beyond the last step) load zeros.
+  __device__ inline void issue( i32x4 rsrc, uint32_t lds_stage, int wave, int32_t k0,
+                                int32_t K, uint32_t kstep_bytes ) {
+#pragma unroll
+    for( int l_j = 0; l_j < NJ; l_j++ ) {
+      uint32_t l_off = m_off[l_j] + kstep_bytes;
+      if( k0 + m_kk[l_j] >= K ) l_off = kDmaOob;
+      dma16( rsrc, l_off, lds_stage + ( wave * NJ + l_j ) * 1024 );
+    }
+  }
+};
+
+template< int R, int BK, int W >
+struct DmaLoader< R, BK, W, LOAD_VEC_K > {
+  static constexpr int SEGS  = BK / 8;         // 16-byte segments per row
+  static constexpr int RPC   = 64 / SEGS;      // rows per KiB chunk
+  static constexpr int NCH   = R / RPC;
+  static constexpr int NJ    = NCH / W;
+  static constexpr int STAGE_BYTES = BK * R * 2;
+  static_assert( SEGS == 8, "VEC_K DMA: BK must be 64" );
+  static_assert( NCH % W == 0, "VEC_K DMA: chunks must divide over the waves" );
+
+  uint32_t m_off[NJ];
+  int32_t  m_kl[NJ];   // local k of this lane's segment in chunk j
+
+  __device__ inline void init( int32_t const * tab_rows, int32_t rows, int32_t row0, int32_t sk,
+                               int wave, int lane ) {
+    int const l_p = lane % SEGS;
+#pragma unroll
+    for( int l_j = 0; l_j < NJ; l_j++ ) {
+      int const l_r   = ( wave * NJ + l_j ) * RPC + lane / SEGS;
+      int const l_g   = l_p ^ int( swz_k( l_r ) );
+      int32_t const l_row = row0 + l_r;
+      m_off[l_j] = ( l_row < rows ) ? uint32_t( 2 * ( tab_rows[l_row] + 8 * l_g * sk ) ) : kDmaOob;
+      m_kl[l_j]  = 8 * l_g;
+    }
+  }
+
+  __device__ inline void issue( i32x4 rsrc, uint32_t lds_stage, int wave, int32_t k0,
+                                int32_t K, uint32_t kstep_bytes ) {
+#pragma unroll
+    for( int l_j = 0; l_j < NJ; l_j++ ) {
+      uint32_t const l_off = ( k0 + m_kl[l_j] < K ) ? m_off[l_j] + kstep_bytes : kDmaOob;
+      dma16( rsrc, l_off, lds_stage + ( wave * NJ + l_j ) * 1024 );
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// fragment readers: per-lane byte addresses for each 32-row block, k-substep
+// offsets are immediates
+// ---------------------------------------------------------------------------
+template< int R, int BK, int NB, int MODE >
+struct DmaFrag;
+
+template< int R, int BK, int NB >
+struct DmaFrag< R, BK, NB, LOAD_VEC_MN > {
+  typedef short v4i16 __attribute__( ( ext_vector_type( 4 ) ) );
+  typedef short v8i16 __attribute__( ( ext_vector_type( 8 ) ) );
+  typedef __attribute__( ( address_space( 3 ) ) ) v4i16 lds_v4i16;
+  uint32_t m_addr[NB];
+
+  // row0: first row of this wave's NB blocks of 32 rows
+  __device__ inline void init( int row0, int lane ) {
+    int const l_q  = lane >> 4;
+    int const l_L  = lane & 15;
+    int const l_kb = 8 * ( l_q >> 1 ) + ( l_L >> 2 );
+#pragma unroll
+    for( int l_i = 0; l_i < NB; l_i++ ) {
+      int const l_row = row0 + 32 * l_i + 16 * ( l_q & 1 ) + 4 * ( l_L & 3 );
+      m_addr[l_i] = uint32_t( l_kb * R * 2 ) + ( uint32_t( ( l_row >> 3 ) ^ int( swz_mn( l_kb ) ) ) << 4 )
+                  + uint32_t( ( l_row & 7 ) * 2 );
+    }
+  }
+
+  // fragment (8 consecutive k of one row per lane) of block i, k substep s
+  __device__ inline bf16x8 read( char const * lds_stage, int i, int s ) const {
+    char const * l_p0 = lds_stage + m_addr[i] + s * 16 * R * 2;
+    v4i16 l_lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16( (lds_v4i16 *) ( l_p0 ) );
+    v4i16 l_hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16( (lds_v4i16 *) ( l_p0 + 4 * R * 2 ) );
+    v8i16 l_all = __builtin_shufflevector( l_lo, l_hi, 0, 1, 2, 3, 4, 5, 6, 7 );
+    return __builtin_bit_cast( bf16x8, l_all );
+  }
+};
+
+template< int R, int BK, int NB >
+struct DmaFrag< R, BK, NB, LOAD_VEC_K > {
+  // [R][64] bf16, 128 bytes per row; lane: row = lane % 32, segment 2 s + lane / 32
+  uint32_t m_row_addr;
+  uint32_t m_seg[BK / 16];
+
+  __device__ inline void init( int row0, int lane ) {
+    int const l_r = row0 + ( lane & 31 );
+    m_row_addr = uint32_t( l_r * BK * 2 );
+#pragma unroll
+    for( int l_s = 0; l_s < BK / 16; l_s++ ) {
+      m_seg[l_s] = uint32_t( ( 2 * l_s + ( lane >> 5 ) ) ^ int( swz_k( l_r ) ) ) << 4;
+    }
+  }
+
+  __device__ inline bf16x8 read( char const * lds_stage, int i, int s ) const {
+    return *reinterpret_cast< bf16x8 const * >( lds_stage + m_row_addr + m_seg[s] + i * 32 * BK * 2 );
+  }
+};
+
+// ---------------------------------------------------------------------------
+// the kernel
+// ---------------------------------------------------------------------------
+template< int BM, int BN, int BK, int WM, int WN, int MA, int MB, int STAGES >
+__global__ __launch_bounds__( 64 * WM * WN, 1 )
+void contract_dma_kernel( ContractArgs a ) {
+  constexpr int W   = WM * WN;
+  constexpr int T   = 64 * W;
+  constexpr int TM  = BM / WM / 32;
+  constexpr int TN  = BN / WN / 32;
+  constexpr int SUB = BK / 16;
+  typedef DmaLoader< BM, BK, W, MA > LdA;
+  typedef DmaLoader< BN, BK, W, MB > LdB;
+  constexpr int SA  = LdA::STAGE_BYTES;
+  constexpr int SB  = LdB::STAGE_BYTES;
+  constexpr int NJW = LdA::NJ + LdB::NJ;     // DMA instructions per wave and stage
+  static_assert( STAGES >= 2, "at least double buffering" );
+  static_assert( ( STAGES - 2 ) * NJW < 64, "vmcnt range" );
+
+  __shared__ __attribute__( ( aligned( 1024 ) ) ) char l_lds[STAGES * ( SA + SB )];
+
+  // tile order: see contract_kernel (XCD-contiguous ranges, groups of 8 tile rows)
+  int32_t const l_ntiles = a.tiles_m * a.tiles_n;
+  int32_t const l_nblk   = gridDim.x;
+  int32_t l_bid = blockIdx.x;
+  if( ( l_nblk & 7 ) == 0 ) l_bid = ( l_bid & 7 ) * ( l_nblk >> 3 ) + ( l_bid >> 3 );
+  int32_t const l_c      = l_bid / l_ntiles;
+  int32_t const l_tile   = l_bid - l_c * l_ntiles;
+  constexpr int32_t kGroupM = 8;
+  int32_t const l_in_grp = kGroupM * a.tiles_n;
+  int32_t const l_grp    = l_tile / l_in_grp;
+  int32_t const l_fm     = l_grp * kGroupM;
+  int32_t const l_gsz    = min( a.tiles_m - l_fm, kGroupM );
+  int32_t const l_tm     = l_fm + ( l_tile - l_grp * l_in_grp ) % l_gsz;
+  int32_t const l_tn     = ( l_tile - l_grp * l_in_grp ) / l_gsz;
+  int32_t const l_m0     = l_tm * BM;
+  int32_t const l_n0     = l_tn * BN;
+
+  int const l_lane = threadIdx.x & 63;
+  int const l_wave = __builtin_amdgcn_readfirstlane( threadIdx.x >> 6 );
+  int const l_wm   = l_wave / WN;
+  int const l_wn   = l_wave - l_wm * WN;
+
+  uint16_t const * l_pa = reinterpret_cast< uint16_t const * >( a.a ) + a.tc_a[l_c];
+  uint16_t const * l_pb = reinterpret_cast< uint16_t const * >( a.b ) + a.tc_b[l_c];
+  i32x4 const l_ra = make_rsrc( l_pa, kDmaOob );
+  i32x4 const l_rb = make_rsrc( l_pb, kDmaOob );
+
+  LdA l_lda;
+  LdB l_ldb;
+  l_lda.init( a.tm_a, a.M, l_m0, a.sk_a, l_wave, l_lane );
+  l_ldb.init( a.tn_b, a.N, l_n0, a.sk_b, l_wave, l_lane );
+
+  DmaFrag< BM, BK, TM, MA > l_fra;
+  DmaFrag< BN, BK, TN, MB > l_frb;
+  l_fra.init( l_wm * TM * 32, l_lane );
+  l_frb.init( l_wn * TN * 32, l_lane );
+
+  f32x16 l_acc[TM][TN];
+#pragma unroll
+  for( int l_i = 0; l_i < TM; l_i++ )
+#pragma unroll
+    for( int l_j = 0; l_j < TN; l_j++ )
+      l_acc[l_i][l_j] = f32x16( 0.0f );
+
+  int32_t const l_K  = a.K;
+  int32_t const l_nk = ( l_K + BK - 1 ) / BK;
+  uint32_t const l_kb_a = uint32_t( 2 * BK * a.sk_a );   // bytes per k step
+  uint32_t const l_kb_b = uint32_t( 2 * BK * a.sk_b );
+  uint32_t const l_lds0 = lds_addr( l_lds );
+
+  if( l_nk > 0 ) {
+    // prologue: steps 0 .. STAGES-2 (steps >= nk load zeros)
+#pragma unroll
+    for( int l_t = 0; l_t < STAGES - 1; l_t++ ) {
+      uint32_t const l_st = l_lds0 + uint32_t( l_t ) * ( SA + SB );
+      l_lda.issue( l_ra, l_st, l_wave, l_t * BK, l_K, uint32_t( l_t ) * l_kb_a );
+      l_ldb.issue( l_rb, l_st + SA, l_wave, l_t * BK, l_K, uint32_t( l_t ) * l_kb_b );
+    }
+    wait_vmcnt< ( STAGES - 2 ) * NJW >();
+    barrier_lds();
+
+    bf16x8 l_fa[2][TM];
+    bf16x8 l_fb[2][TN];
+#pragma unroll
+    for( int l_i = 0; l_i < TM; l_i++ ) l_fa[0][l_i] = l_fra.read( l_lds, l_i, 0 );
+#pragma unroll
+    for( int l_j = 0; l_j < TN; l_j++ ) l_fb[0][l_j] = l_frb.read( l_lds + SA, l_j, 0 );
+
+    for( int32_t l_t = 0; l_t < l_nk; l_t++ ) {
+      // loads for step t + STAGES - 1 go into the buffer of step t - 1, which
+      // every wave finished reading before the barrier that ended step t - 1
+      {
+        int32_t const l_tl = l_t + STAGES - 1;
+        uint32_t const l_st = l_lds0 + uint32_t( l_tl % STAGES ) * ( SA + SB );
+        l_lda.issue( l_ra, l_st, l_wave, l_tl * BK, l_K, uint32_t( l_tl ) * l_kb_a );
+        l_ldb.issue( l_rb, l_st + SA, l_wave, l_tl * BK, l_K, uint32_t( l_tl ) * l_kb_b );
+      }
+      char const * l_sa = l_lds + ( l_t % STAGES ) * ( SA + SB );
+      char const * l_sb = l_sa + SA;
+#pragma unroll
+      for( int l_s = 0; l_s < SUB; l_s++ ) {
+        int const l_cur = l_s & 1;
+        int const l_nxt = l_cur ^ 1;
+        if( l_s + 1 < SUB ) {
+#pragma unroll
+          for( int l_i = 0; l_i < TM; l_i++ ) l_fa[l_nxt][l_i] = l_fra.read( l_sa, l_i, l_s + 1 );
+#pragma unroll
+          for( int l_j = 0; l_j < TN; l_j++ ) l_fb[l_nxt][l_j] = l_frb.read( l_sb, l_j, l_s + 1 );
+        }
+        else if( l_t + 1 < l_nk ) {
+          // step t + 1 must have landed (own loads: vmcnt; everyone's: barrier)
+          wait_vmcnt< ( STAGES - 2 ) * NJW >();
+          wait_lgkmcnt0();                    // this step's LDS reads are done
+          barrier_lds();
+          char const * l_na = l_lds + ( ( l_t + 1 ) % STAGES ) * ( SA + SB );
+#pragma unroll
+          for( int l_i = 0; l_i < TM; l_i++ ) l_fa[l_nxt][l_i] = l_fra.read( l_na, l_i, 0 );
+#pragma unroll
+          for( int l_j = 0; l_j < TN; l_j++ ) l_fb[l_nxt][l_j] = l_frb.read( l_na + SA, l_j, 0 );
+        }
+#pragma unroll
+        for( int l_i = 0; l_i < TM; l_i++ )
+#pragma unroll
+          for( int l_j = 0; l_j < TN; l_j++ )
+            l_acc[l_i][l_j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16( l_fa[l_cur][l_i], l_fb[l_cur][l_j],
+                                                                       l_acc[l_i][l_j], 0, 0, 0 );
+      }
+    }
+    // the trailing (zero) loads still target LDS: drain them before the
+    // epilogue reuses it
+    wait_vmcnt< 0 >();
+    barrier_lds();
+  }
+
+  static_assert( EpilogueLds< BM, BN, WM, WN, TM, TN >::BYTES <= int( sizeof( l_lds ) ),
+                 "LDS too small for the epilogue" );
+  epilogue< BM, BN, WM, WN, TM, TN, T >( a, l_acc, l_lds, l_c, l_m0, l_n0, l_wm, l_wn, l_lane );
+}
+
+}  // namespace kern
+}  // namespace etir
+
+#endif

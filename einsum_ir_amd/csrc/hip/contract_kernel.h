@@ -34,6 +34,7 @@
 
 #include "etir_internal.h"
 #include <type_traits>
+#include <utility>
 
 namespace etir {
 namespace kern {
@@ -334,6 +335,183 @@ struct LdsSize {
 };
 
 // ---------------------------------------------------------------------------
+// epilogue: first/last-touch kernels and the output store of one tile.
+// The tile's output (and aux) row/column offsets are staged in LDS first
+// (s_tabs, 2*(BM+BN) int32): table reads from global memory between the
+// stores would make every store wait for all earlier ones (one vector-memory
+// counter on gfx9).  Accumulator layout of v_mfma_f32_32x32x*: register r of
+// lane l holds row = 8*(r/4) + 4*(l/32) + r%4, column = l%32.
+// ---------------------------------------------------------------------------
+// compile-time loop: f( std::integral_constant< int, 0 .. N-1 > ); keeps
+// register-array indices static where #pragma unroll alone may give up
+template< typename F, int... Is >
+__device__ __attribute__( ( always_inline ) ) inline void static_for_impl( F && f,
+                                                                          std::integer_sequence< int, Is... > ) {
+  ( f( std::integral_constant< int, Is >{} ), ... );
+}
+template< int N, typename F >
+__device__ __attribute__( ( always_inline ) ) inline void static_for( F && f ) {
+  static_for_impl( f, std::make_integer_sequence< int, N >{} );
+}
+
+// a pointer whose value is the same in every lane, moved to scalar registers
+// (buffer resources must be wave-uniform; the compiler cannot always prove it)
+template< typename P >
+__device__ __attribute__( ( always_inline ) ) inline P * uniform_ptr( P * p ) {
+  uint64_t const l_v = reinterpret_cast< uint64_t >( p );
+  uint32_t const l_lo = __builtin_amdgcn_readfirstlane( uint32_t( l_v ) );
+  uint32_t const l_hi = __builtin_amdgcn_readfirstlane( uint32_t( l_v >> 32 ) );
+  return reinterpret_cast< P * >( ( uint64_t( l_hi ) << 32 ) | l_lo );
+}
+
+// Epilogue of one tile: first/last-touch kernels and the output store.
+//
+// The tile's output (and aux) row/column offsets are staged in LDS first
+// (2*(BM+BN) int32 at the start of `lds`): table reads from global memory
+// between the stores would make every store wait for all earlier ones (one
+// vector-memory counter on gfx9).  Accumulator layout of v_mfma_f32_32x32x*:
+// register r of lane l holds row = 8*(r/4) + 4*(l/32) + r%4, column = l%32.
+//
+// Fast path -- a full tile, fp32 output, first touch ZERO, last touch none
+// or RELU, output byte offsets below 2^32: no bounds checks, the four row
+// offsets r%4 = 0..3 of one accumulator group come from one ds_read_b128,
+// and every value is one buffer_store_dword with a 32-bit byte offset from a
+// per-tile base in scalar registers.  When the output's column index is
+// unit-stride each store writes two 128-byte runs (lanes 0-31 and 32-63).
+//
+// General path -- edge tiles, auxiliary tensors, accumulation into the
+// output, bf16 output: each wave stages one 32-row slab of its accumulators in
+// its own LDS area and walks it in a rolled loop, consecutive lanes on
+// consecutive columns.
+template< int BM, int BN, int WM, int WN, int TM, int TN >
+struct EpilogueLds {
+  static constexpr int TABS  = 2 * ( BM + BN ) * 4;              // bytes of staged tables
+  static constexpr int WCOLS = TN * 32;                          // columns of one wave
+  static constexpr int PITCH = WCOLS + 4;                        // floats per slab row
+  static constexpr int SLAB  = 32 * PITCH * 4;                   // bytes per wave
+  static constexpr int BYTES = TABS + WM * WN * SLAB;
+};
+
+template< int TM, int TN, bool RELU >
+__device__ __attribute__( ( always_inline ) ) inline void epilogue_fast_f32(
+    float * l_base, f32x16 const ( &l_acc )[TM][TN], int32_t const * l_s_m_out,
+    int32_t const * l_s_n_out, int l_row0, int l_col0, int l_lane ) {
+  int const l_lr = l_lane & 31;
+  int const l_lg = l_lane >> 5;
+  __amdgpu_buffer_rsrc_t const l_rs = __builtin_amdgcn_make_buffer_rsrc( uniform_ptr( l_base ), (short) 0,
+                                                                         (int) 0xffffffff, 0x00020000 );
+  uint32_t l_noff[TN];
+#pragma unroll
+  for( int l_j = 0; l_j < TN; l_j++ ) l_noff[l_j] = uint32_t( l_s_n_out[l_col0 + l_j * 32 + l_lr] ) * 4u;
+  static_for< TM >( [&]( auto ic ) __attribute__( ( always_inline ) ) {
+    constexpr int l_i = decltype( ic )::value;
+    static_for< 4 >( [&]( auto gc ) __attribute__( ( always_inline ) ) {
+      constexpr int l_g = decltype( gc )::value;
+      typedef int32_t i32x4v __attribute__( ( ext_vector_type( 4 ) ) );
+      i32x4v const l_m4 = *reinterpret_cast< i32x4v const * >( l_s_m_out + l_row0 + l_i * 32 + 8 * l_g + 4 * l_lg );
+      static_for< TN >( [&]( auto jc ) __attribute__( ( always_inline ) ) {
+        constexpr int l_j = decltype( jc )::value;
+        static_for< 4 >( [&]( auto ec ) __attribute__( ( always_inline ) ) {
+          constexpr int l_e = decltype( ec )::value;
+          float l_v = l_acc[l_i][l_j][4 * l_g + l_e];
+          if constexpr( RELU ) l_v = fmaxf( l_v, 0.0f );
+          __builtin_amdgcn_raw_buffer_store_b32( __builtin_bit_cast( uint32_t, l_v ), l_rs,
+                                                 uint32_t( l_m4[l_e] ) * 4u + l_noff[l_j], 0, 0 );
+        } );
+      } );
+    } );
+  } );
+}
+
+template< int BM, int BN, int WM, int WN, int TM, int TN, int T >
+__device__ __attribute__( ( always_inline ) ) inline void epilogue( ContractArgs const & a,
+                                                                    f32x16 const ( &l_acc )[TM][TN],
+                                                                    char * lds, int32_t l_c, int32_t l_m0,
+                                                                    int32_t l_n0, int l_wm, int l_wn,
+                                                                    int l_lane ) {
+  typedef EpilogueLds< BM, BN, WM, WN, TM, TN > L;
+  int32_t * l_s_m_out = reinterpret_cast< int32_t * >( lds );
+  int32_t * l_s_m_aux = l_s_m_out + BM;
+  int32_t * l_s_n_out = l_s_m_aux + BM;
+  int32_t * l_s_n_aux = l_s_n_out + BN;
+  bool const l_has_aux = ( a.aux != nullptr );
+  for( int l_x = threadIdx.x; l_x < BM; l_x += T ) {
+    int32_t const l_m = l_m0 + l_x;
+    l_s_m_out[l_x] = ( l_m < a.M ) ? a.tm_out[l_m] : 0;
+    l_s_m_aux[l_x] = ( l_has_aux && l_m < a.M ) ? a.tm_aux[l_m] : 0;
+  }
+  for( int l_x = threadIdx.x; l_x < BN; l_x += T ) {
+    int32_t const l_n = l_n0 + l_x;
+    l_s_n_out[l_x] = ( l_n < a.N ) ? a.tn_out[l_n] : 0;
+    l_s_n_aux[l_x] = ( l_has_aux && l_n < a.N ) ? a.tn_aux[l_n] : 0;
+  }
+  __syncthreads();
+
+  int64_t const l_coff_out = a.tc_out[l_c];
+  int const l_row0 = l_wm * TM * 32;      // first tile row of this wave
+  int const l_col0 = l_wn * TN * 32;
+  bool const l_full = ( l_m0 + BM <= a.M ) && ( l_n0 + BN <= a.N );
+  if(    l_full && a.out_off32 && !a.out_bf16 && a.first_touch == ETIR_KTYPE_ZERO
+      && ( a.last_touch == ETIR_KTYPE_UNDEFINED || a.last_touch == ETIR_KTYPE_RELU ) ) {
+    float * l_base = reinterpret_cast< float * >( a.out ) + l_coff_out;
+    if( a.last_touch == ETIR_KTYPE_RELU ) {
+      epilogue_fast_f32< TM, TN, true >( l_base, l_acc, l_s_m_out, l_s_n_out, l_row0, l_col0, l_lane );
+    }
+    else {
+      epilogue_fast_f32< TM, TN, false >( l_base, l_acc, l_s_m_out, l_s_n_out, l_row0, l_col0, l_lane );
+    }
+    return;
+  }
+
+  int64_t const l_coff_aux = l_has_aux ? a.tc_aux[l_c] : 0;
+  float const * l_aux_f = reinterpret_cast< float const * >( a.aux ) + l_coff_aux;
+  uint16_t const * l_aux_h = reinterpret_cast< uint16_t const * >( a.aux ) + l_coff_aux;
+  float * l_out_f = reinterpret_cast< float * >( a.out ) + l_coff_out;
+  uint16_t * l_out_h = reinterpret_cast< uint16_t * >( a.out ) + l_coff_out;
+  bool const l_read_out = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_UNDEFINED );
+  bool const l_aux_first = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_COPY );
+  bool const l_need_aux = l_has_aux && ( l_aux_first || a.last_touch == ETIR_KTYPE_ADD );
+  int const l_lr = l_lane & 31;
+  int const l_lg = l_lane >> 5;
+  float * l_slab = reinterpret_cast< float * >( lds + L::TABS + ( l_wm * WN + l_wn ) * L::SLAB );
+
+#pragma unroll
+  for( int l_i = 0; l_i < TM; l_i++ ) {
+    // stage slab i (32 rows x WCOLS) of this wave; the previous slab's reads
+    // were issued earlier by this wave, and LDS executes one wave's accesses
+    // in order
+#pragma unroll
+    for( int l_j = 0; l_j < TN; l_j++ )
+#pragma unroll
+      for( int l_r = 0; l_r < 16; l_r++ )
+        l_slab[( 8 * ( l_r >> 2 ) + 4 * l_lg + ( l_r & 3 ) ) * L::PITCH + l_j * 32 + l_lr] = l_acc[l_i][l_j][l_r];
+    for( int l_e = l_lane; l_e < 32 * L::WCOLS; l_e += 64 ) {
+      int const l_row = l_e / L::WCOLS;
+      int const l_col = l_e - l_row * L::WCOLS;
+      int const l_ml = l_row0 + l_i * 32 + l_row;
+      int const l_nl = l_col0 + l_col;
+      if( l_m0 + l_ml >= a.M || l_n0 + l_nl >= a.N ) continue;
+      int64_t const l_off = int64_t( l_s_n_out[l_nl] ) + l_s_m_out[l_ml];
+      float l_v = l_slab[l_row * L::PITCH + l_col];
+      float l_aux = 0.0f;
+      if( l_need_aux ) {
+        int64_t const l_aoff = int64_t( l_s_n_aux[l_nl] ) + l_s_m_aux[l_ml];
+        l_aux = a.out_bf16 ? bf16_to_f32( l_aux_h[l_aoff] ) : l_aux_f[l_aoff];
+      }
+      if( l_read_out ) {
+        float const l_old = a.out_bf16 ? bf16_to_f32( l_out_h[l_off] ) : l_out_f[l_off];
+        l_v = l_old + l_v;
+      }
+      if( l_aux_first ) l_v = l_aux + l_v;
+      if( a.last_touch == ETIR_KTYPE_RELU ) l_v = fmaxf( l_v, 0.0f );
+      else if( a.last_touch == ETIR_KTYPE_ADD ) l_v = l_v + l_aux;
+      if( a.out_bf16 ) l_out_h[l_off] = f32_to_bf16_rne( l_v );
+      else             l_out_f[l_off] = l_v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // the kernel
 // ---------------------------------------------------------------------------
 template< int DT, int BM, int BN, int BK, int WM, int WN, int MA, int MB, bool KAFF, int WPE >
@@ -348,8 +526,14 @@ void contract_kernel( ContractArgs a ) {
   constexpr int SZB  = LdsSize< ESZ, MB, BN, BK >::value;
   static_assert( TM >= 1 && TN >= 1, "wave tile must hold at least one 32x32 block" );
 
-  __shared__ __attribute__( ( aligned( 16 ) ) ) TE l_lds_a[2][SZA];
-  __shared__ __attribute__( ( aligned( 16 ) ) ) TE l_lds_b[2][SZB];
+  // one allocation: double-buffered A and B tiles, reused by the epilogue
+  constexpr int LDS_MAIN  = 2 * ( SZA + SZB ) * ESZ;
+  constexpr int LDS_EPI   = EpilogueLds< BM, BN, WM, WN, TM, TN >::BYTES;
+  constexpr int LDS_BYTES = LDS_MAIN > LDS_EPI ? LDS_MAIN : LDS_EPI;
+  static_assert( ( 2 * SZA * ESZ ) % 16 == 0, "B tile must stay 16-byte aligned" );
+  __shared__ __attribute__( ( aligned( 16 ) ) ) char l_lds_raw[LDS_BYTES];
+  TE ( *l_lds_a )[SZA] = reinterpret_cast< TE ( * )[SZA] >( l_lds_raw );
+  TE ( *l_lds_b )[SZB] = reinterpret_cast< TE ( * )[SZB] >( l_lds_raw + 2 * SZA * ESZ );
 
   // XCD-aware order: consecutive workgroup ids are dispatched round-robin over
   // the 8 XCDs; remap so that each XCD works on one contiguous range of tiles
@@ -466,76 +650,8 @@ void contract_kernel( ContractArgs a ) {
   }
 
   // ---------------------------------------------------------------- epilogue
-  // The tile's output (and aux) row/column offsets are staged in LDS first:
-  // table reads from global memory between the stores would make every store
-  // wait for all earlier ones (one vector-memory counter on gfx9).
-  // 32x32 accumulator layout: register r of lane l holds
-  //   row = 8*(r/4) + 4*(l/32) + r%4,  column = l%32
-  static_assert( ( 2 * ( BM + BN ) ) * 4 <= ( SZA + SZB ) * ESZ * 2, "LDS too small for the epilogue tables" );
-  int32_t * l_s_m_out = reinterpret_cast< int32_t * >( &l_lds_a[0][0] );
-  int32_t * l_s_m_aux = l_s_m_out + BM;
-  int32_t * l_s_n_out = l_s_m_aux + BM;
-  int32_t * l_s_n_aux = l_s_n_out + BN;
-  bool const l_has_aux = ( a.aux != nullptr );
-  for( int l_x = threadIdx.x; l_x < BM; l_x += T ) {
-    int32_t const l_m = l_m0 + l_x;
-    l_s_m_out[l_x] = ( l_m < a.M ) ? a.tm_out[l_m] : 0;
-    l_s_m_aux[l_x] = ( l_has_aux && l_m < a.M ) ? a.tm_aux[l_m] : 0;
-  }
-  for( int l_x = threadIdx.x; l_x < BN; l_x += T ) {
-    int32_t const l_n = l_n0 + l_x;
-    l_s_n_out[l_x] = ( l_n < a.N ) ? a.tn_out[l_n] : 0;
-    l_s_n_aux[l_x] = ( l_has_aux && l_n < a.N ) ? a.tn_aux[l_n] : 0;
-  }
-  __syncthreads();
-
-  int const l_lg = l_lane >> 5;
-  int64_t const l_coff_out = a.tc_out[l_c];
-  int64_t const l_coff_aux = l_has_aux ? a.tc_aux[l_c] : 0;
-  float const * l_aux_f = reinterpret_cast< float const * >( a.aux ) + l_coff_aux;
-  uint16_t const * l_aux_h = reinterpret_cast< uint16_t const * >( a.aux ) + l_coff_aux;
-  float * l_out_f = reinterpret_cast< float * >( a.out ) + l_coff_out;
-  uint16_t * l_out_h = reinterpret_cast< uint16_t * >( a.out ) + l_coff_out;
-  bool const l_read_out = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_UNDEFINED );
-  bool const l_aux_first = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_COPY );
-  bool const l_need_aux = l_has_aux && ( l_aux_first || a.last_touch == ETIR_KTYPE_ADD );
-  bool const l_plain = !l_read_out && !l_need_aux && a.last_touch == ETIR_KTYPE_UNDEFINED && !a.out_bf16;
-
-#pragma unroll
-  for( int l_j = 0; l_j < TN; l_j++ ) {
-    int32_t const l_nl = ( l_wn * TN + l_j ) * 32 + l_lr;
-    bool const l_nok = ( l_n0 + l_nl ) < a.N;
-    int32_t const l_noff_out = l_s_n_out[l_nl];
-    int32_t const l_noff_aux = l_s_n_aux[l_nl];
-#pragma unroll
-    for( int l_i = 0; l_i < TM; l_i++ ) {
-#pragma unroll
-      for( int l_r = 0; l_r < 16; l_r++ ) {
-        int32_t const l_ml = ( l_wm * TM + l_i ) * 32 + 8 * ( l_r >> 2 ) + 4 * l_lg + ( l_r & 3 );
-        if( !l_nok || ( l_m0 + l_ml ) >= a.M ) continue;
-        int64_t const l_off = int64_t( l_noff_out ) + l_s_m_out[l_ml];
-        float l_v = l_acc[l_i][l_j][l_r];
-        if( l_plain ) {
-          l_out_f[l_off] = l_v;
-          continue;
-        }
-        float l_aux = 0.0f;
-        if( l_need_aux ) {
-          int64_t const l_aoff = int64_t( l_noff_aux ) + l_s_m_aux[l_ml];
-          l_aux = a.out_bf16 ? bf16_to_f32( l_aux_h[l_aoff] ) : l_aux_f[l_aoff];
-        }
-        if( l_read_out ) {
-          float const l_old = a.out_bf16 ? bf16_to_f32( l_out_h[l_off] ) : l_out_f[l_off];
-          l_v = l_old + l_v;
-        }
-        if( l_aux_first ) l_v = l_aux + l_v;
-        if( a.last_touch == ETIR_KTYPE_RELU ) l_v = fmaxf( l_v, 0.0f );
-        else if( a.last_touch == ETIR_KTYPE_ADD ) l_v = l_v + l_aux;
-        if( a.out_bf16 ) l_out_h[l_off] = f32_to_bf16_rne( l_v );
-        else             l_out_f[l_off] = l_v;
-      }
-    }
-  }
+  epilogue< BM, BN, WM, WN, TM, TN, T >( a, l_acc, l_lds_raw,
+                                         l_c, l_m0, l_n0, l_wm, l_wn, l_lane );
 }
 
 }  // namespace kern

@@ -44,6 +44,8 @@ int launch_contract_bf16_128x128( int32_t ma, int32_t mb, bool kaff, ContractArg
                                   uint32_t grid, hipStream_t stream );
 int launch_contract_bf16_64x64( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
                                 uint32_t grid, hipStream_t stream );
+int launch_contract_bf16_dma( int32_t ma, int32_t mb, int32_t variant, ContractArgs const & a,
+                              uint32_t grid, hipStream_t stream );
 
 namespace {
 
@@ -147,6 +149,7 @@ char const * tile_str( int32_t t ) {
     case TILE_F32_64x64:    return "f32_64x64x32";
     case TILE_BF16_256x256: return "bf16_256x256x64";
     case TILE_BF16_256x128: return "bf16_256x128x32";
+    case TILE_BF16_DMA_256x256: return "bf16_dma_256x256";
     case TILE_BF16_128x128: return "bf16_128x128x64";
     case TILE_BF16_64x64:   return "bf16_64x64x64";
     default:                return "?";
@@ -159,6 +162,7 @@ void tile_shape( int32_t t, int64_t & bm, int64_t & bn ) {
     case TILE_F32_64x64:    bm = 64;  bn = 64;  break;
     case TILE_BF16_256x256: bm = 256; bn = 256; break;
     case TILE_BF16_256x128: bm = 256; bn = 128; break;
+    case TILE_BF16_DMA_256x256: bm = 256; bn = 256; break;
     case TILE_BF16_128x128: bm = 128; bn = 128; break;
     default:                bm = 64;  bn = 64;  break;
   }
@@ -359,11 +363,35 @@ int plan_contraction( int64_t            num_loops,
     else if( n_tiles( TILE_BF16_128x128 ) >= l_cus ) plan.tile = TILE_BF16_128x128;
     else                                             plan.tile = TILE_BF16_64x64;
   }
+  // direct-to-LDS kernel: 16-byte vector modes on both operands, affine K,
+  // every byte offset below the buffer range (2^31), and enough 256 x 256
+  // tiles to give each CU at least one
+  auto max_of = []( std::vector< int64_t > const & t ) {
+    int64_t l_m = 0;
+    for( int64_t l_v : t ) l_m = std::max( l_m, l_v );
+    return l_m;
+  };
+  bool const l_dma_ok =
+         l_bf16
+      && ( plan.mode_a == LOAD_VEC_MN || plan.mode_a == LOAD_VEC_K )
+      && ( plan.mode_b == LOAD_VEC_MN || plan.mode_b == LOAD_VEC_K )
+      && l_k_affine
+      && 2 * ( max_of( l_tm_a ) + std::max< int64_t >( l_size_k - 1, 0 ) * l_sk_a ) + 64 < ( int64_t( 1 ) << 31 )
+      && 2 * ( max_of( l_tn_b ) + std::max< int64_t >( l_size_k - 1, 0 ) * l_sk_b ) + 64 < ( int64_t( 1 ) << 31 )
+      && 2 * int64_t( 64 ) * std::max( l_sk_a, l_sk_b ) * ( ( l_size_k + 63 ) / 64 + 4 ) < ( int64_t( 1 ) << 31 );
+  plan.tile_fallback = plan.tile;
+  if( l_dma_ok && n_tiles( TILE_BF16_DMA_256x256 ) >= l_cus ) plan.tile = TILE_BF16_DMA_256x256;
   if( char const * l_env = std::getenv( "ETIR_TILE" ) ) {
     // diagnostic override of the tile heuristic (must match the dtype)
     int32_t l_t = std::atoi( l_env );
     bool const l_t_f32 = ( l_t == TILE_F32_128x128 || l_t == TILE_F32_64x64 );
-    if( l_t >= 0 && l_t <= TILE_BF16_256x128 && l_t != TILE_F64_64x64 && l_t_f32 == l_f32 ) plan.tile = l_t;
+    bool const l_t_ok = ( l_t >= 0 && l_t <= TILE_BF16_DMA_256x256 && l_t != TILE_F64_64x64 && l_t_f32 == l_f32 )
+                     && ( l_t != TILE_BF16_DMA_256x256 || l_dma_ok );
+    if( l_t_ok ) plan.tile = l_t;
+  }
+  if( char const * l_env = std::getenv( "ETIR_DMA_VARIANT" ) ) {
+    // diagnostic: 1 selects BK 32 with 4 stages for VEC_MN x VEC_MN
+    plan.dma_variant = ( std::atoi( l_env ) == 1 && plan.mode_a == LOAD_VEC_MN && plan.mode_b == LOAD_VEC_MN ) ? 1 : 0;
   }
   int64_t l_bm, l_bn;
   tile_shape( plan.tile, l_bm, l_bn );
@@ -453,6 +481,12 @@ int plan_contraction( int64_t            num_loops,
   a.first_touch = ktype_first_touch;
   a.last_touch  = ktype_last_touch;
   a.out_bf16 = ( dtype_out == ETIR_BF16 ) ? 1 : 0;
+  {
+    int64_t l_mo = 0, l_no = 0;
+    for( int64_t l_v : l_tm_out ) l_mo = std::max( l_mo, l_v );
+    for( int64_t l_v : l_tn_out ) l_no = std::max( l_no, l_v );
+    a.out_off32 = ( 4 * ( l_mo + l_no ) + 4 < ( int64_t( 1 ) << 32 ) ) ? 1 : 0;
+  }
   return ETIR_SUCCESS;
 }
 
@@ -485,6 +519,16 @@ int launch_contraction( ContractionPlan const & plan,
   };
   if( uintptr_t( a.a ) % align_of( l_ma ) != 0 ) l_ma = LOAD_SCALAR;
   if( uintptr_t( a.b ) % align_of( l_mb ) != 0 ) l_mb = LOAD_SCALAR;
+  int32_t l_tile = plan.tile;
+  if( l_tile == TILE_BF16_DMA_256x256 && ( l_ma != plan.mode_a || l_mb != plan.mode_b ) ) {
+    // the DMA kernel needs the 16-byte vector modes: use the register-staged
+    // kernel with its own tile grid
+    l_tile = plan.tile_fallback;
+    int64_t l_bm, l_bn;
+    tile_shape( l_tile, l_bm, l_bn );
+    a.tiles_m = (int32_t) ( ( plan.M + l_bm - 1 ) / l_bm );
+    a.tiles_n = (int32_t) ( ( plan.N + l_bn - 1 ) / l_bn );
+  }
 
   int64_t const l_grid = int64_t( a.tiles_m ) * a.tiles_n * a.C;
   if( l_grid > 0x7fffffffLL ) {
@@ -493,13 +537,16 @@ int launch_contraction( ContractionPlan const & plan,
   bool const l_kaff = ( a.k_affine != 0 );
   uint32_t const l_g = (uint32_t) l_grid;
   int l_err;
-  switch( plan.tile ) {
+  switch( l_tile ) {
     case TILE_F32_128x128:  l_err = launch_contract_f32_128x128( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_F32_64x64:    l_err = launch_contract_f32_64x64( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_BF16_256x256: l_err = launch_contract_bf16_256x256( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_BF16_256x128: l_err = launch_contract_bf16_256x128( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_BF16_128x128: l_err = launch_contract_bf16_128x128( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_BF16_64x64:   l_err = launch_contract_bf16_64x64( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
+    case TILE_BF16_DMA_256x256:
+      l_err = launch_contract_bf16_dma( l_ma, l_mb, plan.dma_variant, a, l_g, stream );
+      break;
     default: return fail( ETIR_COMPILATION_FAILED, "contraction: unknown tile configuration" );
   }
   if( l_err != ETIR_SUCCESS ) return l_err;

@@ -109,7 +109,8 @@ enum TileCfg : int32_t {
   TILE_BF16_128x128 = 3,
   TILE_BF16_64x64  = 4,
   TILE_F64_64x64   = 5,
-  TILE_BF16_256x128 = 6
+  TILE_BF16_256x128 = 6,
+  TILE_BF16_DMA_256x256 = 7   // direct-to-LDS kernel (contract_dma.h)
 };
 
 struct ContractArgs {
@@ -140,6 +141,7 @@ struct ContractArgs {
   int32_t last_touch;     // ETIR_KTYPE_{RELU,ADD,UNDEFINED}
   int32_t k_full;         // K % BK == 0: no K masking needed
   int32_t out_bf16;       // output stored as bf16 (RNE)
+  int32_t out_off32;      // every output byte offset (M part + N part, C part excluded) is < 2^32
 };
 
 struct ContractionPlan {
@@ -154,6 +156,8 @@ struct ContractionPlan {
   int32_t mode_a = LOAD_SCALAR;
   int32_t mode_b = LOAD_SCALAR;
   int32_t tile = TILE_F32_128x128;
+  int32_t tile_fallback = TILE_BF16_256x128;  // used when the DMA kernel's alignment needs fail at launch
+  int32_t dma_variant = 0;                    // 0: BK 64, 2 stages; 1: BK 32, 4 stages (VEC_MN x VEC_MN)
   int64_t flops = 0;
   int64_t bytes = 0;
   // fused loops per kernel role (outer -> inner) for diagnostics
