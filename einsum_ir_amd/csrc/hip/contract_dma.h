@@ -144,14 +144,19 @@ struct DmaLoader< R, BK, W, LOAD_VEC_MN > {
 
   // k0: first k of the step; kstep_bytes = 2 * k0 * sk.  Lanes whose k is at
   // or past K (partial last step, prefetches beyond the last step) load zeros.
+  template< int J >
+  __device__ __attribute__( ( always_inline ) ) inline void issue_one( i32x4 rsrc, uint32_t lds_stage, int wave,
+                                                                       int32_t k0, int32_t K,
+                                                                       uint32_t kstep_bytes ) {
+    uint32_t l_off = m_off[J] + kstep_bytes;
+    if( k0 + m_kk[J] >= K ) l_off = kDmaOob;
+    dma16( rsrc, l_off, lds_stage + ( wave * NJ + J ) * 1024 );
+  }
   __device__ inline void issue( i32x4 rsrc, uint32_t lds_stage, int wave, int32_t k0,
                                 int32_t K, uint32_t kstep_bytes ) {
-#pragma unroll
-    for( int l_j = 0; l_j < NJ; l_j++ ) {
-      uint32_t l_off = m_off[l_j] + kstep_bytes;
-      if( k0 + m_kk[l_j] >= K ) l_off = kDmaOob;
-      dma16( rsrc, l_off, lds_stage + ( wave * NJ + l_j ) * 1024 );
-    }
+    static_for< NJ >( [&]( auto jc ) __attribute__( ( always_inline ) ) {
+      issue_one< decltype( jc )::value >( rsrc, lds_stage, wave, k0, K, kstep_bytes );
+    } );
   }
 };
 
@@ -181,13 +186,18 @@ struct DmaLoader< R, BK, W, LOAD_VEC_K > {
     }
   }
 
+  template< int J >
+  __device__ __attribute__( ( always_inline ) ) inline void issue_one( i32x4 rsrc, uint32_t lds_stage, int wave,
+                                                                       int32_t k0, int32_t K,
+                                                                       uint32_t kstep_bytes ) {
+    uint32_t const l_off = ( k0 + m_kl[J] < K ) ? m_off[J] + kstep_bytes : kDmaOob;
+    dma16( rsrc, l_off, lds_stage + ( wave * NJ + J ) * 1024 );
+  }
   __device__ inline void issue( i32x4 rsrc, uint32_t lds_stage, int wave, int32_t k0,
                                 int32_t K, uint32_t kstep_bytes ) {
-#pragma unroll
-    for( int l_j = 0; l_j < NJ; l_j++ ) {
-      uint32_t const l_off = ( k0 + m_kl[l_j] < K ) ? m_off[l_j] + kstep_bytes : kDmaOob;
-      dma16( rsrc, l_off, lds_stage + ( wave * NJ + l_j ) * 1024 );
-    }
+    static_for< NJ >( [&]( auto jc ) __attribute__( ( always_inline ) ) {
+      issue_one< decltype( jc )::value >( rsrc, lds_stage, wave, k0, K, kstep_bytes );
+    } );
   }
 };
 
@@ -226,6 +236,19 @@ struct DmaFrag< R, BK, NB, LOAD_VEC_MN > {
     v8i16 l_all = __builtin_shufflevector( l_lo, l_hi, 0, 1, 2, 3, 4, 5, 6, 7 );
     return __builtin_bit_cast( bf16x8, l_all );
   }
+
+  // the same fragment as two separately issued reads (units 0 and 1)
+  static constexpr int UNITS = 2;
+  struct Part { v4i16 h[2]; };
+  template< int U >
+  __device__ __attribute__( ( always_inline ) ) inline void read_unit( char const * lds_stage, int i, int s,
+                                                                       Part & f ) const {
+    char const * l_p = lds_stage + m_addr[i] + s * 16 * R * 2 + U * 4 * R * 2;
+    f.h[U] = __builtin_amdgcn_ds_read_tr16_b64_v4i16( (lds_v4i16 *) l_p );
+  }
+  __device__ static __attribute__( ( always_inline ) ) inline bf16x8 value( Part const & f ) {
+    return __builtin_bit_cast( bf16x8, __builtin_shufflevector( f.h[0], f.h[1], 0, 1, 2, 3, 4, 5, 6, 7 ) );
+  }
 };
 
 template< int R, int BK, int NB >
@@ -246,7 +269,188 @@ struct DmaFrag< R, BK, NB, LOAD_VEC_K > {
   __device__ inline bf16x8 read( char const * lds_stage, int i, int s ) const {
     return *reinterpret_cast< bf16x8 const * >( lds_stage + m_row_addr + m_seg[s] + i * 32 * BK * 2 );
   }
+
+  static constexpr int UNITS = 1;
+  struct Part { bf16x8 v; };
+  template< int U >
+  __device__ __attribute__( ( always_inline ) ) inline void read_unit( char const * lds_stage, int i, int s,
+                                                                       Part & f ) const {
+    f.v = read( lds_stage, i, s );
+  }
+  __device__ static __attribute__( ( always_inline ) ) inline bf16x8 value( Part const & f ) { return f.v; }
 };
+
+// ---------------------------------------------------------------------------
+// compile-time schedule of one k substep (TM x TN MFMAs)
+//   reads: A0 (all units), B0, A1, B1, ...
+//   MFMAs: (i, j) ordered by the read position of their later operand, so
+//          each MFMA of the next substep finds its fragments long landed
+// ---------------------------------------------------------------------------
+template< int TM, int TN >
+struct MfmaOrder {
+  int i[TM * TN];
+  int j[TM * TN];
+  constexpr MfmaOrder() : i(), j() {
+    int l_p = 0;
+    int const l_kmax = 2 * ( TM > TN ? TM : TN );
+    for( int l_key = 0; l_key <= l_kmax; l_key++ )
+      for( int l_i = 0; l_i < TM; l_i++ )
+        for( int l_j = 0; l_j < TN; l_j++ ) {
+          int const l_k = ( 2 * l_i > 2 * l_j + 1 ) ? 2 * l_i : 2 * l_j + 1;
+          if( l_k == l_key ) { i[l_p] = l_i; j[l_p] = l_j; l_p++; }
+        }
+  }
+};
+
+template< int TM, int TN, int UA, int UB >
+struct ReadOrder {
+  static constexpr int U = TM * UA + TN * UB;
+  int isb[U];
+  int idx[U];
+  int unit[U];
+  constexpr ReadOrder() : isb(), idx(), unit() {
+    int l_r = 0;
+    for( int l_f = 0; l_f < ( TM > TN ? TM : TN ); l_f++ ) {
+      if( l_f < TM ) for( int l_u = 0; l_u < UA; l_u++ ) { isb[l_r] = 0; idx[l_r] = l_f; unit[l_r] = l_u; l_r++; }
+      if( l_f < TN ) for( int l_u = 0; l_u < UB; l_u++ ) { isb[l_r] = 1; idx[l_r] = l_f; unit[l_r] = l_u; l_r++; }
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Main loop with an explicit instruction schedule (BK 32 = two k substeps,
+// four LDS stages).  With one wave per SIMD the matrix core idles whenever
+// the wave stalls, so every MFMA is followed by the LDS reads of the next
+// substep's fragments, the eight DMA issues of a step are spread over the
+// MFMAs of its first substep, and the wait + barrier that publish the next
+// stage sit after four MFMAs of the last substep, when the data has long
+// landed.  sched_barrier(0) keeps the compiler from regrouping the sequence.
+//
+// Step t (stage buffer t % 4):
+//   substep 0: 16 MFMAs on fragment set 0, reads of substep 1 into set 1,
+//              DMA of step t + 3 into the buffer of step t - 1
+//   substep 1: 4 MFMAs on set 1; wait for step t + 1 (own DMA: vmcnt,
+//              everyone's: barrier); 12 MFMAs with the reads of step t + 1,
+//              substep 0 into set 0
+// The last three steps issue no DMA (vmcnt(0) before the barrier) and the
+// final step has no barrier.
+// ---------------------------------------------------------------------------
+template< int BM, int BN, int BK, int WM, int WN, int MA, int MB, int STAGES, typename LdA, typename LdB,
+          typename FrA, typename FrB, int TM, int TN >
+__device__ __attribute__( ( always_inline ) ) inline void mainloop_scheduled(
+    f32x16 ( &l_acc )[TM][TN], char * l_lds, LdA & l_lda, LdB & l_ldb, FrA const & l_fra, FrB const & l_frb,
+    i32x4 l_ra, i32x4 l_rb, int l_wave, int32_t l_K, int32_t l_nk, uint32_t l_kb_a, uint32_t l_kb_b ) {
+  constexpr int SA  = LdA::STAGE_BYTES;
+  constexpr int SB  = LdB::STAGE_BYTES;
+  constexpr int NJA = LdA::NJ;
+  constexpr int NJW = LdA::NJ + LdB::NJ;
+  constexpr int NMF = TM * TN;
+  constexpr int PB  = 4;                           // MFMAs before the barrier
+  typedef ReadOrder< TM, TN, FrA::UNITS, FrB::UNITS > RO;
+  constexpr int U   = RO::U;
+  constexpr MfmaOrder< TM, TN > kMo{};
+  constexpr RO kRo{};
+  static_assert( NMF % NJW == 0, "DMA issues must spread evenly over the MFMAs" );
+
+  uint32_t const l_lds0 = lds_addr( l_lds );
+  typename FrA::Part l_pa[2][TM];
+  typename FrB::Part l_pb[2][TN];
+
+  // prologue: steps 0 .. STAGES-2 (steps >= nk load zeros), then fragments
+  // of step 0, substep 0
+#pragma unroll
+  for( int l_t = 0; l_t < STAGES - 1; l_t++ ) {
+    uint32_t const l_st = l_lds0 + uint32_t( l_t ) * ( SA + SB );
+    l_lda.issue( l_ra, l_st, l_wave, l_t * BK, l_K, uint32_t( l_t ) * l_kb_a );
+    l_ldb.issue( l_rb, l_st + SA, l_wave, l_t * BK, l_K, uint32_t( l_t ) * l_kb_b );
+  }
+  wait_vmcnt< ( STAGES - 2 ) * NJW >();
+  barrier_lds();
+  static_for< U >( [&]( auto rc ) __attribute__( ( always_inline ) ) {
+    constexpr int l_r = decltype( rc )::value;
+    if constexpr( kRo.isb[l_r] == 0 ) l_fra.template read_unit< kRo.unit[l_r] >( l_lds, kRo.idx[l_r], 0, l_pa[0][kRo.idx[l_r]] );
+    else l_frb.template read_unit< kRo.unit[l_r] >( l_lds + SA, kRo.idx[l_r], 0, l_pb[0][kRo.idx[l_r]] );
+  } );
+
+  auto iteration = [&]( int32_t l_t, auto dma_c, auto next_c ) __attribute__( ( always_inline ) ) {
+    constexpr bool DMA  = decltype( dma_c )::value;
+    constexpr bool NEXT = decltype( next_c )::value;
+    char const * l_sa = l_lds + ( l_t % STAGES ) * ( SA + SB );
+    char const * l_sb = l_sa + SA;
+    char const * l_na = l_lds + ( ( l_t + 1 ) % STAGES ) * ( SA + SB );
+    int32_t const l_tl = l_t + STAGES - 1;
+    uint32_t const l_st = l_lds0 + uint32_t( l_tl % STAGES ) * ( SA + SB );
+
+    // substep 0
+    static_for< NMF >( [&]( auto pc ) __attribute__( ( always_inline ) ) {
+      constexpr int l_p = decltype( pc )::value;
+      constexpr int l_i = kMo.i[l_p];
+      constexpr int l_j = kMo.j[l_p];
+      l_acc[l_i][l_j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16( FrA::value( l_pa[0][l_i] ), FrB::value( l_pb[0][l_j] ),
+                                                                 l_acc[l_i][l_j], 0, 0, 0 );
+      static_for< U >( [&]( auto rc ) __attribute__( ( always_inline ) ) {
+        constexpr int l_r = decltype( rc )::value;
+        if constexpr( ( l_r * NMF ) / U == l_p ) {
+          if constexpr( kRo.isb[l_r] == 0 )
+            l_fra.template read_unit< kRo.unit[l_r] >( l_sa, kRo.idx[l_r], 1, l_pa[1][kRo.idx[l_r]] );
+          else
+            l_frb.template read_unit< kRo.unit[l_r] >( l_sb, kRo.idx[l_r], 1, l_pb[1][kRo.idx[l_r]] );
+        }
+      } );
+      if constexpr( DMA ) {
+        static_for< NJW >( [&]( auto dc ) __attribute__( ( always_inline ) ) {
+          constexpr int l_d = decltype( dc )::value;
+          if constexpr( l_d * ( NMF / NJW ) + ( NMF / NJW - 1 ) == l_p ) {
+            if constexpr( l_d < NJA )
+              l_lda.template issue_one< l_d >( l_ra, l_st, l_wave, l_tl * BK, l_K, uint32_t( l_tl ) * l_kb_a );
+            else
+              l_ldb.template issue_one< l_d - NJA >( l_rb, l_st + SA, l_wave, l_tl * BK, l_K,
+                                                     uint32_t( l_tl ) * l_kb_b );
+          }
+        } );
+      }
+      __builtin_amdgcn_sched_barrier( 0 );
+    } );
+
+    // substep 1
+    static_for< NMF >( [&]( auto pc ) __attribute__( ( always_inline ) ) {
+      constexpr int l_p = decltype( pc )::value;
+      constexpr int l_i = kMo.i[l_p];
+      constexpr int l_j = kMo.j[l_p];
+      l_acc[l_i][l_j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16( FrA::value( l_pa[1][l_i] ), FrB::value( l_pb[1][l_j] ),
+                                                                 l_acc[l_i][l_j], 0, 0, 0 );
+      if constexpr( NEXT ) {
+        if constexpr( l_p == PB - 1 ) {
+          if constexpr( DMA ) wait_vmcnt< ( STAGES - 2 ) * NJW >();
+          else                wait_vmcnt< 0 >();
+          wait_lgkmcnt0();
+          barrier_lds();
+        }
+        static_for< U >( [&]( auto rc ) __attribute__( ( always_inline ) ) {
+          constexpr int l_r = decltype( rc )::value;
+          if constexpr( l_p >= PB && PB + ( l_r * ( NMF - PB ) ) / U == l_p ) {
+            if constexpr( kRo.isb[l_r] == 0 )
+              l_fra.template read_unit< kRo.unit[l_r] >( l_na, kRo.idx[l_r], 0, l_pa[0][kRo.idx[l_r]] );
+            else
+              l_frb.template read_unit< kRo.unit[l_r] >( l_na + SA, kRo.idx[l_r], 0, l_pb[0][kRo.idx[l_r]] );
+          }
+        } );
+      }
+      __builtin_amdgcn_sched_barrier( 0 );
+    } );
+  };
+
+  std::integral_constant< bool, true >  const l_yes{};
+  std::integral_constant< bool, false > const l_no{};
+  int32_t l_t = 0;
+  for( ; l_t < l_nk - ( STAGES - 1 ); l_t++ ) iteration( l_t, l_yes, l_yes );
+  for( ; l_t < l_nk - 1; l_t++ ) iteration( l_t, l_no, l_yes );
+  iteration( l_nk - 1, l_no, l_no );
+  // the prologue's loads past the last step (zeros) still target LDS: drain
+  // them before the epilogue reuses it
+  wait_vmcnt< 0 >();
+  barrier_lds();
+}
 
 // ---------------------------------------------------------------------------
 // the kernel
@@ -319,7 +523,13 @@ void contract_dma_kernel( ContractArgs a ) {
   uint32_t const l_kb_b = uint32_t( 2 * BK * a.sk_b );
   uint32_t const l_lds0 = lds_addr( l_lds );
 
-  if( l_nk > 0 ) {
+  if constexpr( SUB == 2 && STAGES == 4 ) {
+    if( l_nk > 0 ) {
+      mainloop_scheduled< BM, BN, BK, WM, WN, MA, MB, STAGES >( l_acc, l_lds, l_lda, l_ldb, l_fra, l_frb, l_ra,
+                                                                l_rb, l_wave, l_K, l_nk, l_kb_a, l_kb_b );
+    }
+  }
+  else if( l_nk > 0 ) {
     // prologue: steps 0 .. STAGES-2 (steps >= nk load zeros)
 #pragma unroll
     for( int l_t = 0; l_t < STAGES - 1; l_t++ ) {
