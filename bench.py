@@ -9,6 +9,10 @@ is one execution of that contraction (one kernel launch).  The other configs
 (permute abcd->dbca in GB/s, the fp32 contraction of config 1, the 4-layer
 MLP tree of config 4) are reported under "extra".
 
+Before the config-3 timing the same kernel runs untimed for about one second
+so the GPU is at its steady clock; the timed region is exactly --steps
+launches after --warmup untimed ones.
+
 `roofline` is for the dominant kernel (the config-3 contraction kernel):
 achieved = 2*C*M*N*K FLOP per launch / average launch duration, measured with
 HIP events recorded on the stream the kernel is launched on; peak = MI355X
@@ -50,10 +54,23 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def time_launches(torch, stream, fn, steps, warmup):
-    """Runs fn() warmup times untimed, then steps times between HIP events on
-    `stream`; returns (total seconds by host clock, average seconds per launch
-    by device events)."""
+def settle_clocks(torch, fn, seconds=1.0):
+    """Runs fn() untimed for about `seconds` so the GPU reaches its steady
+    clock under this load before anything is measured (the first kernels of a
+    fresh process otherwise run up to 10 % slower while the clock ramps)."""
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+
+
+def time_launches(torch, stream, fn, steps, warmup, settle=0.0):
+    """Optionally settles the clock (untimed), runs fn() warmup times untimed,
+    then steps times between HIP events on `stream`; returns (total seconds by
+    host clock, average seconds per launch by device events)."""
+    if settle > 0.0:
+        settle_clocks(torch, fn, settle)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -93,7 +110,7 @@ def bench_c3(torch, eir, stream, steps, warmup):
                                dtype_out=eir.FP32)
     flops = plan.flops
     fn = lambda: plan.execute(left, right, out, stream=stream)
-    wall, per_launch = time_launches(torch, stream, fn, steps, warmup)
+    wall, per_launch = time_launches(torch, stream, fn, steps, warmup, settle=1.0)
     res = dict(flops=flops, wall=wall, per_launch=per_launch, desc=plan.describe(), bytes=plan.bytes)
     plan.close()
     del left, right, out

@@ -3,6 +3,7 @@
 // strings; planning and kernels live in contract_plan.cpp / permute.hip.
 #include "etir_internal.h"
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 namespace etir {
@@ -54,9 +55,16 @@ int etir_hip_contraction_create( int64_t         num_loops,
                                       ktype_first_touch, ktype_main, ktype_last_touch,
                                       l_plan->cont );
   if( l_err != ETIR_SUCCESS ) {
-    if( l_plan->cont.d_tables != nullptr ) (void) hipFree( l_plan->cont.d_tables );
+    etir::release_contraction( l_plan->cont );
     delete l_plan;
     return l_err;
+  }
+  if( char const * l_v = std::getenv( "ETIR_VERBOSE" ) ) {
+    // diagnostic: one line per compiled contraction plan
+    if( l_v[0] != '\0' && l_v[0] != '0' ) {
+      std::fprintf( stderr, "etir plan %p: %s (%.3f GFLOP)\n", (void *) l_plan, l_plan->cont.desc.c_str(),
+                    double( l_plan->cont.flops ) * 1e-9 );
+    }
   }
   *plan = l_plan;
   return ETIR_SUCCESS;
@@ -116,9 +124,7 @@ int etir_hip_permute_execute( etir_plan_t  plan,
 
 int etir_hip_plan_destroy( etir_plan_t plan ) {
   if( plan == nullptr ) return ETIR_SUCCESS;
-  if( plan->kind == 1 && plan->cont.d_tables != nullptr ) {
-    ETIR_HIP_CHECK( hipFree( plan->cont.d_tables ) );
-  }
+  if( plan->kind == 1 ) etir::release_contraction( plan->cont );
   delete plan;
   return ETIR_SUCCESS;
 }

@@ -44,7 +44,7 @@ typedef int32_t i32x4 __attribute__( ( ext_vector_type( 4 ) ) );
 // buffer resource of a raw (stride 0) buffer: base address, num_records
 // bytes, gfx9 word-3 format bits for untyped dword access
 __device__ inline i32x4 make_rsrc( void const * base, uint32_t num_records ) {
-  uint64_t const l_b = reinterpret_cast< uint64_t >( base );
+  uint64_t const l_b = reinterpret_cast< uint64_t >( uniform_ptr( base ) );
   i32x4 l_r;
   l_r[0] = int32_t( uint32_t( l_b ) );
   l_r[1] = int32_t( uint32_t( l_b >> 32 ) & 0xffffu );
@@ -78,13 +78,7 @@ __device__ inline uint32_t lds_addr( void const * p ) {
 template< int N >
 __device__ inline void wait_vmcnt() {
   static_assert( N >= 0 && N < 64, "vmcnt out of range" );
-  if constexpr( N == 0 )      asm volatile( "s_waitcnt vmcnt(0)" ::: "memory" );
-  else if constexpr( N == 8 ) asm volatile( "s_waitcnt vmcnt(8)" ::: "memory" );
-  else if constexpr( N == 16 ) asm volatile( "s_waitcnt vmcnt(16)" ::: "memory" );
-  else if constexpr( N == 24 ) asm volatile( "s_waitcnt vmcnt(24)" ::: "memory" );
-  else if constexpr( N == 32 ) asm volatile( "s_waitcnt vmcnt(32)" ::: "memory" );
-  else if constexpr( N == 48 ) asm volatile( "s_waitcnt vmcnt(48)" ::: "memory" );
-  else static_assert( N == 0, "add the vmcnt value" );
+  asm volatile( "s_waitcnt vmcnt(%0)" :: "n"( N ) : "memory" );
 }
 
 // workgroup barrier that also orders LDS accesses around it (no waitcnt)
@@ -321,17 +315,18 @@ struct ReadOrder {
 // Main loop with an explicit instruction schedule (BK 32 = two k substeps,
 // four LDS stages).  With one wave per SIMD the matrix core idles whenever
 // the wave stalls, so every MFMA is followed by the LDS reads of the next
-// substep's fragments, the eight DMA issues of a step are spread over the
-// MFMAs of its first substep, and the wait + barrier that publish the next
+// substep's fragments, the eight DMA issues of a step are spread over all
+// of its MFMAs (one per four), and the wait + barrier that publish the next
 // stage sit after four MFMAs of the last substep, when the data has long
 // landed.  sched_barrier(0) keeps the compiler from regrouping the sequence.
 //
 // Step t (stage buffer t % 4):
-//   substep 0: 16 MFMAs on fragment set 0, reads of substep 1 into set 1,
-//              DMA of step t + 3 into the buffer of step t - 1
+//   substep 0: 16 MFMAs on fragment set 0, reads of substep 1 into set 1
 //   substep 1: 4 MFMAs on set 1; wait for step t + 1 (own DMA: vmcnt,
 //              everyone's: barrier); 12 MFMAs with the reads of step t + 1,
 //              substep 0 into set 0
+//   throughout: DMA of step t + 3 into the buffer of step t - 1 (freed by
+//              the barrier that ended step t - 1)
 // The last three steps issue no DMA (vmcnt(0) before the barrier) and the
 // final step has no barrier.
 // ---------------------------------------------------------------------------
@@ -350,7 +345,13 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_scheduled(
   constexpr int U   = RO::U;
   constexpr MfmaOrder< TM, TN > kMo{};
   constexpr RO kRo{};
-  static_assert( NMF % NJW == 0, "DMA issues must spread evenly over the MFMAs" );
+  static_assert( ( 2 * NMF ) % NJW == 0, "DMA issues must spread evenly over the MFMAs" );
+  static_assert( STAGES == 4, "the wait count below assumes loads three steps ahead" );
+  // DMA issue d sits after MFMA d * GAP + GAP - 1 of the step (MFMA index over
+  // both substeps), after any wait at that MFMA; the wait + barrier sit after
+  // MFMA NMF + PB - 1.  DMA_BEFORE = issues of this step that precede it.
+  constexpr int GAP = ( 2 * NMF ) / NJW;
+  constexpr int DMA_BEFORE = ( NMF + PB - 1 ) / GAP;
 
   uint32_t const l_lds0 = lds_addr( l_lds );
   typename FrA::Part l_pa[2][TM];
@@ -381,51 +382,41 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_scheduled(
     int32_t const l_tl = l_t + STAGES - 1;
     uint32_t const l_st = l_lds0 + uint32_t( l_tl % STAGES ) * ( SA + SB );
 
-    // substep 0
-    static_for< NMF >( [&]( auto pc ) __attribute__( ( always_inline ) ) {
-      constexpr int l_p = decltype( pc )::value;
+    // both substeps as one sequence of 2 * NMF MFMAs; DMA issues spread
+    // evenly over it (one per 2 * NMF / NJW MFMAs) so the address unit is
+    // never asked for a whole step's loads at once
+    static_for< 2 * NMF >( [&]( auto qc ) __attribute__( ( always_inline ) ) {
+      constexpr int l_q = decltype( qc )::value;
+      constexpr int l_s = l_q / NMF;                 // substep
+      constexpr int l_p = l_q % NMF;                 // MFMA within the substep
       constexpr int l_i = kMo.i[l_p];
       constexpr int l_j = kMo.j[l_p];
-      l_acc[l_i][l_j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16( FrA::value( l_pa[0][l_i] ), FrB::value( l_pb[0][l_j] ),
+      l_acc[l_i][l_j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16( FrA::value( l_pa[l_s][l_i] ),
+                                                                 FrB::value( l_pb[l_s][l_j] ),
                                                                  l_acc[l_i][l_j], 0, 0, 0 );
-      static_for< U >( [&]( auto rc ) __attribute__( ( always_inline ) ) {
-        constexpr int l_r = decltype( rc )::value;
-        if constexpr( ( l_r * NMF ) / U == l_p ) {
-          if constexpr( kRo.isb[l_r] == 0 )
-            l_fra.template read_unit< kRo.unit[l_r] >( l_sa, kRo.idx[l_r], 1, l_pa[1][kRo.idx[l_r]] );
-          else
-            l_frb.template read_unit< kRo.unit[l_r] >( l_sb, kRo.idx[l_r], 1, l_pb[1][kRo.idx[l_r]] );
-        }
-      } );
-      if constexpr( DMA ) {
-        static_for< NJW >( [&]( auto dc ) __attribute__( ( always_inline ) ) {
-          constexpr int l_d = decltype( dc )::value;
-          if constexpr( l_d * ( NMF / NJW ) + ( NMF / NJW - 1 ) == l_p ) {
-            if constexpr( l_d < NJA )
-              l_lda.template issue_one< l_d >( l_ra, l_st, l_wave, l_tl * BK, l_K, uint32_t( l_tl ) * l_kb_a );
+      if constexpr( l_s == 0 ) {
+        // fragments of substep 1 of this step
+        static_for< U >( [&]( auto rc ) __attribute__( ( always_inline ) ) {
+          constexpr int l_r = decltype( rc )::value;
+          if constexpr( ( l_r * NMF ) / U == l_p ) {
+            if constexpr( kRo.isb[l_r] == 0 )
+              l_fra.template read_unit< kRo.unit[l_r] >( l_sa, kRo.idx[l_r], 1, l_pa[1][kRo.idx[l_r]] );
             else
-              l_ldb.template issue_one< l_d - NJA >( l_rb, l_st + SA, l_wave, l_tl * BK, l_K,
-                                                     uint32_t( l_tl ) * l_kb_b );
+              l_frb.template read_unit< kRo.unit[l_r] >( l_sb, kRo.idx[l_r], 1, l_pb[1][kRo.idx[l_r]] );
           }
         } );
       }
-      __builtin_amdgcn_sched_barrier( 0 );
-    } );
-
-    // substep 1
-    static_for< NMF >( [&]( auto pc ) __attribute__( ( always_inline ) ) {
-      constexpr int l_p = decltype( pc )::value;
-      constexpr int l_i = kMo.i[l_p];
-      constexpr int l_j = kMo.j[l_p];
-      l_acc[l_i][l_j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16( FrA::value( l_pa[1][l_i] ), FrB::value( l_pb[1][l_j] ),
-                                                                 l_acc[l_i][l_j], 0, 0, 0 );
-      if constexpr( NEXT ) {
+      else if constexpr( NEXT ) {
         if constexpr( l_p == PB - 1 ) {
-          if constexpr( DMA ) wait_vmcnt< ( STAGES - 2 ) * NJW >();
+          // step t + 1 is complete once at most the loads issued after it
+          // are in flight: all of step t + 2 (issued during step t - 1) and
+          // the DMA_BEFORE loads of step t + 3 issued so far in this step
+          if constexpr( DMA ) wait_vmcnt< ( STAGES - 3 ) * NJW + DMA_BEFORE >();
           else                wait_vmcnt< 0 >();
           wait_lgkmcnt0();
           barrier_lds();
         }
+        // fragments of substep 0 of step t + 1
         static_for< U >( [&]( auto rc ) __attribute__( ( always_inline ) ) {
           constexpr int l_r = decltype( rc )::value;
           if constexpr( l_p >= PB && PB + ( l_r * ( NMF - PB ) ) / U == l_p ) {
@@ -433,6 +424,18 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_scheduled(
               l_fra.template read_unit< kRo.unit[l_r] >( l_na, kRo.idx[l_r], 0, l_pa[0][kRo.idx[l_r]] );
             else
               l_frb.template read_unit< kRo.unit[l_r] >( l_na + SA, kRo.idx[l_r], 0, l_pb[0][kRo.idx[l_r]] );
+          }
+        } );
+      }
+      if constexpr( DMA ) {
+        static_for< NJW >( [&]( auto dc ) __attribute__( ( always_inline ) ) {
+          constexpr int l_d = decltype( dc )::value;
+          if constexpr( l_d * GAP + GAP - 1 == l_q ) {
+            if constexpr( l_d < NJA )
+              l_lda.template issue_one< l_d >( l_ra, l_st, l_wave, l_tl * BK, l_K, uint32_t( l_tl ) * l_kb_a );
+            else
+              l_ldb.template issue_one< l_d - NJA >( l_rb, l_st + SA, l_wave, l_tl * BK, l_K,
+                                                     uint32_t( l_tl ) * l_kb_b );
           }
         } );
       }

@@ -375,8 +375,8 @@ __device__ __attribute__( ( always_inline ) ) inline P * uniform_ptr( P * p ) {
 // Fast path -- a full tile, fp32 output, first touch ZERO, last touch none
 // or RELU, output byte offsets below 2^32: no bounds checks, the four row
 // offsets r%4 = 0..3 of one accumulator group come from one ds_read_b128,
-// and every value is one buffer_store_dword with a 32-bit byte offset from a
-// per-tile base in scalar registers.  When the output's column index is
+// and every value is one non-temporal buffer_store_dword with a 32-bit byte
+// offset from a per-tile base in scalar registers.  When the output's column index is
 // unit-stride each store writes two 128-byte runs (lanes 0-31 and 32-63).
 //
 // General path -- edge tiles, auxiliary tensors, accumulation into the
@@ -391,6 +391,11 @@ struct EpilogueLds {
   static constexpr int SLAB  = 32 * PITCH * 4;                   // bytes per wave
   static constexpr int BYTES = TABS + WM * WN * SLAB;
 };
+
+// cache policy of the output stores: non-temporal (the output is written
+// once and not read by the kernel; streaming it keeps the operand tiles that
+// neighbouring workgroups still need in L2)
+constexpr int kStoreNt = 2;
 
 template< int TM, int TN, bool RELU >
 __device__ __attribute__( ( always_inline ) ) inline void epilogue_fast_f32(
@@ -416,7 +421,7 @@ __device__ __attribute__( ( always_inline ) ) inline void epilogue_fast_f32(
           float l_v = l_acc[l_i][l_j][4 * l_g + l_e];
           if constexpr( RELU ) l_v = fmaxf( l_v, 0.0f );
           __builtin_amdgcn_raw_buffer_store_b32( __builtin_bit_cast( uint32_t, l_v ), l_rs,
-                                                 uint32_t( l_m4[l_e] ) * 4u + l_noff[l_j], 0, 0 );
+                                                 uint32_t( l_m4[l_e] ) * 4u + l_noff[l_j], 0, kStoreNt );
         } );
       } );
     } );

@@ -170,21 +170,24 @@ void tile_shape( int32_t t, int64_t & bm, int64_t & bn ) {
 
 }  // namespace
 
-int plan_contraction( int64_t            num_loops,
-                      int32_t const    * dim_types,
-                      int64_t const    * sizes,
-                      int64_t const    * strides_left,
-                      int64_t const    * strides_right,
-                      int64_t const    * strides_out_aux,
-                      int64_t const    * strides_out,
-                      int32_t            dtype_left,
-                      int32_t            dtype_right,
-                      int32_t            dtype_comp,
-                      int32_t            dtype_out,
-                      int32_t            ktype_first_touch,
-                      int32_t            ktype_main,
-                      int32_t            ktype_last_touch,
-                      ContractionPlan  & plan ) {
+namespace {
+
+int plan_contraction_impl( int64_t            num_loops,
+                           int32_t const    * dim_types,
+                           int64_t const    * sizes,
+                           int64_t const    * strides_left,
+                           int64_t const    * strides_right,
+                           int64_t const    * strides_out_aux,
+                           int64_t const    * strides_out,
+                           int32_t            dtype_left,
+                           int32_t            dtype_right,
+                           int32_t            dtype_comp,
+                           int32_t            dtype_out,
+                           int32_t            ktype_first_touch,
+                           int32_t            ktype_main,
+                           int32_t            ktype_last_touch,
+                           bool               allow_split,
+                           ContractionPlan  & plan ) {
   plan = ContractionPlan();
 
   // ---------------------------------------------------------------- checks
@@ -389,12 +392,123 @@ int plan_contraction( int64_t            num_loops,
                      && ( l_t != TILE_BF16_DMA_256x256 || l_dma_ok );
     if( l_t_ok ) plan.tile = l_t;
   }
+  // VEC_MN x VEC_MN runs the explicitly scheduled BK 32 / 4-stage main loop;
+  // the other pairings (VEC_K needs 64-wide k rows) the generic BK 64 / 2-stage one
+  plan.dma_variant = ( plan.mode_a == LOAD_VEC_MN && plan.mode_b == LOAD_VEC_MN ) ? 1 : 0;
   if( char const * l_env = std::getenv( "ETIR_DMA_VARIANT" ) ) {
-    // diagnostic: 1 selects BK 32 with 4 stages for VEC_MN x VEC_MN
-    plan.dma_variant = ( std::atoi( l_env ) == 1 && plan.mode_a == LOAD_VEC_MN && plan.mode_b == LOAD_VEC_MN ) ? 1 : 0;
+    // diagnostic override: 0 forces the generic BK 64 / 2-stage loop
+    if( std::atoi( l_env ) == 0 ) plan.dma_variant = 0;
   }
   int64_t l_bm, l_bn;
   tile_shape( plan.tile, l_bm, l_bn );
+
+  // ------------------------------------------------------------- split K
+  // Few output tiles and a long K leave most CUs idle (e.g. an einsum-tree
+  // node with M = 64, N = 1024, K = 32768).  Then the outermost K loops (one
+  // of them factored if needed) become C loops of a partial contraction that
+  // writes one workspace slice per split, and split_reduce sums the slices.
+  if( allow_split && l_size_k >= 512 ) {
+    int64_t const l_tiles = n_tiles( plan.tile );
+    if( l_tiles > 0 && l_tiles < l_cus ) {
+      // at least 128 k per split; aim for two workgroups per CU
+      int64_t const l_smax   = l_size_k / 128;
+      int64_t const l_target = std::min( ( 2 * l_cus + l_tiles - 1 ) / l_tiles, l_smax );
+      std::vector< Loop > l_kk = l_k;          // K loops, outer -> inner
+      std::vector< Loop > l_sp;                // split parts, outer -> inner
+      int64_t l_sf = 1;
+      std::size_t l_i = 0;
+      while( l_sf < l_target && l_i < l_kk.size() ) {
+        Loop & l_lp = l_kk[l_i];
+        int64_t const l_need = ( l_target + l_sf - 1 ) / l_sf;
+        // factor of this loop: the smallest divisor that reaches the target,
+        // else the largest one that stays within l_smax
+        int64_t l_f = 0;
+        for( int64_t l_d = 2; l_d <= l_lp.size; l_d++ ) {
+          if( l_lp.size % l_d != 0 || l_sf * l_d > l_smax ) continue;
+          l_f = l_d;
+          if( l_d >= l_need ) break;
+        }
+        if( l_f == 0 ) break;
+        if( l_f == l_lp.size ) {
+          l_sp.push_back( l_lp );
+          l_sf *= l_lp.size;
+          l_lp.size = 1;
+          l_i++;
+        }
+        else {
+          // k = ko * (size / f) + ki: the outer part steps over size / f
+          Loop l_outer = l_lp;
+          int64_t const l_inner = l_lp.size / l_f;
+          l_outer.size = l_f;
+          for( int l_t = 0; l_t < 4; l_t++ ) l_outer.s[l_t] *= l_inner;
+          l_lp.size = l_inner;
+          l_sp.push_back( l_outer );
+          l_sf *= l_f;
+          break;
+        }
+      }
+      // extent of the output (elements) over its C, M and N loops
+      int64_t l_span = 1;
+      for( auto const * l_set : { &l_c, &l_m, &l_n } ) {
+        for( Loop const & l_x : *l_set ) l_span += ( l_x.size - 1 ) * l_x.s[T_OUT];
+      }
+      int64_t const l_ws_bytes = 4 * l_sf * l_span;
+      if( l_sf >= 2 && l_size_k / l_sf >= 128 && l_ws_bytes <= ( int64_t( 1 ) << 29 ) ) {
+        // loop arrays of the partial contraction
+        std::vector< int32_t > l_pt;
+        std::vector< int64_t > l_psz, l_pl, l_pr, l_pa, l_po;
+        auto add = [&]( int32_t t, int64_t sz, int64_t sl, int64_t sr, int64_t sa, int64_t so ) {
+          l_pt.push_back( t ); l_psz.push_back( sz ); l_pl.push_back( sl ); l_pr.push_back( sr );
+          l_pa.push_back( sa ); l_po.push_back( so );
+        };
+        int64_t l_inner_sp = 1;
+        for( std::size_t l_j = l_sp.size(); l_j-- > 0; ) {
+          Loop const & l_x = l_sp[l_j];
+          add( ETIR_DIM_C, l_x.size, l_x.s[T_L], l_x.s[T_R], 0, l_span * l_inner_sp );
+          l_inner_sp *= l_x.size;
+        }
+        for( auto const * l_set : { &l_c, &l_m, &l_n } ) {
+          for( Loop const & l_x : *l_set ) add( l_x.type, l_x.size, l_x.s[T_L], l_x.s[T_R], l_x.s[T_AUX], l_x.s[T_OUT] );
+        }
+        for( Loop const & l_x : l_kk ) {
+          if( l_x.size > 1 ) add( ETIR_DIM_K, l_x.size, l_x.s[T_L], l_x.s[T_R], 0, 0 );
+        }
+        auto l_part = std::make_shared< ContractionPlan >();
+        int l_err = plan_contraction_impl( (int64_t) l_pt.size(), l_pt.data(), l_psz.data(), l_pl.data(),
+                                           l_pr.data(), l_pa.data(), l_po.data(), dtype_left, dtype_right,
+                                           ETIR_FP32, ETIR_FP32, ETIR_KTYPE_ZERO, ETIR_KTYPE_MADD,
+                                           ETIR_KTYPE_UNDEFINED, false, *l_part );
+        if( l_err != ETIR_SUCCESS ) {
+          release_contraction( *l_part );
+          return l_err;
+        }
+        hipError_t l_he = hipMalloc( &plan.d_ws, (std::size_t) l_ws_bytes );
+        if( l_he != hipSuccess ) {
+          plan.d_ws = nullptr;
+          release_contraction( *l_part );
+          return fail( ETIR_UNDEFINED_ERROR, std::string( "contraction: workspace allocation failed: " )
+                                             + hipGetErrorString( l_he ) );
+        }
+        plan.split    = (int32_t) l_sf;
+        plan.out_span = l_span;
+        plan.partial  = l_part;
+        plan.C = l_size_c;
+        plan.M = l_part->M;
+        plan.N = l_part->N;
+        plan.K = l_size_k;
+        plan.mode_a = l_part->mode_a;
+        plan.mode_b = l_part->mode_b;
+        plan.tile = l_part->tile;
+        plan.flops = 2 * l_size_c * l_size_m * l_size_n * l_size_k;
+        int64_t const l_esz_o = ( dtype_out == ETIR_BF16 ) ? 2 : 4;
+        plan.bytes = l_esz * l_size_c * ( l_size_m + l_size_n ) * l_size_k
+                   + l_esz_o * l_size_c * l_size_m * l_size_n;
+        plan.desc = "split-K S=" + std::to_string( l_sf ) + " K'=" + std::to_string( l_size_k / l_sf )
+                  + " | " + l_part->desc + " | reduce";
+        return ETIR_SUCCESS;
+      }
+    }
+  }
 
   plan.C = l_size_c;
   plan.M = l_kern_m;
@@ -490,6 +604,40 @@ int plan_contraction( int64_t            num_loops,
   return ETIR_SUCCESS;
 }
 
+}  // namespace
+
+int plan_contraction( int64_t            num_loops,
+                      int32_t const    * dim_types,
+                      int64_t const    * sizes,
+                      int64_t const    * strides_left,
+                      int64_t const    * strides_right,
+                      int64_t const    * strides_out_aux,
+                      int64_t const    * strides_out,
+                      int32_t            dtype_left,
+                      int32_t            dtype_right,
+                      int32_t            dtype_comp,
+                      int32_t            dtype_out,
+                      int32_t            ktype_first_touch,
+                      int32_t            ktype_main,
+                      int32_t            ktype_last_touch,
+                      ContractionPlan  & plan ) {
+  return plan_contraction_impl( num_loops, dim_types, sizes, strides_left, strides_right, strides_out_aux,
+                                strides_out, dtype_left, dtype_right, dtype_comp, dtype_out,
+                                ktype_first_touch, ktype_main, ktype_last_touch,
+                                std::getenv( "ETIR_NO_SPLIT_K" ) == nullptr, plan );
+}
+
+void release_contraction( ContractionPlan & plan ) {
+  if( plan.d_tables != nullptr ) (void) hipFree( plan.d_tables );
+  if( plan.d_ws != nullptr ) (void) hipFree( plan.d_ws );
+  plan.d_tables = nullptr;
+  plan.d_ws = nullptr;
+  if( plan.partial ) {
+    release_contraction( *plan.partial );
+    plan.partial.reset();
+  }
+}
+
 int launch_contraction( ContractionPlan const & plan,
                         void const            * left,
                         void const            * right,
@@ -502,6 +650,36 @@ int launch_contraction( ContractionPlan const & plan,
   }
   if( plan.needs_aux && out_aux == nullptr ) {
     return fail( ETIR_NO_DATA_PTR_PROVIDED, "contraction: touch kernel needs the auxiliary tensor" );
+  }
+  if( plan.split > 1 ) {
+    int l_err = launch_contraction( *plan.partial, left, right, nullptr, plan.d_ws, stream );
+    if( l_err != ETIR_SUCCESS ) return l_err;
+    ContractArgs const & p = plan.partial->args;
+    SplitReduceArgs r{};
+    r.ws = reinterpret_cast< float const * >( plan.d_ws );
+    r.aux = plan.needs_aux ? out_aux : nullptr;
+    r.out = out;
+    r.tc_out = p.tc_out;              // the first C entries belong to split 0
+    r.tc_aux = p.tc_aux;
+    r.tm_out = p.tm_out;
+    r.tm_aux = p.tm_aux;
+    r.tn_out = p.tn_out;
+    r.tn_aux = p.tn_aux;
+    r.span = plan.out_span;
+    r.C = (int32_t) plan.C;
+    r.M = p.M;
+    r.N = p.N;
+    r.S = plan.split;
+    r.first_touch = plan.first_touch;
+    r.last_touch = plan.last_touch;
+    r.out_bf16 = ( plan.dtype_out == ETIR_BF16 ) ? 1 : 0;
+    l_err = launch_split_reduce( r, stream );
+    if( l_err != ETIR_SUCCESS ) return l_err;
+    hipError_t l_he = hipGetLastError();
+    if( l_he != hipSuccess ) {
+      return fail( ETIR_UNDEFINED_ERROR, std::string( "split reduce launch failed: " ) + hipGetErrorString( l_he ) );
+    }
+    return ETIR_SUCCESS;
   }
   ContractArgs a = plan.args;
   a.a   = plan.swapped ? right : left;

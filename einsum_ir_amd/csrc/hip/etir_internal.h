@@ -5,6 +5,7 @@
 #define ETIR_INTERNAL_H
 
 #include <cstdint>
+#include <memory>
 #include <string>
 #include <vector>
 #include <hip/hip_runtime.h>
@@ -157,7 +158,7 @@ struct ContractionPlan {
   int32_t mode_b = LOAD_SCALAR;
   int32_t tile = TILE_F32_128x128;
   int32_t tile_fallback = TILE_BF16_256x128;  // used when the DMA kernel's alignment needs fail at launch
-  int32_t dma_variant = 0;                    // 0: BK 64, 2 stages; 1: BK 32, 4 stages (VEC_MN x VEC_MN)
+  int32_t dma_variant = 0;                    // 0: BK 64, 2 stages; 1: BK 32, 4 stages, scheduled (VEC_MN x VEC_MN)
   int64_t flops = 0;
   int64_t bytes = 0;
   // fused loops per kernel role (outer -> inner) for diagnostics
@@ -165,7 +166,37 @@ struct ContractionPlan {
   // device blob with all tables
   void *  d_tables = nullptr;
   ContractArgs args{};          // table pointers + sizes; tensor pointers set at execute
+  // split K: the contraction runs as `partial` -- the split K loops turned
+  // into C loops that write one slice each of the workspace (laid out like
+  // the output, `out_span` elements per slice) -- followed by split_reduce,
+  // which sums the slices in a fixed order and applies the touch kernels
+  int32_t split = 1;
+  int64_t out_span = 0;
+  void *  d_ws = nullptr;
+  std::shared_ptr< ContractionPlan > partial;
 };
+
+// frees the device memory of a contraction plan (tables, workspace, partial plan)
+void release_contraction( ContractionPlan & plan );
+
+struct SplitReduceArgs {
+  float const * ws;
+  void const  * aux;
+  void        * out;
+  int64_t const * tc_out;
+  int64_t const * tc_aux;
+  int32_t const * tm_out;
+  int32_t const * tm_aux;
+  int32_t const * tn_out;
+  int32_t const * tn_aux;
+  int64_t span;
+  int32_t C, M, N, S;
+  int32_t first_touch;
+  int32_t last_touch;
+  int32_t out_bf16;
+};
+
+int launch_split_reduce( SplitReduceArgs const & a, hipStream_t stream );
 
 int  plan_contraction( int64_t            num_loops,
                        int32_t const    * dim_types,
