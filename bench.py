@@ -47,6 +47,8 @@ def parse_args():
     p.add_argument("--only", default="", help="comma list of configs to run (c1,c2,c3,c4,c5)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also time a plain 512 MiB device copy (reference for the PMC byte counters)")
+    p.add_argument("--settle", type=float, default=1.0,
+                   help="seconds of untimed config-3 launches before its timing (GPU clock settling)")
     return p.parse_args()
 
 
@@ -96,7 +98,7 @@ def traffic_from_profile(name):
     return float(m.group(1)) if m else None
 
 
-def bench_c3(torch, eir, stream, steps, warmup):
+def bench_c3(torch, eir, stream, steps, warmup, settle=1.0):
     sizes = dict(z=8, a=64, m=64, b=64, n=64, k=1024)
     loops = eir.binary_loops("zakm,zbkn->zabmn", sizes)
     g = torch.Generator(device="cuda").manual_seed(3)
@@ -110,7 +112,7 @@ def bench_c3(torch, eir, stream, steps, warmup):
                                dtype_out=eir.FP32)
     flops = plan.flops
     fn = lambda: plan.execute(left, right, out, stream=stream)
-    wall, per_launch = time_launches(torch, stream, fn, steps, warmup, settle=1.0)
+    wall, per_launch = time_launches(torch, stream, fn, steps, warmup, settle=settle)
     res = dict(flops=flops, wall=wall, per_launch=per_launch, desc=plan.describe(), bytes=plan.bytes)
     plan.close()
     del left, right, out
@@ -238,7 +240,7 @@ def main():
         log(f"copy: {per*1e6:.1f} us, {2 * 4 * n / per * 1e-9:.0f} GB/s")
         del src, dst
     if run("c3"):
-        c3 = bench_c3(torch, eir, stream, args.steps, args.warmup)
+        c3 = bench_c3(torch, eir, stream, args.steps, args.warmup, settle=args.settle)
         log(f"c3: {c3['desc']}  {c3['per_launch']*1e6:.1f} us/launch")
     if run("c2"):
         c2 = bench_c2(torch, eir, stream, max(args.steps, 20), args.warmup)
