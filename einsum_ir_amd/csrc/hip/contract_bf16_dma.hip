@@ -13,10 +13,21 @@ int launch_one( ContractArgs const & a, uint32_t grid, hipStream_t stream ) {
   return ETIR_SUCCESS;
 }
 
+// 256 x 128 tiles, two workgroups per CU (72 KB of LDS each)
+int launch_bf16_dma_256x128( int32_t ma, int32_t mb, ContractArgs const & a, uint32_t grid, hipStream_t stream ) {
+  if( ma == LOAD_VEC_MN && mb == LOAD_VEC_MN ) {
+    hipLaunchKernelGGL( ( kern::contract_dma_kernel< 256, 128, 32, 2, 2, LOAD_VEC_MN, LOAD_VEC_MN, 3, 2 > ),
+                        dim3( grid ), dim3( 256 ), 0, stream, a );
+    return ETIR_SUCCESS;
+  }
+  return fail( ETIR_COMPILATION_FAILED, "no 256x128 direct-to-LDS kernel for this load-mode combination" );
+}
+
 }  // namespace
 
 int launch_contract_bf16_dma( int32_t ma, int32_t mb, int32_t variant, ContractArgs const & a,
                               uint32_t grid, hipStream_t stream ) {
+  if( variant == 2 ) return launch_bf16_dma_256x128( ma, mb, a, grid, stream );
   if( ma == LOAD_VEC_MN && mb == LOAD_VEC_MN ) {
     if( variant == 1 ) return launch_one< LOAD_VEC_MN, LOAD_VEC_MN, 32, 4 >( a, grid, stream );
     return launch_one< LOAD_VEC_MN, LOAD_VEC_MN, 64, 2 >( a, grid, stream );

@@ -296,6 +296,20 @@ struct MfmaOrder {
   }
 };
 
+// slot (MFMA index) of DMA issue d when ND issues spread over NQ MFMAs
+template< int NQ, int ND >
+constexpr int dma_slot( int d ) {
+  return ( ( d + 1 ) * NQ ) / ND - 1;
+}
+
+// number of DMA issues placed before the instruction that follows MFMA q
+template< int NQ, int ND >
+constexpr int dma_before( int q ) {
+  int l_n = 0;
+  for( int l_d = 0; l_d < ND; l_d++ ) if( dma_slot< NQ, ND >( l_d ) < q ) l_n++;
+  return l_n;
+}
+
 template< int TM, int TN, int UA, int UB >
 struct ReadOrder {
   static constexpr int U = TM * UA + TN * UB;
@@ -345,13 +359,12 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_scheduled(
   constexpr int U   = RO::U;
   constexpr MfmaOrder< TM, TN > kMo{};
   constexpr RO kRo{};
-  static_assert( ( 2 * NMF ) % NJW == 0, "DMA issues must spread evenly over the MFMAs" );
-  static_assert( STAGES == 4, "the wait count below assumes loads three steps ahead" );
-  // DMA issue d sits after MFMA d * GAP + GAP - 1 of the step (MFMA index over
-  // both substeps), after any wait at that MFMA; the wait + barrier sit after
-  // MFMA NMF + PB - 1.  DMA_BEFORE = issues of this step that precede it.
-  constexpr int GAP = ( 2 * NMF ) / NJW;
-  constexpr int DMA_BEFORE = ( NMF + PB - 1 ) / GAP;
+  static_assert( STAGES >= 3, "loads run at least two steps ahead" );
+  static_assert( NJW <= 2 * NMF, "at most one DMA issue per MFMA" );
+  // DMA issue d sits after MFMA dma_slot(d) of the step (MFMA index over both
+  // substeps, evenly spread), after any wait at that MFMA; the wait + barrier
+  // sit after MFMA NMF + PB - 1.  DMA_BEFORE = issues of this step before it.
+  constexpr int DMA_BEFORE = dma_before< 2 * NMF, NJW >( NMF + PB - 1 );
 
   uint32_t const l_lds0 = lds_addr( l_lds );
   typename FrA::Part l_pa[2][TM];
@@ -409,8 +422,9 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_scheduled(
       else if constexpr( NEXT ) {
         if constexpr( l_p == PB - 1 ) {
           // step t + 1 is complete once at most the loads issued after it
-          // are in flight: all of step t + 2 (issued during step t - 1) and
-          // the DMA_BEFORE loads of step t + 3 issued so far in this step
+          // are in flight: all of steps t + 2 .. t + STAGES - 2 (issued in
+          // earlier steps) and the DMA_BEFORE loads of step t + STAGES - 1
+          // issued so far in this step
           if constexpr( DMA ) wait_vmcnt< ( STAGES - 3 ) * NJW + DMA_BEFORE >();
           else                wait_vmcnt< 0 >();
           wait_lgkmcnt0();
@@ -430,7 +444,7 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_scheduled(
       if constexpr( DMA ) {
         static_for< NJW >( [&]( auto dc ) __attribute__( ( always_inline ) ) {
           constexpr int l_d = decltype( dc )::value;
-          if constexpr( l_d * GAP + GAP - 1 == l_q ) {
+          if constexpr( dma_slot< 2 * NMF, NJW >( l_d ) == l_q ) {
             if constexpr( l_d < NJA )
               l_lda.template issue_one< l_d >( l_ra, l_st, l_wave, l_tl * BK, l_K, uint32_t( l_tl ) * l_kb_a );
             else
@@ -458,8 +472,8 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_scheduled(
 // ---------------------------------------------------------------------------
 // the kernel
 // ---------------------------------------------------------------------------
-template< int BM, int BN, int BK, int WM, int WN, int MA, int MB, int STAGES >
-__global__ __launch_bounds__( 64 * WM * WN, 1 )
+template< int BM, int BN, int BK, int WM, int WN, int MA, int MB, int STAGES, int WPE = 1 >
+__global__ __launch_bounds__( 64 * WM * WN, WPE )
 void contract_dma_kernel( ContractArgs a ) {
   constexpr int W   = WM * WN;
   constexpr int T   = 64 * W;
@@ -526,7 +540,7 @@ void contract_dma_kernel( ContractArgs a ) {
   uint32_t const l_kb_b = uint32_t( 2 * BK * a.sk_b );
   uint32_t const l_lds0 = lds_addr( l_lds );
 
-  if constexpr( SUB == 2 && STAGES == 4 ) {
+  if constexpr( SUB == 2 && STAGES >= 3 ) {
     if( l_nk > 0 ) {
       mainloop_scheduled< BM, BN, BK, WM, WN, MA, MB, STAGES >( l_acc, l_lds, l_lda, l_ldb, l_fra, l_frb, l_ra,
                                                                 l_rb, l_wave, l_K, l_nk, l_kb_a, l_kb_b );

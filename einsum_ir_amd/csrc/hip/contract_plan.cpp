@@ -150,6 +150,7 @@ char const * tile_str( int32_t t ) {
     case TILE_BF16_256x256: return "bf16_256x256x64";
     case TILE_BF16_256x128: return "bf16_256x128x32";
     case TILE_BF16_DMA_256x256: return "bf16_dma_256x256";
+    case TILE_BF16_DMA_256x128: return "bf16_dma_256x128";
     case TILE_BF16_128x128: return "bf16_128x128x64";
     case TILE_BF16_64x64:   return "bf16_64x64x64";
     default:                return "?";
@@ -163,6 +164,7 @@ void tile_shape( int32_t t, int64_t & bm, int64_t & bn ) {
     case TILE_BF16_256x256: bm = 256; bn = 256; break;
     case TILE_BF16_256x128: bm = 256; bn = 128; break;
     case TILE_BF16_DMA_256x256: bm = 256; bn = 256; break;
+    case TILE_BF16_DMA_256x128: bm = 256; bn = 128; break;
     case TILE_BF16_128x128: bm = 128; bn = 128; break;
     default:                bm = 64;  bn = 64;  break;
   }
@@ -358,8 +360,19 @@ int plan_contraction_impl( int64_t            num_loops,
     return ( ( l_kern_m + l_bm - 1 ) / l_bm ) * ( ( l_kern_n + l_bn - 1 ) / l_bn ) * l_size_c;
   };
   int64_t const l_cus = 256;
+  // useful fraction of the padded tile grid times the fraction of CUs with a
+  // tile: M = 64 on 128 x 128 tiles wastes half of every tile
+  auto score = [&]( int32_t t ) {
+    int64_t l_bm, l_bn;
+    tile_shape( t, l_bm, l_bn );
+    double const l_pad = double( ( ( l_kern_m + l_bm - 1 ) / l_bm ) * l_bm )
+                       * double( ( ( l_kern_n + l_bn - 1 ) / l_bn ) * l_bn );
+    double const l_util = l_pad > 0.0 ? double( l_kern_m ) * double( l_kern_n ) / l_pad : 1.0;
+    return l_util * std::min( 1.0, double( n_tiles( t ) ) / double( l_cus ) );
+  };
   if( l_f32 ) {
-    plan.tile = ( n_tiles( TILE_F32_128x128 ) >= l_cus ) ? TILE_F32_128x128 : TILE_F32_64x64;
+    // the larger tile unless the smaller one wastes clearly less
+    plan.tile = ( score( TILE_F32_128x128 ) >= 0.95 * score( TILE_F32_64x64 ) ) ? TILE_F32_128x128 : TILE_F32_64x64;
   }
   else {
     if(      n_tiles( TILE_BF16_256x128 ) >= 2 * l_cus ) plan.tile = TILE_BF16_256x128;
@@ -388,8 +401,11 @@ int plan_contraction_impl( int64_t            num_loops,
     // diagnostic override of the tile heuristic (must match the dtype)
     int32_t l_t = std::atoi( l_env );
     bool const l_t_f32 = ( l_t == TILE_F32_128x128 || l_t == TILE_F32_64x64 );
-    bool const l_t_ok = ( l_t >= 0 && l_t <= TILE_BF16_DMA_256x256 && l_t != TILE_F64_64x64 && l_t_f32 == l_f32 )
-                     && ( l_t != TILE_BF16_DMA_256x256 || l_dma_ok );
+    bool const l_t_dma = ( l_t == TILE_BF16_DMA_256x256 || l_t == TILE_BF16_DMA_256x128 );
+    bool const l_t_ok = ( l_t >= 0 && l_t <= TILE_BF16_DMA_256x128 && l_t != TILE_F64_64x64 && l_t_f32 == l_f32 )
+                     && ( !l_t_dma || l_dma_ok )
+                     && ( l_t != TILE_BF16_DMA_256x128
+                          || ( plan.mode_a == LOAD_VEC_MN && plan.mode_b == LOAD_VEC_MN ) );
     if( l_t_ok ) plan.tile = l_t;
   }
   // VEC_MN x VEC_MN runs the explicitly scheduled BK 32 / 4-stage main loop;
@@ -698,7 +714,8 @@ int launch_contraction( ContractionPlan const & plan,
   if( uintptr_t( a.a ) % align_of( l_ma ) != 0 ) l_ma = LOAD_SCALAR;
   if( uintptr_t( a.b ) % align_of( l_mb ) != 0 ) l_mb = LOAD_SCALAR;
   int32_t l_tile = plan.tile;
-  if( l_tile == TILE_BF16_DMA_256x256 && ( l_ma != plan.mode_a || l_mb != plan.mode_b ) ) {
+  if(    ( l_tile == TILE_BF16_DMA_256x256 || l_tile == TILE_BF16_DMA_256x128 )
+      && ( l_ma != plan.mode_a || l_mb != plan.mode_b ) ) {
     // the DMA kernel needs the 16-byte vector modes: use the register-staged
     // kernel with its own tile grid
     l_tile = plan.tile_fallback;
@@ -724,6 +741,9 @@ int launch_contraction( ContractionPlan const & plan,
     case TILE_BF16_64x64:   l_err = launch_contract_bf16_64x64( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_BF16_DMA_256x256:
       l_err = launch_contract_bf16_dma( l_ma, l_mb, plan.dma_variant, a, l_g, stream );
+      break;
+    case TILE_BF16_DMA_256x128:
+      l_err = launch_contract_bf16_dma( l_ma, l_mb, 2, a, l_g, stream );
       break;
     default: return fail( ETIR_COMPILATION_FAILED, "contraction: unknown tile configuration" );
   }

@@ -111,7 +111,8 @@ enum TileCfg : int32_t {
   TILE_BF16_64x64  = 4,
   TILE_F64_64x64   = 5,
   TILE_BF16_256x128 = 6,
-  TILE_BF16_DMA_256x256 = 7   // direct-to-LDS kernel (contract_dma.h)
+  TILE_BF16_DMA_256x256 = 7,  // direct-to-LDS kernel (contract_dma.h), one workgroup per CU
+  TILE_BF16_DMA_256x128 = 8   // direct-to-LDS kernel, two workgroups per CU
 };
 
 struct ContractArgs {

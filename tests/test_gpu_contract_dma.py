@@ -29,6 +29,14 @@ def test_dma_layouts(torch_cuda, oracle, monkeypatch, expr, sizes, modes, varian
     assert "bf16_dma_256x256" in desc and modes in desc, desc
 
 
+@pytest.mark.parametrize("expr,sizes", [("km,kn->mn", dict(k=136, m=264, n=520)),
+                                        ("zakm,zbkn->zabmn", dict(z=2, a=3, m=64, b=5, n=64, k=200))])
+def test_dma_256x128_two_per_cu(torch_cuda, oracle, monkeypatch, expr, sizes):
+    monkeypatch.setenv("ETIR_TILE", "8")
+    _, desc = run_case(torch_cuda, oracle, expr, sizes, dtype=eir.BF16, seed=17)
+    assert "bf16_dma_256x128" in desc, desc
+
+
 @pytest.mark.parametrize("first,last", [(eir.COPY, eir.UNDEFINED_KTYPE), (eir.ADD, eir.UNDEFINED_KTYPE),
                                         (eir.UNDEFINED_KTYPE, eir.UNDEFINED_KTYPE), (eir.ZERO, eir.RELU),
                                         (eir.COPY, eir.RELU), (eir.ZERO, eir.ADD)])
