@@ -184,6 +184,11 @@ def bench_c5(torch, eir, stream, steps, warmup):
     wall, per_eval = time_launches(torch, stream, e.eval_async, steps, warmup)
     res = dict(flops=fx["flops"], wall=wall, per_launch=per_eval, num_ops=e.num_ops())
     e.close()
+    # the same tree replayed as a recorded HIP graph (needs a stream of its own)
+    gs = torch.cuda.Stream()
+    e = host.Expression(expr, sizes, path, tensors, stream=gs)
+    _, res["per_launch_graph"] = time_launches(torch, gs, e.eval_graph_async, steps, warmup)
+    e.close()
     return res
 
 
@@ -273,8 +278,9 @@ def main():
                                                ms_per_eval=round(c5["per_launch"] * 1e3, 3),
                                                frac_fp32_peak=round(gf / (PEAK_FP32_TFLOPS * 1e3), 4),
                                                flops_per_eval=c5["flops"],
+                                               ms_per_eval_graph=round(c5["per_launch_graph"] * 1e3, 3),
                                                path="EinsumExpression, tests/golden/c5_network.json")
-        log(f"c5: {c5['per_launch']*1e3:.3f} ms/eval")
+        log(f"c5: {c5['per_launch']*1e3:.3f} ms/eval, {c5['per_launch_graph']*1e3:.3f} ms/eval as graph replay")
 
     cpu = None
     if not args.no_cpu_baseline and run("c3"):

@@ -222,4 +222,64 @@ int etir_hip_device_count( void ) {
   return l_n;
 }
 
+int etir_hip_stream_create( void ** stream ) {
+  if( stream == nullptr ) return fail( ETIR_UNDEFINED_ERROR, "stream_create: invalid arguments" );
+  *stream = nullptr;
+  hipStream_t l_s = nullptr;
+  ETIR_HIP_CHECK( hipStreamCreateWithFlags( &l_s, hipStreamNonBlocking ) );
+  *stream = l_s;
+  return ETIR_SUCCESS;
+}
+
+int etir_hip_stream_destroy( void * stream ) {
+  if( stream == nullptr ) return ETIR_SUCCESS;
+  ETIR_HIP_CHECK( hipStreamDestroy( reinterpret_cast< hipStream_t >( stream ) ) );
+  return ETIR_SUCCESS;
+}
+
+int etir_hip_graph_begin( void * stream ) {
+  if( stream == nullptr ) return fail( ETIR_UNDEFINED_ERROR, "graph_begin: the null stream cannot be recorded" );
+  ETIR_HIP_CHECK( hipStreamBeginCapture( reinterpret_cast< hipStream_t >( stream ),
+                                         hipStreamCaptureModeThreadLocal ) );
+  return ETIR_SUCCESS;
+}
+
+int etir_hip_graph_end( void * stream, etir_graph_t * graph ) {
+  if( stream == nullptr || graph == nullptr ) return fail( ETIR_UNDEFINED_ERROR, "graph_end: invalid arguments" );
+  *graph = nullptr;
+  hipGraph_t l_g = nullptr;
+  ETIR_HIP_CHECK( hipStreamEndCapture( reinterpret_cast< hipStream_t >( stream ), &l_g ) );
+  hipGraphExec_t l_exec = nullptr;
+  hipError_t l_e = hipGraphInstantiate( &l_exec, l_g, nullptr, nullptr, 0 );
+  (void) hipGraphDestroy( l_g );
+  if( l_e != hipSuccess ) {
+    return fail( ETIR_UNDEFINED_ERROR, std::string( "hipGraphInstantiate failed: " ) + hipGetErrorString( l_e ) );
+  }
+  *graph = reinterpret_cast< etir_graph_t >( l_exec );
+  return ETIR_SUCCESS;
+}
+
+int etir_hip_graph_abort( void * stream ) {
+  if( stream == nullptr ) return ETIR_SUCCESS;
+  hipGraph_t l_g = nullptr;
+  hipError_t l_e = hipStreamEndCapture( reinterpret_cast< hipStream_t >( stream ), &l_g );
+  if( l_g != nullptr ) (void) hipGraphDestroy( l_g );
+  (void) hipGetLastError();
+  return l_e == hipSuccess ? ETIR_SUCCESS
+                           : fail( ETIR_UNDEFINED_ERROR, std::string( "graph_abort: " ) + hipGetErrorString( l_e ) );
+}
+
+int etir_hip_graph_launch( etir_graph_t graph, void * stream ) {
+  if( graph == nullptr ) return fail( ETIR_CALLED_BEFORE_COMPILATION, "graph_launch: no graph" );
+  ETIR_HIP_CHECK( hipGraphLaunch( reinterpret_cast< hipGraphExec_t >( graph ),
+                                  reinterpret_cast< hipStream_t >( stream ) ) );
+  return ETIR_SUCCESS;
+}
+
+int etir_hip_graph_destroy( etir_graph_t graph ) {
+  if( graph == nullptr ) return ETIR_SUCCESS;
+  ETIR_HIP_CHECK( hipGraphExecDestroy( reinterpret_cast< hipGraphExec_t >( graph ) ) );
+  return ETIR_SUCCESS;
+}
+
 }  // extern "C"

@@ -234,6 +234,18 @@ int etir_expression_eval_async( etir_expression_t handle ) {
   return handle->expr.m_nodes.back().eval_async();
 }
 
+int etir_expression_eval_graph( etir_expression_t handle ) {
+  if( handle == nullptr || !handle->expr.m_compiled ) return err_t::CALLED_BEFORE_COMPILATION;
+  err_t l_err = handle->expr.eval_graph_async();
+  if( l_err != err_t::SUCCESS ) return l_err;
+  return etir_hip_synchronize( handle->expr.m_stream ) == ETIR_SUCCESS ? err_t::SUCCESS : err_t::UNDEFINED_ERROR;
+}
+
+int etir_expression_eval_graph_async( etir_expression_t handle ) {
+  if( handle == nullptr || !handle->expr.m_compiled ) return err_t::CALLED_BEFORE_COMPILATION;
+  return handle->expr.eval_graph_async();
+}
+
 int64_t etir_expression_num_ops( etir_expression_t handle ) {
   return handle == nullptr ? 0 : handle->expr.num_ops();
 }

@@ -1,5 +1,6 @@
 // Behaviour follows reference src/frontend/EinsumExpression.cpp:9-367.
 #include "EinsumExpression.h"
+#include "einsum_ir_hip.h"
 #include <algorithm>
 #include <deque>
 #include <set>
@@ -84,6 +85,7 @@ void einsum_ir::frontend::EinsumExpression::init( int64_t                 i_num_
 }
 
 einsum_ir::err_t einsum_ir::frontend::EinsumExpression::compile() {
+  reset_graph();
   if( m_ctype_ext != complex_t::REAL_ONLY ) {
     // complex tensors (BATCH_INNER) need the reference's BLAS backend
     return err_t::INVALID_BACKEND;
@@ -165,17 +167,48 @@ einsum_ir::err_t einsum_ir::frontend::EinsumExpression::compile() {
 einsum_ir::err_t einsum_ir::frontend::EinsumExpression::store_and_lock_data( int64_t i_tensor_id ) {
   if( !m_compiled ) return err_t::CALLED_BEFORE_COMPILATION;
   if( i_tensor_id < 0 || i_tensor_id >= m_num_conts + 1 ) return err_t::INVALID_ID;
+  reset_graph();
   return m_nodes[i_tensor_id].store_and_lock_data();
 }
 
 einsum_ir::err_t einsum_ir::frontend::EinsumExpression::unlock_data( int64_t i_tensor_id ) {
   if( !m_compiled ) return err_t::CALLED_BEFORE_COMPILATION;
   if( i_tensor_id < 0 || i_tensor_id >= m_num_conts + 1 ) return err_t::INVALID_ID;
+  reset_graph();
   return m_nodes[i_tensor_id].unlock_data();
 }
 
 void einsum_ir::frontend::EinsumExpression::eval() {
   m_nodes.back().eval();
+}
+
+einsum_ir::frontend::EinsumExpression::~EinsumExpression() {
+  reset_graph();
+}
+
+void einsum_ir::frontend::EinsumExpression::reset_graph() {
+  if( m_graph != nullptr ) {
+    etir_hip_graph_destroy( static_cast< etir_graph_t >( m_graph ) );
+    m_graph = nullptr;
+  }
+}
+
+einsum_ir::err_t einsum_ir::frontend::EinsumExpression::eval_graph_async() {
+  if( !m_compiled ) return err_t::CALLED_BEFORE_COMPILATION;
+  if( m_stream == nullptr ) return err_t::UNDEFINED_ERROR;
+  if( m_graph == nullptr ) {
+    if( etir_hip_graph_begin( m_stream ) != ETIR_SUCCESS ) return err_t::UNDEFINED_ERROR;
+    err_t l_err = m_nodes.back().eval_async();
+    if( l_err != err_t::SUCCESS ) {
+      etir_hip_graph_abort( m_stream );
+      return l_err;
+    }
+    etir_graph_t l_graph = nullptr;
+    if( etir_hip_graph_end( m_stream, &l_graph ) != ETIR_SUCCESS ) return err_t::UNDEFINED_ERROR;
+    m_graph = l_graph;
+  }
+  return etir_hip_graph_launch( static_cast< etir_graph_t >( m_graph ), m_stream ) == ETIR_SUCCESS
+           ? err_t::SUCCESS : err_t::UNDEFINED_ERROR;
 }
 
 int64_t einsum_ir::frontend::EinsumExpression::num_ops() {

@@ -37,6 +37,13 @@ class einsum_ir::frontend::EinsumExpression {
     backend::MemoryManager m_memory;
     bool m_compiled = false;
     void * m_stream = nullptr;
+    //! recorded evaluation of the tree (etir_graph_t as void*), replayed by eval_graph()
+    void * m_graph = nullptr;
+
+    EinsumExpression() = default;
+    EinsumExpression( EinsumExpression const & ) = delete;
+    EinsumExpression & operator=( EinsumExpression const & ) = delete;
+    ~EinsumExpression();
 
     /** Number of occurrences of each dim id (reference EinsumExpression.cpp:9-23). **/
     static void histogram( int64_t         i_num_dims,
@@ -86,6 +93,18 @@ class einsum_ir::frontend::EinsumExpression {
     err_t unlock_data( int64_t i_tensor_id );
 
     void eval();
+
+    /**
+     * Enqueues one evaluation of the tree as a replay of a HIP graph recorded
+     * from eval's launches (recorded on the first call, and again after
+     * store_and_lock_data / unlock_data changed what eval launches).  The
+     * stream must not be the null stream.  Does not wait.  The results are
+     * those of eval(): the same kernels on the same data in the same order.
+     **/
+    err_t eval_graph_async();
+
+    //! drops the recorded graph (the next eval_graph_async records a new one)
+    void reset_graph();
 
     int64_t num_ops();
 };

@@ -28,6 +28,8 @@ _SIGS = {
                                               ctypes.c_int32, ctypes.POINTER(_vp), _vp, ctypes.POINTER(_vp)]),
     "etir_expression_eval": (ctypes.c_int, [_vp]),
     "etir_expression_eval_async": (ctypes.c_int, [_vp]),
+    "etir_expression_eval_graph": (ctypes.c_int, [_vp]),
+    "etir_expression_eval_graph_async": (ctypes.c_int, [_vp]),
     "etir_expression_num_ops": (ctypes.c_int64, [_vp]),
     "etir_expression_store_and_lock_data": (ctypes.c_int, [_vp, ctypes.c_int64]),
     "etir_expression_unlock_data": (ctypes.c_int, [_vp, ctypes.c_int64]),
@@ -187,6 +189,14 @@ class Expression(_Handle):
 
     def eval_async(self):
         _check(host_lib().etir_expression_eval_async(self._h))
+
+    def eval_graph(self):
+        """eval() as the replay of a recorded HIP graph (needs a stream other
+        than the null stream at construction); waits for the replay."""
+        _check(host_lib().etir_expression_eval_graph(self._h))
+
+    def eval_graph_async(self):
+        _check(host_lib().etir_expression_eval_graph_async(self._h))
 
     def num_ops(self):
         return int(host_lib().etir_expression_num_ops(self._h))

@@ -79,6 +79,14 @@ int etir_expression_create( char const        * expr,
 int etir_expression_eval( etir_expression_t handle );
 /* Enqueues the tree on the stream without waiting. */
 int etir_expression_eval_async( etir_expression_t handle );
+/* The tree's evaluation as a replay of a recorded HIP graph (recorded on the
+ * first call and again after store_and_lock_data / unlock_data); the stream
+ * given at creation must not be NULL.  No counterpart in the reference: it
+ * replaces EinsumNode::eval's per-call launches (reference
+ * src/backend/EinsumNode.cpp:496-540) for repeated evaluations.
+ * _eval_graph waits for the replay, _eval_graph_async does not. */
+int etir_expression_eval_graph( etir_expression_t handle );
+int etir_expression_eval_graph_async( etir_expression_t handle );
 int64_t etir_expression_num_ops( etir_expression_t handle );
 /* EinsumExpression::store_and_lock_data / unlock_data for input tensor `tensor_id`. */
 int etir_expression_store_and_lock_data( etir_expression_t handle, int64_t tensor_id );

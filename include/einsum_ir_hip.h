@@ -191,6 +191,28 @@ int etir_hip_synchronize( void * stream );
 /* Number of visible HIP devices (0 on a machine without a GPU). */
 int etir_hip_device_count( void );
 
+/* Streams and graphs for repeated tree evaluation.  These have no
+ * counterpart in the reference (its EinsumNode::eval, reference
+ * src/backend/EinsumNode.cpp:496-540, calls the backends directly each
+ * time); EinsumExpression::eval_graph records one evaluation of the tree with
+ * them and replays it.
+ *   etir_hip_stream_create   a stream of default priority (non-blocking)
+ *   etir_hip_graph_begin     starts recording the work enqueued on `stream`
+ *                            (thread-local capture; not the null stream)
+ *   etir_hip_graph_end       stops the recording and instantiates it
+ *   etir_hip_graph_abort     stops a recording and discards it
+ *   etir_hip_graph_launch    enqueues one replay on `stream`
+ * A recorded graph holds the kernels' arguments, pointers included, as they
+ * were when it was recorded. */
+typedef struct etir_graph_s * etir_graph_t;
+int etir_hip_stream_create( void ** stream );
+int etir_hip_stream_destroy( void * stream );
+int etir_hip_graph_begin( void * stream );
+int etir_hip_graph_end( void * stream, etir_graph_t * graph );
+int etir_hip_graph_abort( void * stream );
+int etir_hip_graph_launch( etir_graph_t graph, void * stream );
+int etir_hip_graph_destroy( etir_graph_t graph );
+
 #ifdef __cplusplus
 }
 #endif
