@@ -44,7 +44,7 @@ def parse_args():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", default="", help="comma list of configs to run (c1,c2,c3,c4,c5)")
+    p.add_argument("--only", default="", help="comma list of configs to run (c1,c2,c3,c4,c5,mlp)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also time a plain 512 MiB device copy (reference for the PMC byte counters)")
     p.add_argument("--settle", type=float, default=1.0,
@@ -192,6 +192,38 @@ def bench_c5(torch, eir, stream, steps, warmup):
     return res
 
 
+def bench_mlp(torch, eir, stream, steps, warmup):
+    """The reference's bench_mlp tree (src/bench_mlp.cpp:85-307): 784-512-512-
+    512-512-10 MLP on a batch of 18 x 64, built node by node, bias COPY first
+    touch broadcast over the batch, ReLU last touch, weights locked into device
+    copies.  Seeded weights (the reference loads a TorchScript model)."""
+    from einsum_ir_amd import host
+    sizes = {0: 18, 1: 64, 2: 8, 3: 98, 4: 8, 5: 64, 6: 8, 7: 64, 8: 8, 9: 64, 10: 8, 11: 64, 12: 10}
+    aux = {0: 1, 1: 1, 4: 8, 5: 64, 6: 8, 7: 64, 8: 8, 9: 64, 10: 8, 11: 64, 12: 10}
+    ids_w = [[4, 5, 2, 3], [6, 7, 4, 5], [8, 9, 6, 7], [10, 11, 8, 9], [12, 10, 11]]
+    ids_h = [[0, 1, 4, 5], [0, 1, 6, 7], [0, 1, 8, 9], [0, 1, 10, 11], [0, 1, 12]]
+    widths = [784, 512, 512, 512, 512, 10]
+    g = torch.Generator(device="cuda").manual_seed(6)
+    x = torch.randn(1152 * 784, device="cuda", generator=g)
+    ws = [(torch.rand(fo * fi, device="cuda", generator=g) * 2 - 1) / fi ** 0.5 for fi, fo in zip(widths, widths[1:])]
+    bs = [(torch.rand(fo, device="cuda", generator=g) * 2 - 1) / fi ** 0.5 for fi, fo in zip(widths, widths[1:])]
+    out = torch.empty(1152 * 10, device="cuda")
+    nodes = host.Nodes(sizes, aux, stream=stream)
+    prev = nodes.add_leaf([0, 1, 2, 3], x)
+    n_w = [nodes.add_leaf(i, w) for i, w in zip(ids_w, ws)]
+    for layer in range(5):
+        last = eir.RELU if layer < 4 else eir.UNDEFINED_KTYPE
+        prev = nodes.add_binary(ids_h[layer], prev, n_w[layer], tensor=out if layer == 4 else None,
+                                aux=bs[layer], first=eir.COPY, main=eir.MADD, last=last)
+    nodes.compile(prev)
+    for n in n_w:
+        nodes.store_and_lock_data(n)
+    flops = nodes.num_ops()
+    wall, per_eval = time_launches(torch, stream, nodes.eval_async, steps, warmup)
+    nodes.close()
+    return dict(flops=flops, wall=wall, per_launch=per_eval)
+
+
 def cpu_baseline_c3():
     """CPU restatement of the reference algorithm on a bounded sample of config 3:
     one batch (z=1), a=16 of 64 (M = 16*64 = 1024), all of N = 4096 and K = 1024."""
@@ -281,6 +313,17 @@ def main():
                                                ms_per_eval_graph=round(c5["per_launch_graph"] * 1e3, 3),
                                                path="EinsumExpression, tests/golden/c5_network.json")
         log(f"c5: {c5['per_launch']*1e3:.3f} ms/eval, {c5['per_launch_graph']*1e3:.3f} ms/eval as graph replay")
+
+    if run("mlp"):
+        mlp = bench_mlp(torch, eir, stream, max(args.steps, 20), args.warmup)
+        gf = mlp["flops"] / mlp["per_launch"] * 1e-9
+        extra["bench_mlp_bias_relu_fp32"] = dict(value=round(gf, 1), unit="GFLOP/s",
+                                                 us_per_eval=round(mlp["per_launch"] * 1e6, 2),
+                                                 frac_fp32_peak=round(gf / (PEAK_FP32_TFLOPS * 1e3), 4),
+                                                 flops_per_eval=mlp["flops"],
+                                                 path="EinsumNode tree, 5 contractions with bias COPY + ReLU, "
+                                                      "weights locked")
+        log(f"mlp: {mlp['per_launch']*1e6:.1f} us/eval")
 
     cpu = None
     if not args.no_cpu_baseline and run("c3"):

@@ -7,6 +7,7 @@
 #include "frontend/EinsumExpressionAscii.h"
 #include "frontend/EinsumTree.h"
 #include "frontend/EinsumTreeAscii.h"
+#include <deque>
 #include <memory>
 #include <string>
 
@@ -74,6 +75,19 @@ struct etir_tree_s {
   std::map< int64_t, int64_t > sizes;
   std::vector< void * > ptrs;
   frontend::EinsumTree tree;
+};
+
+// EinsumNodes built one by one (reference src/bench_mlp.cpp:85-307): the
+// handle owns the size maps, the dim-id arrays the nodes borrow, the nodes and
+// their memory manager; deque storage keeps every borrowed address stable
+struct etir_nodes_s {
+  std::map< int64_t, int64_t > sizes;
+  std::map< int64_t, int64_t > aux_sizes;
+  std::deque< std::vector< int64_t > > dim_ids;
+  std::deque< backend::EinsumNode > nodes;
+  backend::MemoryManager memory;
+  void * stream = nullptr;
+  int64_t root = -1;
 };
 
 extern "C" {
@@ -312,6 +326,122 @@ int64_t etir_tree_num_ops( etir_tree_t handle ) {
 }
 
 int etir_tree_destroy( etir_tree_t handle ) {
+  delete handle;
+  return err_t::SUCCESS;
+}
+
+int etir_nodes_create( int64_t         num_ids,
+                       int64_t const * ids,
+                       int64_t const * sizes,
+                       int64_t         num_aux_ids,
+                       int64_t const * aux_ids,
+                       int64_t const * aux_sizes,
+                       void          * stream,
+                       etir_nodes_t  * handle ) {
+  if( handle == nullptr ) return err_t::UNDEFINED_ERROR;
+  *handle = nullptr;
+  if( num_ids < 0 || num_aux_ids < 0 || ( num_ids > 0 && ( ids == nullptr || sizes == nullptr ) )
+      || ( num_aux_ids > 0 && ( aux_ids == nullptr || aux_sizes == nullptr ) ) ) {
+    return err_t::COMPILATION_FAILED;
+  }
+  std::unique_ptr< etir_nodes_s > l_h( new etir_nodes_s() );
+  for( int64_t l_i = 0; l_i < num_ids; l_i++ ) l_h->sizes[ ids[l_i] ] = sizes[l_i];
+  for( int64_t l_i = 0; l_i < num_aux_ids; l_i++ ) l_h->aux_sizes[ aux_ids[l_i] ] = aux_sizes[l_i];
+  l_h->stream = stream;
+  *handle = l_h.release();
+  return err_t::SUCCESS;
+}
+
+int etir_nodes_add_leaf( etir_nodes_t    handle,
+                         int64_t         num_dims,
+                         int64_t const * dim_ids,
+                         int32_t         dtype,
+                         void          * data,
+                         int64_t       * node ) {
+  if( handle == nullptr || node == nullptr || num_dims < 0 || ( num_dims > 0 && dim_ids == nullptr ) ) {
+    return err_t::COMPILATION_FAILED;
+  }
+  handle->dim_ids.emplace_back( dim_ids, dim_ids + num_dims );
+  handle->nodes.emplace_back();
+  handle->nodes.back().init( num_dims, handle->dim_ids.back().data(), &handle->sizes, nullptr,
+                             (data_t) dtype, data, &handle->memory );
+  *node = (int64_t) handle->nodes.size() - 1;
+  return err_t::SUCCESS;
+}
+
+int etir_nodes_add_binary( etir_nodes_t    handle,
+                           int64_t         num_dims,
+                           int64_t const * dim_ids,
+                           int32_t         dtype,
+                           void          * aux,
+                           void          * data,
+                           int32_t         ktype_first_touch,
+                           int32_t         ktype_main,
+                           int32_t         ktype_last_touch,
+                           int64_t         left,
+                           int64_t         right,
+                           int64_t       * node ) {
+  if( handle == nullptr || node == nullptr || num_dims < 0 || ( num_dims > 0 && dim_ids == nullptr ) ) {
+    return err_t::COMPILATION_FAILED;
+  }
+  int64_t const l_n = (int64_t) handle->nodes.size();
+  if( left < 0 || left >= l_n || right < 0 || right >= l_n || left == right ) return err_t::INVALID_ID;
+  handle->dim_ids.emplace_back( dim_ids, dim_ids + num_dims );
+  handle->nodes.emplace_back();
+  std::map< int64_t, int64_t > const * l_aux_sizes = ( aux != nullptr && !handle->aux_sizes.empty() )
+                                                       ? &handle->aux_sizes : nullptr;
+  handle->nodes.back().init( num_dims, handle->dim_ids.back().data(), &handle->sizes, l_aux_sizes, nullptr,
+                             nullptr, nullptr, (data_t) dtype, aux, data,
+                             (kernel_t) ktype_first_touch, (kernel_t) ktype_main, (kernel_t) ktype_last_touch,
+                             &handle->nodes[left], &handle->nodes[right], &handle->memory, 1 );
+  *node = l_n;
+  return err_t::SUCCESS;
+}
+
+int etir_nodes_compile( etir_nodes_t handle, int64_t root ) {
+  if( handle == nullptr ) return err_t::CALLED_BEFORE_COMPILATION;
+  if( root < 0 || root >= (int64_t) handle->nodes.size() ) return err_t::INVALID_ID;
+  try {
+    handle->nodes[root].set_stream( handle->stream );
+    err_t l_err = handle->nodes[root].compile();
+    if( l_err != err_t::SUCCESS ) return l_err;
+  }
+  catch( std::exception const & ) {
+    return err_t::COMPILATION_FAILED;
+  }
+  handle->root = root;
+  return err_t::SUCCESS;
+}
+
+int etir_nodes_store_and_lock_data( etir_nodes_t handle, int64_t node ) {
+  if( handle == nullptr || handle->root < 0 ) return err_t::CALLED_BEFORE_COMPILATION;
+  if( node < 0 || node >= (int64_t) handle->nodes.size() ) return err_t::INVALID_ID;
+  return handle->nodes[node].store_and_lock_data();
+}
+
+int etir_nodes_unlock_data( etir_nodes_t handle, int64_t node ) {
+  if( handle == nullptr || handle->root < 0 ) return err_t::CALLED_BEFORE_COMPILATION;
+  if( node < 0 || node >= (int64_t) handle->nodes.size() ) return err_t::INVALID_ID;
+  return handle->nodes[node].unlock_data();
+}
+
+int etir_nodes_eval_async( etir_nodes_t handle ) {
+  if( handle == nullptr || handle->root < 0 ) return err_t::CALLED_BEFORE_COMPILATION;
+  return handle->nodes[ handle->root ].eval_async();
+}
+
+int etir_nodes_eval( etir_nodes_t handle ) {
+  err_t l_err = (err_t) etir_nodes_eval_async( handle );
+  if( l_err != err_t::SUCCESS ) return l_err;
+  return etir_hip_synchronize( handle->stream ) == ETIR_SUCCESS ? err_t::SUCCESS : err_t::UNDEFINED_ERROR;
+}
+
+int64_t etir_nodes_num_ops( etir_nodes_t handle ) {
+  if( handle == nullptr || handle->root < 0 ) return 0;
+  return handle->nodes[ handle->root ].num_ops( true );
+}
+
+int etir_nodes_destroy( etir_nodes_t handle ) {
   delete handle;
   return err_t::SUCCESS;
 }

@@ -41,6 +41,19 @@ _SIGS = {
     "etir_tree_eval": (ctypes.c_int, [_vp]),
     "etir_tree_num_ops": (ctypes.c_int64, [_vp]),
     "etir_tree_destroy": (ctypes.c_int, [_vp]),
+    "etir_nodes_create": (ctypes.c_int, [ctypes.c_int64, _i64p, _i64p, ctypes.c_int64, _i64p, _i64p, _vp,
+                                         ctypes.POINTER(_vp)]),
+    "etir_nodes_add_leaf": (ctypes.c_int, [_vp, ctypes.c_int64, _i64p, ctypes.c_int32, _vp, _i64p]),
+    "etir_nodes_add_binary": (ctypes.c_int, [_vp, ctypes.c_int64, _i64p, ctypes.c_int32, _vp, _vp,
+                                             ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64,
+                                             ctypes.c_int64, _i64p]),
+    "etir_nodes_compile": (ctypes.c_int, [_vp, ctypes.c_int64]),
+    "etir_nodes_store_and_lock_data": (ctypes.c_int, [_vp, ctypes.c_int64]),
+    "etir_nodes_unlock_data": (ctypes.c_int, [_vp, ctypes.c_int64]),
+    "etir_nodes_eval": (ctypes.c_int, [_vp]),
+    "etir_nodes_eval_async": (ctypes.c_int, [_vp]),
+    "etir_nodes_num_ops": (ctypes.c_int64, [_vp]),
+    "etir_nodes_destroy": (ctypes.c_int, [_vp]),
 }
 
 
@@ -233,3 +246,56 @@ class Tree(_Handle):
 
     def num_ops(self):
         return int(host_lib().etir_tree_num_ops(self._h))
+
+
+class Nodes(_Handle):
+    """EinsumNode tree built node by node (the reference's bench_mlp way).
+
+    sizes: {dim_id: size}; aux_sizes: {dim_id: outer size of the auxiliary
+    tensors} (1 for the dims a bias broadcasts over).  add_leaf/add_binary
+    return node ids; tensors are device tensors (or raw pointers), None for
+    intermediates."""
+    _destroy = "etir_nodes_destroy"
+
+    def __init__(self, sizes, aux_sizes=None, stream=None):
+        super().__init__()
+        ids = sorted(sizes)
+        aux = sorted(aux_sizes or {})
+        self._keep = []
+        _check(host_lib().etir_nodes_create(len(ids), _lib.i64_array(ids), _lib.i64_array([sizes[i] for i in ids]),
+                                            len(aux), _lib.i64_array(aux),
+                                            _lib.i64_array([aux_sizes[i] for i in aux]) if aux else None,
+                                            _stream(stream), ctypes.byref(self._h)))
+
+    def add_leaf(self, dim_ids, tensor, dtype=_lib.FP32):
+        node = ctypes.c_int64()
+        self._keep.append(tensor)
+        _check(host_lib().etir_nodes_add_leaf(self._h, len(dim_ids), _lib.i64_array(dim_ids), dtype, _ptr(tensor),
+                                              ctypes.byref(node)))
+        return node.value
+
+    def add_binary(self, dim_ids, left, right, tensor=None, aux=None, first=_lib.ZERO, main=_lib.MADD,
+                   last=_lib.UNDEFINED_KTYPE, dtype=_lib.FP32):
+        node = ctypes.c_int64()
+        self._keep.extend([tensor, aux])
+        _check(host_lib().etir_nodes_add_binary(self._h, len(dim_ids), _lib.i64_array(dim_ids), dtype, _ptr(aux),
+                                                _ptr(tensor), first, main, last, left, right, ctypes.byref(node)))
+        return node.value
+
+    def compile(self, root):
+        _check(host_lib().etir_nodes_compile(self._h, root))
+
+    def store_and_lock_data(self, node):
+        _check(host_lib().etir_nodes_store_and_lock_data(self._h, node))
+
+    def unlock_data(self, node):
+        _check(host_lib().etir_nodes_unlock_data(self._h, node))
+
+    def eval(self):
+        _check(host_lib().etir_nodes_eval(self._h))
+
+    def eval_async(self):
+        _check(host_lib().etir_nodes_eval_async(self._h))
+
+    def num_ops(self):
+        return int(host_lib().etir_nodes_num_ops(self._h))

@@ -29,6 +29,7 @@ typedef struct etir_binary_s     * etir_binary_t;
 typedef struct etir_unary_s      * etir_unary_t;
 typedef struct etir_expression_s * etir_expression_t;
 typedef struct etir_tree_s       * etir_tree_t;
+typedef struct etir_nodes_s      * etir_nodes_t;
 
 /* BinaryContraction (reference src/backend/BinaryContraction.h:279-391)
  * through BinaryContractionHip: `expr` is "abkl,cdkl->abcd" or the bracketed
@@ -104,6 +105,36 @@ int etir_tree_create( char const * tree, char const * dim_sizes, int32_t dtype,
 int etir_tree_eval( etir_tree_t handle );
 int64_t etir_tree_num_ops( etir_tree_t handle );
 int etir_tree_destroy( etir_tree_t handle );
+
+/* EinsumNode trees built node by node, as the reference's bench_mlp does
+ * (reference src/bench_mlp.cpp:85-307 with EinsumNode's init overloads,
+ * src/backend/EinsumNode.h:141-216).  One handle owns the dim-size map
+ * (`ids[i]` has size `sizes[i]`), the auxiliary tensors' outer sizes
+ * (`aux_ids`/`aux_sizes`, e.g. 1 for the batch dims a bias broadcasts over),
+ * the nodes, their MemoryManager and the stream (NULL = null stream).
+ * Nodes are numbered in the order they are added. */
+int etir_nodes_create( int64_t num_ids, int64_t const * ids, int64_t const * sizes,
+                       int64_t num_aux_ids, int64_t const * aux_ids, int64_t const * aux_sizes,
+                       void * stream, etir_nodes_t * handle );
+/* leaf: EinsumNode::init( num_dims, dim_ids, sizes, NULL, dtype, data, memory ) */
+int etir_nodes_add_leaf( etir_nodes_t handle, int64_t num_dims, int64_t const * dim_ids,
+                         int32_t dtype, void * data, int64_t * node );
+/* binary contraction node: EinsumNode::init( num_dims, dim_ids, sizes,
+ * aux ? aux sizes : NULL, NULL, NULL, NULL, dtype, aux, data, first, main,
+ * last, left, right, memory, 1 ); data NULL = intermediate in the arena. */
+int etir_nodes_add_binary( etir_nodes_t handle, int64_t num_dims, int64_t const * dim_ids,
+                           int32_t dtype, void * aux, void * data,
+                           int32_t ktype_first_touch, int32_t ktype_main, int32_t ktype_last_touch,
+                           int64_t left, int64_t right, int64_t * node );
+/* EinsumNode::compile of the root (the whole tree below it). */
+int etir_nodes_compile( etir_nodes_t handle, int64_t root );
+int etir_nodes_store_and_lock_data( etir_nodes_t handle, int64_t node );
+int etir_nodes_unlock_data( etir_nodes_t handle, int64_t node );
+/* EinsumNode::eval of the compiled root: _eval waits, _eval_async does not. */
+int etir_nodes_eval( etir_nodes_t handle );
+int etir_nodes_eval_async( etir_nodes_t handle );
+int64_t etir_nodes_num_ops( etir_nodes_t handle );
+int etir_nodes_destroy( etir_nodes_t handle );
 
 #ifdef __cplusplus
 }
