@@ -1,0 +1,505 @@
+"""etops-compatible tensor operations on the HIP backend.
+
+Mirrors the reference's Python module ``etops`` (reference
+python/src/etops/__init__.py:1-532, python/src/bindings.cpp:10-334,
+python/src/TensorOperation.{h,cpp}): the same enums and names,
+``TensorOperationConfig`` with the same fields, validation, JSON form and
+file I/O, ``TensorOperation.setup/execute``, ``optimize`` and
+``backend.<name>.get_default_optimization_config``.  The backend is ``"hip"``
+(``None`` selects it); the loop IR a config describes goes unchanged to the
+C ABI of libeinsum_ir_hip.so (``etir_hip_contraction_create`` /
+``etir_hip_permute_create``), which plans and runs it on the GPU.
+
+Tensors: ``execute`` takes device arrays -- torch tensors on the GPU, objects
+with ``__cuda_array_interface__`` or ``__dlpack__``, or raw device pointers
+(int) -- and, like the reference, host numpy arrays, which are staged through
+device buffers (copy in, run, copy back; a convenience, not a fast path).
+``execute`` is synchronous like the reference's; ``execute_async`` enqueues on
+a stream and returns.
+
+Differences from the tpp backend, by design:
+  * exec_types are validated and kept but do not steer execution: every loop
+    of the operation is run by one kernel grid (the planner fuses loops and
+    picks tiles itself);
+  * level-1 (packing) strides are accepted and ignored: the kernels stage
+    tiles through LDS instead of packing buffers;
+  * ``optimize`` returns the configuration with the same loops (nothing to
+    hand back: the GPU planner's choices live in the compiled plan) and every
+    exec type ``prim``; tpp's optimisation keys are accepted (and have no
+    effect), unknown keys are rejected as in the reference;
+  * DataType has the additive member ``bfloat16`` (bf16 tensors, fp32
+    accumulation); ``float64`` contractions are not provided by the HIP
+    kernels (``setup`` reports ``compilation_failed``), float64 permutations
+    are.
+"""
+import ctypes
+import enum
+import json
+from dataclasses import dataclass
+from typing import Dict, Optional, Sequence, Union
+
+from . import _lib
+from ._lib import check, hip_lib
+
+
+class ErrorType(enum.IntEnum):
+    """TensorOperation::error_t (reference python/src/TensorOperation.h:74-80)."""
+    success = 0
+    compilation_failed = 1
+    invalid_stride_shape = 2
+    invalid_optimization_config = 3
+
+
+class DataType(enum.IntEnum):
+    """TensorOperation::dtype_t (:68-72); bfloat16 is additive."""
+    float32 = 0
+    float64 = 1
+    bfloat16 = 2
+
+
+class PrimType(enum.IntEnum):
+    """TensorOperation::prim_t (:47-56)."""
+    none = 0
+    zero = 1
+    copy = 2
+    relu = 3
+    gemm = 4
+    brgemm = 5
+
+
+class ExecType(enum.IntEnum):
+    """TensorOperation::exec_t (:39-45)."""
+    seq = 0
+    prim = 1
+    shared = 2
+    sfc = 3
+
+
+class DimType(enum.IntEnum):
+    """TensorOperation::dim_t (:58-65)."""
+    c = 0
+    m = 1
+    n = 2
+    k = 3
+
+
+dtype = DataType
+float32 = DataType.float32
+float64 = DataType.float64
+bfloat16 = DataType.bfloat16
+
+
+class prim:
+    """Namespace for primitive types used in tensor operations."""
+    none = PrimType.none
+    zero = PrimType.zero
+    relu = PrimType.relu
+    copy = PrimType.copy
+    gemm = PrimType.gemm
+    brgemm = PrimType.brgemm
+    __all__ = ["none", "zero", "relu", "copy", "gemm", "brgemm"]
+
+
+class etype:
+    """Namespace for execution types used in tensor operations."""
+    prim = ExecType.prim
+    seq = ExecType.seq
+    shared = ExecType.shared
+    sfc = ExecType.sfc
+    __all__ = ["prim", "seq", "shared", "sfc"]
+
+
+exec = etype  # noqa: A001  (the reference exports this name too)
+
+
+class dim:
+    """Namespace for dimension types used in tensor operations."""
+    c = DimType.c
+    m = DimType.m
+    n = DimType.n
+    k = DimType.k
+    __all__ = ["c", "m", "n", "k"]
+
+
+BACKENDS = ("hip",)
+_BINARY = (PrimType.gemm, PrimType.brgemm)
+_UNARY = (PrimType.copy, PrimType.zero)
+# the tpp backend's optimisation keys (reference bindings.cpp:174-178)
+_OPT_KEYS = ("target_m", "target_n", "target_k", "num_threads", "packed_gemm_support",
+             "br_gemm_support", "packing_support", "sfc_support", "l2_cache_size")
+
+
+def _op_kind(prim_main):
+    if prim_main in _BINARY:
+        return "binary"
+    if prim_main in _UNARY:
+        return "unary"
+    return None
+
+
+@dataclass(frozen=True)
+class TensorOperationConfig:
+    """Configuration of one tensor operation (reference etops/__init__.py:116-268).
+
+    strides has shape [LEVEL][TENSOR][DIMENSION]: level 0 the tensors' own
+    strides (binary: in0, in1, out; unary: in, out), further levels packing
+    strides (accepted, unused by the GPU kernels)."""
+    data_type: DataType
+    prim_first: PrimType
+    prim_main: PrimType
+    prim_last: PrimType
+    dim_types: Sequence[DimType]
+    exec_types: Sequence[ExecType]
+    dim_sizes: Sequence[int]
+    strides: Sequence[Sequence[Sequence[int]]]
+    backend: Optional[str] = None
+
+    def __post_init__(self):
+        if self.backend is not None and self.backend not in BACKENDS:
+            raise ValueError(f"Unsupported backend: '{self.backend}'. This build provides only 'hip'.")
+        kind = _op_kind(self.prim_main)
+        if kind is None:
+            raise ValueError(f"Invalid prim_main: {self.prim_main}. "
+                             "Must be gemm/brgemm (binary) or copy/zero (unary).")
+        num_dims = len(self.dim_types)
+        if len(self.exec_types) != num_dims:
+            raise ValueError(f"exec_types length ({len(self.exec_types)}) must match "
+                             f"dim_types length ({num_dims}).")
+        if len(self.dim_sizes) != num_dims:
+            raise ValueError(f"dim_sizes length ({len(self.dim_sizes)}) must match "
+                             f"dim_types length ({num_dims}).")
+        for i, size in enumerate(self.dim_sizes):
+            if size <= 0:
+                raise ValueError(f"dim_sizes[{i}] must be positive, got {size}.")
+        if len(self.strides) == 0:
+            raise ValueError("strides must have at least one level (level 0).")
+        names = ["in0", "in1", "out"] if kind == "binary" else ["in", "out"]
+        if len(self.strides[0]) != len(names):
+            raise ValueError(f"strides[0] must have {len(names)} tensors ({', '.join(names)}), "
+                             f"got {len(self.strides[0])}.")
+        for t, st in enumerate(self.strides[0]):
+            if len(st) != num_dims:
+                raise ValueError(f"strides[0][{t}] ({names[t]}) length ({len(st)}) must match "
+                                 f"number of dimensions ({num_dims}).")
+        if kind == "unary":
+            for i, dt in enumerate(self.dim_types):
+                if dt != DimType.c:
+                    raise ValueError("For unary operations, all dim_types must be etops.dim.c. "
+                                     f"dim_types[{i}] is {dt}.")
+            if self.prim_first != PrimType.none:
+                raise ValueError(f"For unary operations, prim_first must be etops.prim.none, got {self.prim_first}.")
+            if self.prim_last != PrimType.none:
+                raise ValueError(f"For unary operations, prim_last must be etops.prim.none, got {self.prim_last}.")
+        else:
+            if self.prim_first not in (PrimType.none, PrimType.zero):
+                raise ValueError("For binary contractions, prim_first must be etops.prim.none or "
+                                 f"etops.prim.zero, got {self.prim_first}.")
+            if self.prim_last not in (PrimType.none, PrimType.relu):
+                raise ValueError("For binary contractions, prim_last must be etops.prim.none or "
+                                 f"etops.prim.relu, got {self.prim_last}.")
+
+    def apply(self, op: "TensorOperation") -> None:
+        err = op.setup(self.backend if self.backend is not None else "hip", self.data_type, self.prim_first,
+                       self.prim_main, self.prim_last, tuple(self.dim_types), tuple(self.exec_types),
+                       tuple(self.dim_sizes),
+                       tuple(tuple(tuple(t) for t in level) for level in self.strides))
+        if err != ErrorType.success:
+            raise RuntimeError(f"einsum_ir TensorOperation setup failed: ErrorType.{ErrorType(err).name}")
+
+    def to_json(self, indent: Optional[int] = None) -> str:
+        data = {
+            "data_type": self.data_type.name,
+            "prim_first": self.prim_first.name,
+            "prim_main": self.prim_main.name,
+            "prim_last": self.prim_last.name,
+            "dim_types": [d.name for d in self.dim_types],
+            "exec_types": [e.name for e in self.exec_types],
+            "dim_sizes": list(self.dim_sizes),
+            "strides": [[list(t) for t in level] for level in self.strides],
+        }
+        if self.backend is not None:
+            data["backend"] = self.backend
+        return json.dumps(data, indent=indent)
+
+    @classmethod
+    def from_json(cls, json_str: str) -> "TensorOperationConfig":
+        data = json.loads(json_str)
+        required = ["data_type", "prim_first", "prim_main", "prim_last",
+                    "dim_types", "exec_types", "dim_sizes", "strides"]
+        missing = [f for f in required if f not in data]
+        if missing:
+            raise ValueError(f"Missing required fields: {missing}")
+
+        def get_enum(enum_type, name):
+            try:
+                return enum_type[name]
+            except KeyError:
+                raise ValueError(f"Invalid {enum_type.__name__} value: '{name}'") from None
+
+        return cls(data_type=get_enum(DataType, data["data_type"]),
+                   prim_first=get_enum(PrimType, data["prim_first"]),
+                   prim_main=get_enum(PrimType, data["prim_main"]),
+                   prim_last=get_enum(PrimType, data["prim_last"]),
+                   dim_types=tuple(get_enum(DimType, d) for d in data["dim_types"]),
+                   exec_types=tuple(get_enum(ExecType, e) for e in data["exec_types"]),
+                   dim_sizes=tuple(data["dim_sizes"]),
+                   strides=tuple(tuple(tuple(t) for t in level) for level in data["strides"]),
+                   backend=data.get("backend"))
+
+    def save(self, path: str, indent: Optional[int] = 2) -> None:
+        with open(path, "w") as f:
+            f.write(self.to_json(indent=indent))
+
+    @classmethod
+    def load(cls, path: str) -> "TensorOperationConfig":
+        with open(path) as f:
+            return cls.from_json(f.read())
+
+
+# ---------------------------------------------------------------------------
+# tensors: device arrays, raw pointers, host numpy arrays (staged)
+# ---------------------------------------------------------------------------
+_NP_DTYPE = {DataType.float32: "float32", DataType.float64: "float64", DataType.bfloat16: None}
+
+
+def _device_pointer(x):
+    """Device address of a device array, or None when x is a host array."""
+    if x is None:
+        return 0
+    if isinstance(x, int):
+        return x
+    try:
+        import torch
+        if isinstance(x, torch.Tensor):
+            if not x.is_cuda:
+                raise TypeError("etops (hip): torch tensors must live on the GPU")
+            return x.data_ptr()
+    except ImportError:
+        pass
+    iface = getattr(x, "__cuda_array_interface__", None)
+    if iface is not None:
+        return int(iface["data"][0])
+    if hasattr(x, "__dlpack__") and hasattr(x, "__dlpack_device__"):
+        dev_type, _ = x.__dlpack_device__()
+        if dev_type in (2, 10):          # kDLCUDA, kDLROCM
+            import torch
+            return torch.from_dlpack(x).data_ptr()
+    return None
+
+
+class _Staged:
+    """A host numpy array copied into a device buffer for one execute."""
+
+    def __init__(self, array, np_dtype, writable):
+        import numpy as np
+        if writable:
+            if not (isinstance(array, np.ndarray) and array.dtype == np_dtype and array.flags.c_contiguous
+                    and array.flags.writeable):
+                raise TypeError(f"etops (hip): the output must be a writable C-contiguous {np_dtype} array")
+            self.host = array
+        else:
+            self.host = np.ascontiguousarray(array, dtype=np_dtype)
+        self.nbytes = self.host.nbytes
+        self.dev = ctypes.c_void_p()
+        check(hip_lib().etir_hip_malloc(ctypes.byref(self.dev), self.nbytes))
+        check(hip_lib().etir_hip_memcpy_h2d(self.dev, self.host.ctypes.data, self.nbytes))
+
+    def copy_back(self):
+        check(hip_lib().etir_hip_memcpy_d2h(self.host.ctypes.data, self.dev, self.nbytes))
+
+    def free(self):
+        if self.dev:
+            hip_lib().etir_hip_free(self.dev)
+            self.dev = ctypes.c_void_p()
+
+
+# ---------------------------------------------------------------------------
+# TensorOperation
+# ---------------------------------------------------------------------------
+_KT_FIRST = {PrimType.none: _lib.UNDEFINED_KTYPE, PrimType.zero: _lib.ZERO}
+_KT_LAST = {PrimType.none: _lib.UNDEFINED_KTYPE, PrimType.relu: _lib.RELU}
+_DT = {DataType.float32: (_lib.FP32, _lib.FP32, _lib.FP32, _lib.FP32),
+       DataType.float64: (_lib.FP64, _lib.FP64, _lib.FP64, _lib.FP64),
+       DataType.bfloat16: (_lib.BF16, _lib.BF16, _lib.FP32, _lib.BF16)}
+
+
+class TensorOperation:
+    """One unary or binary tensor operation compiled for the GPU
+    (reference python/src/TensorOperation.cpp:220-479)."""
+
+    def __init__(self, config: Union[TensorOperationConfig, None] = None):
+        self._plan = None
+        self._kind = None
+        self._dtype = None
+        if config is not None:
+            config.apply(self)
+
+    def close(self):
+        if self._plan is not None:
+            self._plan.close()
+            self._plan = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def setup(self, backend, dtype, prim_first, prim_main, prim_last, dim_types, exec_types, dim_sizes,
+              strides) -> ErrorType:
+        """TensorOperation::setup (reference TensorOperation.cpp:220-289)."""
+        self.close()
+        if backend is not None and backend not in BACKENDS:
+            return ErrorType.compilation_failed
+        kind = _op_kind(PrimType(prim_main))
+        if kind is None:
+            return ErrorType.compilation_failed
+        n = len(dim_sizes)
+        if len(strides) == 0 or len(strides[0]) != (3 if kind == "binary" else 2):
+            return ErrorType.invalid_stride_shape
+        if any(len(t) != n for t in strides[0]):
+            return ErrorType.invalid_stride_shape
+        if len(dim_types) != n or len(exec_types) != n:
+            return ErrorType.compilation_failed
+        dtype = DataType(dtype)
+        try:
+            if kind == "binary":
+                if PrimType(prim_first) not in _KT_FIRST or PrimType(prim_last) not in _KT_LAST:
+                    return ErrorType.compilation_failed
+                dl, dr, dc, do = _DT[dtype]
+                from . import ContractionPlan
+                self._plan = ContractionPlan([int(DimType(d)) for d in dim_types], list(dim_sizes),
+                                             list(strides[0][0]), list(strides[0][1]), list(strides[0][2]),
+                                             dtype_left=dl, dtype_right=dr, dtype_comp=dc, dtype_out=do,
+                                             ktype_first_touch=_KT_FIRST[PrimType(prim_first)],
+                                             ktype_main=_lib.MADD,
+                                             ktype_last_touch=_KT_LAST[PrimType(prim_last)])
+            else:
+                if PrimType(prim_first) != PrimType.none or PrimType(prim_last) != PrimType.none:
+                    return ErrorType.compilation_failed
+                # dims in output order (descending output stride), input strides alongside
+                order = sorted(range(n), key=lambda i: -strides[0][1][i])
+                from . import PermutePlan
+                kt = _lib.COPY if PrimType(prim_main) == PrimType.copy else _lib.ZERO
+                self._plan = PermutePlan([dim_sizes[i] for i in order], [strides[0][0][i] for i in order],
+                                         [strides[0][1][i] for i in order], dtype=_DT[dtype][0], ktype=kt)
+        except _lib.EinsumIrError:
+            self._plan = None
+            return ErrorType.compilation_failed
+        self._kind = kind
+        self._dtype = dtype
+        self._extent = self._extents(dim_sizes, strides[0])
+        return ErrorType.success
+
+    @staticmethod
+    def _extents(sizes, level0):
+        """Elements spanned by each tensor (largest offset + 1)."""
+        return [1 + sum((s - 1) * abs(st) for s, st in zip(sizes, t)) for t in level0]
+
+    def describe(self) -> str:
+        """The GPU plan's kernel choice (tile, fused loops, load modes)."""
+        return self._plan.describe() if self._plan is not None else ""
+
+    def execute_async(self, in0, in1, out, stream=None) -> None:
+        """Enqueues the operation on `stream` (device arrays / pointers only)."""
+        if self._plan is None:
+            raise RuntimeError("einsum_ir TensorOperation: execute before a successful setup")
+        ptrs = [_device_pointer(x) for x in (in0, in1, out)]
+        if any(p is None for p in ptrs):
+            raise TypeError("etops (hip): execute_async takes device arrays or device pointers")
+        self._launch(*ptrs, stream)
+
+    def _launch(self, p0, p1, pout, stream):
+        if self._kind == "binary":
+            self._plan.execute(p0, p1, pout, stream=stream)
+        else:
+            self._plan.execute(p0, pout, stream=stream)
+
+    def execute(self, in0, in1=None, out=None) -> None:
+        """TensorOperation::execute (reference TensorOperation.cpp:459-468): runs
+        the operation and waits for it.  Device arrays run in place; host
+        numpy arrays are staged through device buffers."""
+        if out is None:
+            raise TypeError("etops: execute needs an output tensor")
+        if self._plan is None:
+            raise RuntimeError("einsum_ir TensorOperation: execute before a successful setup")
+        args = [in0, in1 if self._kind == "binary" else None, out]
+        ptrs = [_device_pointer(x) for x in args]
+        staged = []
+        try:
+            np_dtype = _NP_DTYPE[self._dtype]
+            extents = self._extent if self._kind == "binary" else [self._extent[0], 0, self._extent[1]]
+            for i, (x, p) in enumerate(zip(args, ptrs)):
+                if p is not None:
+                    continue
+                if np_dtype is None:
+                    raise TypeError("etops (hip): bfloat16 operations take device arrays only")
+                st = _Staged(x, np_dtype, writable=(i == 2))
+                if st.host.size < extents[i]:
+                    raise ValueError(f"etops: tensor {i} holds {st.host.size} elements, the strides "
+                                     f"address {extents[i]}")
+                staged.append((i, st))
+                ptrs[i] = st.dev.value
+            self._launch(ptrs[0], ptrs[1], ptrs[2], None)
+            check(hip_lib().etir_hip_synchronize(None))
+            for i, st in staged:
+                if i == 2:
+                    st.copy_back()
+        finally:
+            for _, st in staged:
+                st.free()
+
+    @staticmethod
+    def get_default_optimization_config(backend: str = "hip") -> Dict[str, Union[int, bool]]:
+        if backend not in BACKENDS:
+            return {}
+        # tpp's keys with the GPU kernels' own figures: the largest tile and
+        # K step, all threads of the device (0 = auto), no packing/SFC/BRGEMM
+        # distinction (the planner decides per plan), the L2 of one XCD
+        return {"target_m": 256, "target_n": 256, "target_k": 32, "num_threads": 0,
+                "packed_gemm_support": False, "br_gemm_support": True, "packing_support": False,
+                "sfc_support": False, "l2_cache_size": 4 * 1024 * 1024}
+
+
+class _HIPBackend:
+    """HIP (MI355X, gfx950) backend for tensor operations."""
+    name: str = "hip"
+
+    @staticmethod
+    def get_default_optimization_config() -> Dict[str, Union[int, bool]]:
+        return TensorOperation.get_default_optimization_config("hip")
+
+
+class backend:
+    """Namespace for available backends."""
+    hip = _HIPBackend()
+
+
+def optimize(config: TensorOperationConfig,
+             optimization_config: Optional[Dict[str, Union[int, bool]]] = None) -> TensorOperationConfig:
+    """Optimizes a configuration (reference etops/__init__.py:436-514,
+    TensorOperation.cpp:486-604).  On the HIP backend the loops are returned
+    as given with every exec type ``prim``: the whole operation is one kernel
+    grid and the planner chooses fusion and tiles when the operation is set
+    up.  Keys other than the tpp backend's raise like the reference's."""
+    actual = config.backend if config.backend is not None else "hip"
+    if actual not in BACKENDS:
+        raise ValueError(f"Unknown backend: {actual}")
+    if optimization_config is None:
+        optimization_config = backend.hip.get_default_optimization_config()
+    for key, value in optimization_config.items():
+        if key not in _OPT_KEYS:
+            raise RuntimeError("einsum_ir optimization failed: ErrorType.invalid_optimization_config")
+        if not isinstance(value, (int, bool)):
+            raise RuntimeError("einsum_ir optimization failed: ErrorType.invalid_optimization_config")
+    return TensorOperationConfig(backend=actual, data_type=config.data_type, prim_first=config.prim_first,
+                                 prim_main=config.prim_main, prim_last=config.prim_last,
+                                 dim_types=tuple(config.dim_types),
+                                 exec_types=tuple(ExecType.prim for _ in config.dim_types),
+                                 dim_sizes=tuple(config.dim_sizes),
+                                 strides=(tuple(tuple(t) for t in config.strides[0]),))
+
+
+__all__ = ["TensorOperation", "TensorOperationConfig", "DataType", "PrimType", "ExecType", "DimType",
+           "ErrorType", "dtype", "float32", "float64", "bfloat16", "prim", "etype", "exec", "dim", "backend",
+           "optimize"]
