@@ -62,14 +62,18 @@ __device__ inline uint16_t f32_to_bf16_rne( float f ) {
 template< int DT > struct InType;
 template<> struct InType< ETIR_FP32 > { typedef float    T; };
 template<> struct InType< ETIR_BF16 > { typedef uint16_t T; };
+template<> struct InType< ETIR_FP64 > { typedef double   T; };
 
 // Pitch (elements) of the [k][row] LDS layout.  bf16: 2*PK = 64 (mod 256) so
 // the four k rows of one transpose read land in disjoint bank ranges; fp32:
-// 4*PK = 32 (mod 64) so rows k and k+4 (the two lane groups) do not collide.
+// 4*PK = 32 (mod 64) so rows k and k+4 (the two lane groups) do not collide;
+// fp64: 8*PK = 128 (mod 256) so the two k rows (16 lanes x 8 bytes each) read
+// by one half-wave cover all 64 banks once.
 template< int R, int ESZ >
 struct KmPitch {
   static constexpr int bytes_raw = R * ESZ;
   static constexpr int pad = ( ESZ == 2 ) ? ( ( 64 - bytes_raw % 256 + 256 ) % 256 )
+                           : ( ESZ == 8 ) ? ( ( 128 - bytes_raw % 256 + 256 ) % 256 )
                                           : ( ( 32 - bytes_raw % 64 + 64 ) % 64 );
   static constexpr int value = ( bytes_raw + pad ) / ESZ;
 };

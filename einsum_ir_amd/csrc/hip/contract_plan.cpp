@@ -36,6 +36,8 @@ int launch_contract_f32_128x128( int32_t ma, int32_t mb, bool kaff, ContractArgs
                                  uint32_t grid, hipStream_t stream );
 int launch_contract_f32_64x64( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
                                uint32_t grid, hipStream_t stream );
+int launch_contract_f64_64x64( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
+                               uint32_t grid, hipStream_t stream );
 int launch_contract_bf16_256x256( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
                                   uint32_t grid, hipStream_t stream );
 int launch_contract_bf16_256x128( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
@@ -153,6 +155,7 @@ char const * tile_str( int32_t t ) {
     case TILE_BF16_DMA_256x128: return "bf16_dma_256x128";
     case TILE_BF16_128x128: return "bf16_128x128x64";
     case TILE_BF16_64x64:   return "bf16_64x64x64";
+    case TILE_F64_64x64:    return "f64_64x64x16";
     default:                return "?";
   }
 }
@@ -198,10 +201,9 @@ int plan_contraction_impl( int64_t            num_loops,
   bool const l_bf16 = dtype_left == ETIR_BF16 && dtype_right == ETIR_BF16
                    && dtype_comp == ETIR_FP32
                    && ( dtype_out == ETIR_FP32 || dtype_out == ETIR_BF16 );
-  if( dtype_left == ETIR_FP64 || dtype_right == ETIR_FP64 || dtype_out == ETIR_FP64 ) {
-    return fail( ETIR_COMPILATION_FAILED, "contraction: FP64 is not supported by the HIP backend" );
-  }
-  if( !l_f32 && !l_bf16 ) {
+  bool const l_f64  = dtype_left == ETIR_FP64 && dtype_right == ETIR_FP64
+                   && dtype_comp == ETIR_FP64 && dtype_out == ETIR_FP64;
+  if( !l_f32 && !l_bf16 && !l_f64 ) {
     return fail( ETIR_INVALID_DTYPE, "contraction: unsupported dtype combination" );
   }
   if( ktype_main != ETIR_KTYPE_MADD ) {
@@ -276,7 +278,7 @@ int plan_contraction_impl( int64_t            num_loops,
   int64_t const l_kern_m = l_swap ? l_size_n : l_size_m;
   int64_t const l_kern_n = l_swap ? l_size_m : l_size_n;
 
-  int64_t const l_esz = ( dtype_left == ETIR_BF16 ) ? 2 : 4;
+  int64_t const l_esz = ( dtype_left == ETIR_BF16 ) ? 2 : ( dtype_left == ETIR_FP64 ? 8 : 4 );
   int64_t const l_vk  = 16 / l_esz;   // elements per 16-byte vector
 
   // ordering
@@ -370,7 +372,10 @@ int plan_contraction_impl( int64_t            num_loops,
     double const l_util = l_pad > 0.0 ? double( l_kern_m ) * double( l_kern_n ) / l_pad : 1.0;
     return l_util * std::min( 1.0, double( n_tiles( t ) ) / double( l_cus ) );
   };
-  if( l_f32 ) {
+  if( l_f64 ) {
+    plan.tile = TILE_F64_64x64;
+  }
+  else if( l_f32 ) {
     // the larger tile unless the smaller one wastes clearly less
     plan.tile = ( score( TILE_F32_128x128 ) >= 0.95 * score( TILE_F32_64x64 ) ) ? TILE_F32_128x128 : TILE_F32_64x64;
   }
@@ -397,7 +402,7 @@ int plan_contraction_impl( int64_t            num_loops,
       && 2 * int64_t( 64 ) * std::max( l_sk_a, l_sk_b ) * ( ( l_size_k + 63 ) / 64 + 4 ) < ( int64_t( 1 ) << 31 );
   plan.tile_fallback = plan.tile;
   if( l_dma_ok && n_tiles( TILE_BF16_DMA_256x256 ) >= l_cus ) plan.tile = TILE_BF16_DMA_256x256;
-  if( char const * l_env = std::getenv( "ETIR_TILE" ) ) {
+  if( char const * l_env = l_f64 ? nullptr : std::getenv( "ETIR_TILE" ) ) {
     // diagnostic override of the tile heuristic (must match the dtype)
     int32_t l_t = std::atoi( l_env );
     bool const l_t_f32 = ( l_t == TILE_F32_128x128 || l_t == TILE_F32_64x64 );
@@ -423,7 +428,7 @@ int plan_contraction_impl( int64_t            num_loops,
   // node with M = 64, N = 1024, K = 32768).  Then the outermost K loops (one
   // of them factored if needed) become C loops of a partial contraction that
   // writes one workspace slice per split, and split_reduce sums the slices.
-  if( allow_split && l_size_k >= 512 ) {
+  if( allow_split && !l_f64 && l_size_k >= 512 ) {
     int64_t const l_tiles = n_tiles( plan.tile );
     if( l_tiles > 0 && l_tiles < l_cus ) {
       // at least 128 k per split; aim for two workgroups per CU
@@ -531,7 +536,7 @@ int plan_contraction_impl( int64_t            num_loops,
   plan.N = l_kern_n;
   plan.K = l_size_k;
   plan.flops = 2 * l_size_c * l_size_m * l_size_n * l_size_k;
-  int64_t const l_esz_out = ( dtype_out == ETIR_BF16 ) ? 2 : 4;
+  int64_t const l_esz_out = ( dtype_out == ETIR_BF16 ) ? 2 : ( dtype_out == ETIR_FP64 ? 8 : 4 );
   bool const l_read_out = ktype_first_touch == ETIR_KTYPE_ADD || ktype_first_touch == ETIR_KTYPE_UNDEFINED;
   plan.bytes =   l_esz * l_size_c * ( l_size_m + l_size_n ) * l_size_k
                + l_esz_out * l_size_c * l_size_m * l_size_n * ( 1 + ( l_read_out ? 1 : 0 )
@@ -706,7 +711,7 @@ int launch_contraction( ContractionPlan const & plan,
   // vector paths need aligned base pointers; otherwise fall back to gathers
   int32_t l_ma = plan.mode_a;
   int32_t l_mb = plan.mode_b;
-  int64_t const l_esz = ( plan.dtype_in == ETIR_BF16 ) ? 2 : 4;
+  int64_t const l_esz = ( plan.dtype_in == ETIR_BF16 ) ? 2 : ( plan.dtype_in == ETIR_FP64 ? 8 : 4 );
   auto align_of = [&]( int32_t mode ) -> uintptr_t {
     if( mode == LOAD_VEC_K || mode == LOAD_VEC_MN ) return 16;
     return uintptr_t( l_esz );
@@ -739,6 +744,7 @@ int launch_contraction( ContractionPlan const & plan,
     case TILE_BF16_256x128: l_err = launch_contract_bf16_256x128( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_BF16_128x128: l_err = launch_contract_bf16_128x128( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_BF16_64x64:   l_err = launch_contract_bf16_64x64( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
+    case TILE_F64_64x64:    l_err = launch_contract_f64_64x64( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_BF16_DMA_256x256:
       l_err = launch_contract_bf16_dma( l_ma, l_mb, plan.dma_variant, a, l_g, stream );
       break;

@@ -28,9 +28,7 @@ Differences from the tpp backend, by design:
     exec type ``prim``; tpp's optimisation keys are accepted (and have no
     effect), unknown keys are rejected as in the reference;
   * DataType has the additive member ``bfloat16`` (bf16 tensors, fp32
-    accumulation); ``float64`` contractions are not provided by the HIP
-    kernels (``setup`` reports ``compilation_failed``), float64 permutations
-    are.
+    accumulation).
 """
 import ctypes
 import enum

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import einsum_ir_amd as eir
-from tests.helpers import TOL_FP32, TOL_BF16, parse_binary, tensor_numel, rel_frobenius, loops_for
+from tests.helpers import TOL_FP32, TOL_BF16, TOL_FP64, parse_binary, tensor_numel, rel_frobenius, loops_for
 
 pytestmark = pytest.mark.gpu
 
@@ -28,11 +28,14 @@ def run_case(torch, oracle, expr, sizes, dtype=eir.FP32, first=eir.ZERO, last=ei
     left, right, out = parse_binary(expr)
     loops = loops_for(expr, sizes, sizes_outer_aux=aux_outer)
     rng = np.random.default_rng(seed)
-    a = rng.uniform(-1, 1, tensor_numel(left, sizes)).astype(np.float32)
-    b = rng.uniform(-1, 1, tensor_numel(right, sizes)).astype(np.float32)
-    o0 = rng.uniform(-1, 1, tensor_numel(out, sizes)).astype(np.float32)
+    npt = np.float64 if dtype == eir.FP64 else np.float32
+    if dtype == eir.FP64:
+        dtype_out = eir.FP64
+    a = rng.uniform(-1, 1, tensor_numel(left, sizes)).astype(npt)
+    b = rng.uniform(-1, 1, tensor_numel(right, sizes)).astype(npt)
+    o0 = rng.uniform(-1, 1, tensor_numel(out, sizes)).astype(npt)
     needs_aux = first in (eir.COPY, eir.ADD) or last == eir.ADD
-    x = rng.uniform(-1, 1, tensor_numel(out, aux_outer or sizes)).astype(np.float32) if needs_aux else None
+    x = rng.uniform(-1, 1, tensor_numel(out, aux_outer or sizes)).astype(npt) if needs_aux else None
     if dtype == eir.BF16:
         a, b = oracle.f32_to_bf16(a), oracle.f32_to_bf16(b)
     if dtype_out == eir.BF16:
@@ -41,7 +44,8 @@ def run_case(torch, oracle, expr, sizes, dtype=eir.FP32, first=eir.ZERO, last=ei
     plan = eir.ContractionPlan(loops["dim_types"], loops["sizes"], loops["strides_left"],
                                loops["strides_right"], loops["strides_out"],
                                strides_out_aux=loops["strides_out_aux"],
-                               dtype_left=dtype, dtype_right=dtype, dtype_comp=eir.FP32,
+                               dtype_left=dtype, dtype_right=dtype,
+                               dtype_comp=eir.FP64 if dtype == eir.FP64 else eir.FP32,
                                dtype_out=dtype_out, ktype_first_touch=first, ktype_last_touch=last)
     da, db, do = _dev(torch, a), _dev(torch, b), _dev(torch, o0)
     dx = _dev(torch, x) if x is not None else None
@@ -60,6 +64,8 @@ def run_case(torch, oracle, expr, sizes, dtype=eir.FP32, first=eir.ZERO, last=ei
         ref = oracle.bf16_to_f32(ref)
     err = rel_frobenius(ref, got)
     tol = TOL_BF16 if (dtype == eir.BF16 or dtype_out == eir.BF16) else TOL_FP32
+    if dtype == eir.FP64:
+        tol = TOL_FP64
     assert err <= tol, f"{expr} {sizes}: rel. Frobenius error {err:.3e} > {tol:.0e} [{desc}]"
     return got, desc
 
@@ -174,13 +180,13 @@ def test_zero_k(torch_cuda, oracle):
     assert not np.any(got)
 
 
-def test_rejects_fp64(torch_cuda):
+def test_rejects_mixed_fp64(torch_cuda):
     loops = loops_for("mk,kn->mn", dict(m=4, k=4, n=4))
     with pytest.raises(eir.EinsumIrError) as e:
         eir.ContractionPlan(loops["dim_types"], loops["sizes"], loops["strides_left"],
                             loops["strides_right"], loops["strides_out"], dtype_left=eir.FP64,
-                            dtype_right=eir.FP64, dtype_comp=eir.FP64, dtype_out=eir.FP64)
-    assert e.value.code == eir.COMPILATION_FAILED
+                            dtype_right=eir.FP64, dtype_comp=eir.FP64, dtype_out=eir.FP32)
+    assert e.value.code == eir.INVALID_DTYPE
 
 
 def test_missing_aux_is_an_error(torch_cuda):

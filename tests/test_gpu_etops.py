@@ -170,14 +170,26 @@ def test_unary_transpose_and_zero(torch_cuda, dtype, npt):
     assert not dout.cpu().numpy().any()
 
 
-def test_float64_contraction_is_reported(torch_cuda):
-    cfg = _config((M, N, K), (8, 8, 8), (1, 0, 8), (0, 8, 1), (1, 8, 0), dtype=etops.float64)
+def test_float64_contraction_and_setup_errors(torch_cuda, oracle):
+    torch = torch_cuda
+    m, n, k = 24, 40, 12
+    cfg = _config((M, N, K), (m, n, k), (1, 0, m), (0, k, 1), (1, m, 0), dtype=etops.float64,
+                  last=etops.prim.relu)
+    rng = np.random.default_rng(8)
+    a, b = rng.uniform(-1, 1, m * k), rng.uniform(-1, 1, k * n)
+    dout = torch.zeros(m * n, dtype=torch.float64, device="cuda")
+    etops.TensorOperation(cfg).execute(torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda(), dout)
+    loops = dict(dim_types=[1, 2, 3], sizes=[m, n, k], strides_left=[1, 0, m], strides_right=[0, k, 1],
+                 strides_out=[1, m, 0])
+    ref = oracle.contract(loops, a, b, np.zeros(m * n), dtype_left=oracle.FP64, dtype_right=oracle.FP64,
+                          dtype_out=oracle.FP64, last_touch=oracle.RELU)
+    assert rel_frobenius(ref, dout.cpu().numpy()) <= 1e-12
     op = etops.TensorOperation()
-    assert op.setup("hip", cfg.data_type, cfg.prim_first, cfg.prim_main, cfg.prim_last, cfg.dim_types,
-                    cfg.exec_types, cfg.dim_sizes, cfg.strides) == etops.ErrorType.compilation_failed
     assert op.setup("tpp", cfg.data_type, cfg.prim_first, cfg.prim_main, cfg.prim_last, cfg.dim_types,
                     cfg.exec_types, cfg.dim_sizes, cfg.strides) == etops.ErrorType.compilation_failed
     assert op.setup(None, etops.float32, cfg.prim_first, cfg.prim_main, cfg.prim_last, cfg.dim_types,
                     cfg.exec_types, cfg.dim_sizes, (cfg.strides[0][:2],)) == etops.ErrorType.invalid_stride_shape
-    with pytest.raises(RuntimeError, match="compilation_failed"):
-        etops.TensorOperation(cfg)
+    assert op.setup("hip", cfg.data_type, cfg.prim_first, etops.prim.relu, cfg.prim_last, cfg.dim_types,
+                    cfg.exec_types, cfg.dim_sizes, cfg.strides) == etops.ErrorType.compilation_failed
+    with pytest.raises(RuntimeError, match="execute before a successful setup"):
+        op.execute(torch.zeros(1, device="cuda"), torch.zeros(1, device="cuda"), dout)
