@@ -11,10 +11,10 @@ import ctypes
 
 from . import _lib
 from ._lib import (SUCCESS, COMPILATION_FAILED, NO_DATA_PTR_PROVIDED, CALLED_BEFORE_COMPILATION,
-                   INVALID_ID, INVALID_BACKEND, INVALID_DTYPE, INVALID_KTYPE, UNDEFINED_ERROR,
+                   INVALID_ID, INVALID_BACKEND, INVALID_CPX_DIM, INVALID_DTYPE, INVALID_KTYPE, UNDEFINED_ERROR,
                    FP32, FP64, BF16, UNDEFINED_DTYPE,
-                   ZERO, RELU, ADD, COPY, MADD, UNDEFINED_KTYPE,
-                   DIM_C, DIM_M, DIM_N, DIM_K, DIM_I, DIM_J,
+                   ZERO, RELU, ADD, COPY, MADD, UNDEFINED_KTYPE, CPX_ZERO, CPX_MADD,
+                   DIM_C, DIM_M, DIM_N, DIM_K, DIM_CPX, DIM_I, DIM_J,
                    DTYPE_BYTES, EinsumIrError, hip_lib, check)
 from .loops import binary_loops, unary_dims, dim_types, row_major_strides  # noqa: F401
 

@@ -18,13 +18,15 @@ NO_DATA_PTR_PROVIDED = 4
 CALLED_BEFORE_COMPILATION = 5
 INVALID_ID = 6
 INVALID_BACKEND = 7
+INVALID_CPX_DIM = 8
 INVALID_DTYPE = 9
 INVALID_KTYPE = 10
 UNDEFINED_ERROR = 99
 
 FP32, FP64, BF16, UNDEFINED_DTYPE = 0, 1, 2, 99
 ZERO, RELU, ADD, COPY, MADD, UNDEFINED_KTYPE = 0, 1, 2, 3, 4, 99
-DIM_C, DIM_M, DIM_N, DIM_K, DIM_I, DIM_J = 0, 1, 2, 3, 5, 6
+CPX_ZERO, CPX_MADD = 6, 8
+DIM_C, DIM_M, DIM_N, DIM_K, DIM_CPX, DIM_I, DIM_J = 0, 1, 2, 3, 4, 5, 6
 
 DTYPE_BYTES = {FP32: 4, FP64: 8, BF16: 2}
 

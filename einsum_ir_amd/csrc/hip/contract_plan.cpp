@@ -38,6 +38,8 @@ int launch_contract_f32_64x64( int32_t ma, int32_t mb, bool kaff, ContractArgs c
                                uint32_t grid, hipStream_t stream );
 int launch_contract_f64_64x64( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
                                uint32_t grid, hipStream_t stream );
+int launch_contract_cpx( bool f64, int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
+                         uint32_t grid, hipStream_t stream );
 int launch_contract_bf16_256x256( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
                                   uint32_t grid, hipStream_t stream );
 int launch_contract_bf16_256x128( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
@@ -156,6 +158,8 @@ char const * tile_str( int32_t t ) {
     case TILE_BF16_128x128: return "bf16_128x128x64";
     case TILE_BF16_64x64:   return "bf16_64x64x64";
     case TILE_F64_64x64:    return "f64_64x64x16";
+    case TILE_CPX_F32_64x64: return "cpx_f32_64x64x16";
+    case TILE_CPX_F64_64x64: return "cpx_f64_64x64x16";
     default:                return "?";
   }
 }
@@ -206,16 +210,31 @@ int plan_contraction_impl( int64_t            num_loops,
   if( !l_f32 && !l_bf16 && !l_f64 ) {
     return fail( ETIR_INVALID_DTYPE, "contraction: unsupported dtype combination" );
   }
-  if( ktype_main != ETIR_KTYPE_MADD ) {
-    return fail( ETIR_INVALID_KTYPE, "contraction: main kernel must be MADD" );
+  // complex: CPX_MADD with the reference BLAS backend's touch kernels
+  // (BinaryContractionBlas.cpp:68-80)
+  bool const l_cpx = ( ktype_main == ETIR_KTYPE_CPX_MADD );
+  if( l_cpx ) {
+    if( l_bf16 ) return fail( ETIR_INVALID_DTYPE, "contraction: complex kernels take FP32 or FP64" );
+    if(    ktype_first_touch != ETIR_KTYPE_ZERO && ktype_first_touch != ETIR_KTYPE_CPX_ZERO
+        && ktype_first_touch != ETIR_KTYPE_UNDEFINED ) {
+      return fail( ETIR_INVALID_KTYPE, "contraction: unsupported complex first-touch kernel" );
+    }
+    if( ktype_last_touch != ETIR_KTYPE_UNDEFINED ) {
+      return fail( ETIR_INVALID_KTYPE, "contraction: complex contractions have no last-touch kernel" );
+    }
   }
-  if(    ktype_first_touch != ETIR_KTYPE_ZERO && ktype_first_touch != ETIR_KTYPE_COPY
-      && ktype_first_touch != ETIR_KTYPE_ADD  && ktype_first_touch != ETIR_KTYPE_UNDEFINED ) {
-    return fail( ETIR_COMPILATION_FAILED, "contraction: unsupported first-touch kernel" );
-  }
-  if(    ktype_last_touch != ETIR_KTYPE_RELU && ktype_last_touch != ETIR_KTYPE_ADD
-      && ktype_last_touch != ETIR_KTYPE_UNDEFINED ) {
-    return fail( ETIR_COMPILATION_FAILED, "contraction: unsupported last-touch kernel" );
+  else {
+    if( ktype_main != ETIR_KTYPE_MADD ) {
+      return fail( ETIR_INVALID_KTYPE, "contraction: main kernel must be MADD or CPX_MADD" );
+    }
+    if(    ktype_first_touch != ETIR_KTYPE_ZERO && ktype_first_touch != ETIR_KTYPE_COPY
+        && ktype_first_touch != ETIR_KTYPE_ADD  && ktype_first_touch != ETIR_KTYPE_UNDEFINED ) {
+      return fail( ETIR_COMPILATION_FAILED, "contraction: unsupported first-touch kernel" );
+    }
+    if(    ktype_last_touch != ETIR_KTYPE_RELU && ktype_last_touch != ETIR_KTYPE_ADD
+        && ktype_last_touch != ETIR_KTYPE_UNDEFINED ) {
+      return fail( ETIR_COMPILATION_FAILED, "contraction: unsupported last-touch kernel" );
+    }
   }
   if( num_loops < 0 || ( num_loops > 0 && ( dim_types == nullptr || sizes == nullptr
                                             || strides_left == nullptr || strides_right == nullptr
@@ -236,7 +255,7 @@ int plan_contraction_impl( int64_t            num_loops,
   int64_t const * l_s_aux = strides_out_aux != nullptr ? strides_out_aux : strides_out;
 
   // ------------------------------------------------------------- loop sets
-  std::vector< Loop > l_c, l_m, l_n, l_k;
+  std::vector< Loop > l_c, l_m, l_n, l_k, l_x;
   for( int64_t l_lo = 0; l_lo < num_loops; l_lo++ ) {
     if( sizes[l_lo] < 0 ) return fail( ETIR_COMPILATION_FAILED, "contraction: negative loop size" );
     if(    strides_left[l_lo] < 0 || strides_right[l_lo] < 0 || strides_out[l_lo] < 0
@@ -246,6 +265,10 @@ int plan_contraction_impl( int64_t            num_loops,
     Loop l_lp{ dim_types[l_lo], sizes[l_lo],
                { strides_left[l_lo], strides_right[l_lo], l_s_aux[l_lo], strides_out[l_lo] } };
     if( l_lp.type == ETIR_DIM_I || l_lp.type == ETIR_DIM_J ) continue;
+    if( l_lp.type == ETIR_DIM_CPX ) {
+      l_x.push_back( l_lp );
+      continue;
+    }
     if( l_lp.size == 1 ) continue;
     if(      l_lp.type == ETIR_DIM_C ) l_c.push_back( l_lp );
     else if( l_lp.type == ETIR_DIM_M ) l_m.push_back( l_lp );
@@ -254,6 +277,12 @@ int plan_contraction_impl( int64_t            num_loops,
     else return fail( ETIR_COMPILATION_FAILED, "contraction: invalid dimension type" );
   }
 
+  if( l_cpx != ( l_x.size() > 0 ) ) {
+    return fail( ETIR_INVALID_CPX_DIM, "contraction: CPX_MADD needs exactly one CPX loop and CPX loops need CPX_MADD" );
+  }
+  if( l_x.size() > 1 || ( l_cpx && l_x[0].size != 2 ) ) {
+    return fail( ETIR_INVALID_CPX_DIM, "contraction: the complex loop must be unique and of size 2" );
+  }
   auto prod = []( std::vector< Loop > const & d ) {
     int64_t l_p = 1;
     for( Loop const & l_x : d ) l_p *= l_x.size;
@@ -344,6 +373,10 @@ int plan_contraction_impl( int64_t            num_loops,
   };
   plan.mode_a = pick_mode( l_tm_a, l_tk_a, l_tc_a );
   plan.mode_b = pick_mode( l_tn_b, l_tk_b, l_tc_b );
+  // complex: the imaginary parts are loaded like the real ones from base +
+  // cpx stride, so that offset has to keep the 16-byte vector alignment
+  if( l_cpx && l_x[0].s[l_sa] % l_vk != 0 ) plan.mode_a = LOAD_SCALAR;
+  if( l_cpx && l_x[0].s[l_sb] % l_vk != 0 ) plan.mode_b = LOAD_SCALAR;
 
   bool l_k_affine = true;
   int64_t l_sk_a = l_tk_a.size() > 1 ? l_tk_a[1] : 0;
@@ -372,7 +405,10 @@ int plan_contraction_impl( int64_t            num_loops,
     double const l_util = l_pad > 0.0 ? double( l_kern_m ) * double( l_kern_n ) / l_pad : 1.0;
     return l_util * std::min( 1.0, double( n_tiles( t ) ) / double( l_cus ) );
   };
-  if( l_f64 ) {
+  if( l_cpx ) {
+    plan.tile = l_f64 ? TILE_CPX_F64_64x64 : TILE_CPX_F32_64x64;
+  }
+  else if( l_f64 ) {
     plan.tile = TILE_F64_64x64;
   }
   else if( l_f32 ) {
@@ -402,7 +438,7 @@ int plan_contraction_impl( int64_t            num_loops,
       && 2 * int64_t( 64 ) * std::max( l_sk_a, l_sk_b ) * ( ( l_size_k + 63 ) / 64 + 4 ) < ( int64_t( 1 ) << 31 );
   plan.tile_fallback = plan.tile;
   if( l_dma_ok && n_tiles( TILE_BF16_DMA_256x256 ) >= l_cus ) plan.tile = TILE_BF16_DMA_256x256;
-  if( char const * l_env = l_f64 ? nullptr : std::getenv( "ETIR_TILE" ) ) {
+  if( char const * l_env = ( l_f64 || l_cpx ) ? nullptr : std::getenv( "ETIR_TILE" ) ) {
     // diagnostic override of the tile heuristic (must match the dtype)
     int32_t l_t = std::atoi( l_env );
     bool const l_t_f32 = ( l_t == TILE_F32_128x128 || l_t == TILE_F32_64x64 );
@@ -428,7 +464,7 @@ int plan_contraction_impl( int64_t            num_loops,
   // node with M = 64, N = 1024, K = 32768).  Then the outermost K loops (one
   // of them factored if needed) become C loops of a partial contraction that
   // writes one workspace slice per split, and split_reduce sums the slices.
-  if( allow_split && !l_f64 && l_size_k >= 512 ) {
+  if( allow_split && !l_f64 && !l_cpx && l_size_k >= 512 ) {
     int64_t const l_tiles = n_tiles( plan.tile );
     if( l_tiles > 0 && l_tiles < l_cus ) {
       // at least 128 k per split; aim for two workgroups per CU
@@ -535,12 +571,14 @@ int plan_contraction_impl( int64_t            num_loops,
   plan.M = l_kern_m;
   plan.N = l_kern_n;
   plan.K = l_size_k;
-  plan.flops = 2 * l_size_c * l_size_m * l_size_n * l_size_k;
+  // complex: four real products per complex multiply-add
+  plan.flops = ( l_cpx ? 8 : 2 ) * l_size_c * l_size_m * l_size_n * l_size_k;
   int64_t const l_esz_out = ( dtype_out == ETIR_BF16 ) ? 2 : ( dtype_out == ETIR_FP64 ? 8 : 4 );
   bool const l_read_out = ktype_first_touch == ETIR_KTYPE_ADD || ktype_first_touch == ETIR_KTYPE_UNDEFINED;
-  plan.bytes =   l_esz * l_size_c * ( l_size_m + l_size_n ) * l_size_k
-               + l_esz_out * l_size_c * l_size_m * l_size_n * ( 1 + ( l_read_out ? 1 : 0 )
-                                                                  + ( plan.needs_aux ? 1 : 0 ) );
+  plan.bytes = ( l_cpx ? 2 : 1 )
+             * (   l_esz * l_size_c * ( l_size_m + l_size_n ) * l_size_k
+                 + l_esz_out * l_size_c * l_size_m * l_size_n * ( 1 + ( l_read_out ? 1 : 0 )
+                                                                    + ( plan.needs_aux ? 1 : 0 ) ) );
 
   std::ostringstream l_d;
   l_d << "contract " << tile_str( plan.tile )
@@ -616,6 +654,11 @@ int plan_contraction_impl( int64_t            num_loops,
   a.first_touch = ktype_first_touch;
   a.last_touch  = ktype_last_touch;
   a.out_bf16 = ( dtype_out == ETIR_BF16 ) ? 1 : 0;
+  if( l_cpx ) {
+    a.cpx_a   = l_x[0].s[l_sa];
+    a.cpx_b   = l_x[0].s[l_sb];
+    a.cpx_out = l_x[0].s[T_OUT];
+  }
   {
     int64_t l_mo = 0, l_no = 0;
     for( int64_t l_v : l_tm_out ) l_mo = std::max( l_mo, l_v );
@@ -745,6 +788,8 @@ int launch_contraction( ContractionPlan const & plan,
     case TILE_BF16_128x128: l_err = launch_contract_bf16_128x128( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_BF16_64x64:   l_err = launch_contract_bf16_64x64( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_F64_64x64:    l_err = launch_contract_f64_64x64( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
+    case TILE_CPX_F32_64x64: l_err = launch_contract_cpx( false, l_ma, l_mb, l_kaff, a, l_g, stream ); break;
+    case TILE_CPX_F64_64x64: l_err = launch_contract_cpx( true, l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_BF16_DMA_256x256:
       l_err = launch_contract_bf16_dma( l_ma, l_mb, plan.dma_variant, a, l_g, stream );
       break;

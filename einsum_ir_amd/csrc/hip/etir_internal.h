@@ -112,7 +112,9 @@ enum TileCfg : int32_t {
   TILE_F64_64x64   = 5,
   TILE_BF16_256x128 = 6,
   TILE_BF16_DMA_256x256 = 7,  // direct-to-LDS kernel (contract_dma.h), one workgroup per CU
-  TILE_BF16_DMA_256x128 = 8   // direct-to-LDS kernel, two workgroups per CU
+  TILE_BF16_DMA_256x128 = 8,  // direct-to-LDS kernel, two workgroups per CU
+  TILE_CPX_F32_64x64    = 9,  // complex (CPX_MADD) kernels, contract_cpx.hip
+  TILE_CPX_F64_64x64    = 10
 };
 
 struct ContractArgs {
@@ -144,6 +146,8 @@ struct ContractArgs {
   int32_t k_full;         // K % BK == 0: no K masking needed
   int32_t out_bf16;       // output stored as bf16 (RNE)
   int32_t out_off32;      // every output byte offset (M part + N part, C part excluded) is < 2^32
+  // complex contractions: element offsets of the imaginary parts (A, B, out)
+  int64_t cpx_a, cpx_b, cpx_out;
 };
 
 struct ContractionPlan {

@@ -62,6 +62,16 @@ einsum_ir::err_t einsum_ir::backend::BinaryContractionHip::compile() {
     l_so[l_i] = find0( l_s_out,   l_id );
   }
 
+  // complex kernels: one C dim is the complex dim
+  if( m_ktype_main == kernel_t::CPX_MADD ) {
+    int64_t const l_cpx = ( m_cpx_dim_id >= 0 ) ? m_cpx_dim_id
+                        : ( m_dim_ids_c.empty() ? -1 : m_dim_ids_c[0] );
+    std::size_t l_i = 0;
+    while( l_i < l_n && !( l_ids[l_i] == l_cpx && l_types[l_i] == (int32_t) dim_t::C ) ) l_i++;
+    if( l_i == l_n || l_sizes[l_i] != 2 ) return err_t::INVALID_CPX_DIM;
+    l_types[l_i] = (int32_t) dim_t::CPX;
+  }
+
   if( m_plan != nullptr ) {
     etir_hip_plan_destroy( m_plan );
     m_plan = nullptr;

@@ -34,6 +34,11 @@ class einsum_ir::backend::BinaryContractionHip : public BinaryContraction {
     /** Selects the HIP stream (hipStream_t as void*, nullptr = null stream). **/
     void set_stream( void * i_stream ) { m_stream = i_stream; }
 
+    //! complex kernels: id of the complex dim (size 2); -1 selects the first
+    //! C dim in the output's order, the reference BLAS backend's rule
+    //! (reference src/backend/BinaryContractionBlas.cpp:82-85)
+    int64_t m_cpx_dim_id = -1;
+
     void contract( void const * i_tensor_left,
                    void const * i_tensor_right,
                    void       * io_tensor_out );

@@ -150,11 +150,11 @@ einsum_ir::err_t einsum_ir::backend::EinsumNode::compile() {
 einsum_ir::err_t einsum_ir::backend::EinsumNode::compile_recursive() {
   err_t l_err = err_t::UNDEFINED_ERROR;
 
-  // backend of the contraction: AUTO resolves to HIP unless the kernels are
-  // complex (the reference sends those to BLAS, which this build lacks)
+  // backend of the contraction: AUTO resolves to HIP, complex kernels
+  // included (the reference sends those to its BLAS backend,
+  // EinsumNode.cpp:207-213; the HIP backend runs them natively)
   if( m_btype_binary == backend_t::AUTO ) {
-    bool l_cpx = ce_cpx_op( m_ktype_first_touch ) || ce_cpx_op( m_ktype_main ) || ce_cpx_op( m_ktype_last_touch );
-    m_btype_binary = l_cpx ? backend_t::BLAS : backend_t::HIP;
+    m_btype_binary = backend_t::HIP;
   }
   if( !BinaryContractionFactory::supports( m_btype_binary ) ) {
     return err_t::INVALID_BACKEND;
@@ -205,6 +205,7 @@ einsum_ir::err_t einsum_ir::backend::EinsumNode::compile_recursive() {
                   m_ktype_first_touch, m_ktype_main, m_ktype_last_touch,
                   m_num_threads );
     static_cast< BinaryContractionHip * >( m_cont )->set_stream( m_stream );
+    static_cast< BinaryContractionHip * >( m_cont )->m_cpx_dim_id = m_cpx_dim_id;
     l_err = m_cont->compile();
     if( l_err != err_t::SUCCESS ) return l_err;
   }

@@ -88,6 +88,10 @@ class einsum_ir::backend::EinsumNode {
     //! HIP stream of the whole tree (hipStream_t as void*, nullptr = null stream)
     void * m_stream = nullptr;
 
+    //! complex trees: id of the complex dim of this node's contraction (-1:
+    //! the contraction's default, the first C dim of the output)
+    int64_t m_cpx_dim_id = -1;
+
     ~EinsumNode();
 
     /** Leaf node (reference EinsumNode.h:141-157). **/

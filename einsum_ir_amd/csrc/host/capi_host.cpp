@@ -203,8 +203,23 @@ int etir_expression_create( char const        * expr,
                             void * const      * data_ptrs,
                             void              * stream,
                             etir_expression_t * handle ) {
+  return etir_expression_create_ctype( expr, dim_sizes, num_dim_sizes, path, path_len, (int32_t) REAL_ONLY,
+                                       dtype, data_ptrs, stream, handle );
+}
+
+int etir_expression_create_ctype( char const        * expr,
+                                  int64_t const     * dim_sizes,
+                                  int64_t             num_dim_sizes,
+                                  int64_t const     * path,
+                                  int64_t             path_len,
+                                  int32_t             ctype,
+                                  int32_t             dtype,
+                                  void * const      * data_ptrs,
+                                  void              * stream,
+                                  etir_expression_t * handle ) {
   if( handle == nullptr ) return err_t::UNDEFINED_ERROR;
   *handle = nullptr;
+  if( ctype != REAL_ONLY && ctype != BATCH_INNER && ctype != BATCH_OUTER ) return err_t::COMPILATION_FAILED;
   std::unique_ptr< etir_expression_s > l_h( new etir_expression_s() );
   try {
     ParsedExpr l_p;
@@ -216,15 +231,27 @@ int etir_expression_create( char const        * expr,
       return err_t::COMPILATION_FAILED;
     }
     l_h->sizes.assign( dim_sizes, dim_sizes + num_dim_sizes );
+    // complex tensors: one more dim of size 2 with the next free id, innermost
+    // (BATCH_INNER, as bench_expression.cpp:110,196-222 appends it) or
+    // outermost (BATCH_OUTER) in every tensor
+    int64_t l_num_ids = num_dim_sizes;
+    if( ctype != REAL_ONLY ) {
+      l_h->sizes.push_back( 2 );
+      for( auto & l_t : l_p.tensors ) {
+        if( ctype == BATCH_INNER ) l_t.push_back( num_dim_sizes );
+        else                       l_t.insert( l_t.begin(), num_dim_sizes );
+      }
+      l_num_ids++;
+    }
     for( auto const & l_t : l_p.tensors ) {
       l_h->string_num_dims.push_back( (int64_t) l_t.size() );
       l_h->string_dim_ids.insert( l_h->string_dim_ids.end(), l_t.begin(), l_t.end() );
     }
     l_h->path.assign( path, path + path_len );
     l_h->ptrs.assign( data_ptrs, data_ptrs + l_num_tensors );
-    l_h->expr.init( num_dim_sizes, l_h->sizes.data(), l_num_conts,
+    l_h->expr.init( l_num_ids, l_h->sizes.data(), l_num_conts,
                     l_h->string_num_dims.data(), l_h->string_dim_ids.data(), l_h->path.data(),
-                    (data_t) dtype, l_h->ptrs.data() );
+                    (complex_t) ctype, (data_t) dtype, l_h->ptrs.data() );
     l_h->expr.set_stream( stream );
     l_err = l_h->expr.compile();
     if( l_err != err_t::SUCCESS ) return l_err;

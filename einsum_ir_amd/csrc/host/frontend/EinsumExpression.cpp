@@ -86,10 +86,6 @@ void einsum_ir::frontend::EinsumExpression::init( int64_t                 i_num_
 
 einsum_ir::err_t einsum_ir::frontend::EinsumExpression::compile() {
   reset_graph();
-  if( m_ctype_ext != complex_t::REAL_ONLY ) {
-    // complex tensors (BATCH_INNER) need the reference's BLAS backend
-    return err_t::INVALID_BACKEND;
-  }
   if( m_num_conts < 1 ) {
     return err_t::COMPILATION_FAILED;
   }
@@ -135,11 +131,35 @@ einsum_ir::err_t einsum_ir::frontend::EinsumExpression::compile() {
   // root: the external output's dims
   int64_t const * l_root_ids = m_string_dim_ids_ext + l_size_in;
   int64_t const l_root_nd = m_string_num_dims_ext[l_num_all - 1];
+
+  // complex tensors: the complex dim (size 2) is the output's innermost
+  // (BATCH_INNER) or outermost (BATCH_OUTER) dim and appears in every tensor;
+  // every contraction runs the complex kernels.  BATCH_INNER contracts into a
+  // complex-outermost root and converts it with one more (unary) node
+  // (reference EinsumExpression.cpp:214-224, 316-330).
+  bool const l_cpx = ( m_ctype_ext != complex_t::REAL_ONLY );
+  bool const l_cpx_inner = ( m_ctype_ext == complex_t::BATCH_INNER );
+  int64_t l_cpx_id = -1;
+  if( l_cpx ) {
+    if( l_root_nd < 1 || m_dtype == data_t::BF16 ) return err_t::INVALID_CPX_DIM;
+    l_cpx_id = l_cpx_inner ? l_root_ids[l_root_nd - 1] : l_root_ids[0];
+    if( m_map_dim_sizes.at( l_cpx_id ) != 2 ) return err_t::INVALID_CPX_DIM;
+  }
+  if( l_cpx_inner ) {
+    m_string_num_dims_int.push_back( l_root_nd );
+    m_string_dim_ids_int.push_back( l_cpx_id );
+    m_string_dim_ids_int.insert( m_string_dim_ids_int.end(), l_root_ids, l_root_ids + l_root_nd - 1 );
+    l_offsets.push_back( (int64_t) m_string_dim_ids_int.size() );
+  }
   m_string_num_dims_int.push_back( l_root_nd );
   m_string_dim_ids_int.insert( m_string_dim_ids_int.end(), l_root_ids, l_root_ids + l_root_nd );
 
-  // nodes: inputs first, then one node per contraction (root last)
-  int64_t const l_num_nodes = l_num_in + m_num_conts;
+  kernel_t const l_first = l_cpx ? kernel_t::CPX_ZERO : kernel_t::ZERO;
+  kernel_t const l_main  = l_cpx ? kernel_t::CPX_MADD : kernel_t::MADD;
+
+  // nodes: inputs first, then one node per contraction, then (BATCH_INNER)
+  // the conversion; the last node is the root
+  int64_t const l_num_nodes = l_num_in + m_num_conts + ( l_cpx_inner ? 1 : 0 );
   m_nodes.clear();
   m_nodes.resize( l_num_nodes );
   for( int64_t l_te = 0; l_te < l_num_in; l_te++ ) {
@@ -148,15 +168,21 @@ einsum_ir::err_t einsum_ir::frontend::EinsumExpression::compile() {
   }
   for( int64_t l_co = 0; l_co < m_num_conts; l_co++ ) {
     int64_t const l_id_out = l_num_in + l_co;
-    bool const l_root = ( l_co == m_num_conts - 1 );
+    bool const l_root = ( l_co == m_num_conts - 1 ) && !l_cpx_inner;
     m_nodes[l_id_out].init( m_string_num_dims_int[l_id_out],
                             m_string_dim_ids_int.data() + l_offsets[l_id_out],
                             &m_map_dim_sizes, nullptr, nullptr, nullptr, nullptr,
                             m_dtype, nullptr,
                             l_root ? m_data_ptrs[l_num_all - 1] : nullptr,
-                            kernel_t::ZERO, kernel_t::MADD, kernel_t::UNDEFINED_KTYPE,
+                            l_first, l_main, kernel_t::UNDEFINED_KTYPE,
                             &m_nodes[ m_path_int[2 * l_co] ], &m_nodes[ m_path_int[2 * l_co + 1] ],
                             &m_memory, 1 );
+    m_nodes[l_id_out].m_cpx_dim_id = l_cpx_id;
+  }
+  if( l_cpx_inner ) {
+    int64_t const l_id = l_num_in + m_num_conts;
+    m_nodes[l_id].init( l_root_nd, m_string_dim_ids_int.data() + l_offsets[l_id], &m_map_dim_sizes, nullptr,
+                        m_dtype, m_data_ptrs[l_num_all - 1], &m_nodes[l_id - 1], &m_memory, 1 );
   }
   m_nodes.back().set_stream( m_stream );
   err_t l_err = m_nodes.back().compile();

@@ -26,6 +26,9 @@ _SIGS = {
     "etir_unary_destroy": (ctypes.c_int, [_vp]),
     "etir_expression_create": (ctypes.c_int, [ctypes.c_char_p, _i64p, ctypes.c_int64, _i64p, ctypes.c_int64,
                                               ctypes.c_int32, ctypes.POINTER(_vp), _vp, ctypes.POINTER(_vp)]),
+    "etir_expression_create_ctype": (ctypes.c_int, [ctypes.c_char_p, _i64p, ctypes.c_int64, _i64p, ctypes.c_int64,
+                                                    ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(_vp), _vp,
+                                                    ctypes.POINTER(_vp)]),
     "etir_expression_eval": (ctypes.c_int, [_vp]),
     "etir_expression_eval_async": (ctypes.c_int, [_vp]),
     "etir_expression_eval_graph": (ctypes.c_int, [_vp]),
@@ -178,6 +181,10 @@ class Unary(_Handle):
         _check(host_lib().etir_unary_eval(self._h, _ptr(inp), _ptr(out)))
 
 
+# complex_t (reference src/constants.h:54-59)
+REAL_ONLY, BATCH_INNER, BATCH_OUTER = 0, 1, 2
+
+
 class Expression(_Handle):
     """EinsumExpression: einsum string + contraction path, evaluated on the GPU.
 
@@ -185,7 +192,7 @@ class Expression(_Handle):
     path: flat list or list of pairs in opt_einsum's standard form."""
     _destroy = "etir_expression_destroy"
 
-    def __init__(self, expr, sizes, path, tensors, dtype=_lib.FP32, stream=None):
+    def __init__(self, expr, sizes, path, tensors, dtype=_lib.FP32, stream=None, ctype=REAL_ONLY):
         super().__init__()
         s = sizes_in_id_order(expr, sizes)
         flat = []
@@ -193,9 +200,9 @@ class Expression(_Handle):
             flat.extend(p if isinstance(p, (tuple, list)) else [p])
         self._tensors = list(tensors)   # keep the buffers alive
         ptrs = (ctypes.c_void_p * len(self._tensors))(*[_ptr(t) for t in self._tensors])
-        _check(host_lib().etir_expression_create(expr.encode(), _lib.i64_array(s), len(s),
-                                                 _lib.i64_array(flat), len(flat), dtype, ptrs,
-                                                 _stream(stream), ctypes.byref(self._h)))
+        _check(host_lib().etir_expression_create_ctype(expr.encode(), _lib.i64_array(s), len(s),
+                                                       _lib.i64_array(flat), len(flat), ctype, dtype, ptrs,
+                                                       _stream(stream), ctypes.byref(self._h)))
 
     def eval(self):
         _check(host_lib().etir_expression_eval(self._h))

@@ -76,6 +76,23 @@ int etir_expression_create( char const        * expr,
                             void * const      * data_ptrs,
                             void              * stream,
                             etir_expression_t * handle );
+/* The same for complex tensors (reference EinsumExpression::init with a
+ * complex_t, src/frontend/EinsumExpression.h:160-170): ctype 0 REAL_ONLY,
+ * 1 BATCH_INNER (every tensor gets an innermost dim of size 2: real and
+ * imaginary parts interleaved, the layout of complex64/complex128 arrays;
+ * bench_expression's CPX_FP32/CPX_FP64), 2 BATCH_OUTER (an outermost dim of
+ * size 2: all real parts, then all imaginary parts).  `expr` and `dim_sizes`
+ * describe the tensors without that dim; dtype FP32 or FP64. */
+int etir_expression_create_ctype( char const        * expr,
+                                  int64_t const     * dim_sizes,
+                                  int64_t             num_dim_sizes,
+                                  int64_t const     * path,
+                                  int64_t             path_len,
+                                  int32_t             ctype,
+                                  int32_t             dtype,
+                                  void * const      * data_ptrs,
+                                  void              * stream,
+                                  etir_expression_t * handle );
 /* EinsumExpression::eval: enqueues the tree and waits for it. */
 int etir_expression_eval( etir_expression_t handle );
 /* Enqueues the tree on the stream without waiting. */

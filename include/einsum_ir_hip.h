@@ -54,6 +54,8 @@ extern "C" {
 #define ETIR_KTYPE_ADD                  2
 #define ETIR_KTYPE_COPY                 3
 #define ETIR_KTYPE_MADD                 4
+#define ETIR_KTYPE_CPX_ZERO             6
+#define ETIR_KTYPE_CPX_MADD             8
 #define ETIR_KTYPE_UNDEFINED           99
 
 /* dimension types: einsum_ir::dim_t (reference src/constants.h:9-18) */
@@ -61,6 +63,7 @@ extern "C" {
 #define ETIR_DIM_M                      1
 #define ETIR_DIM_N                      2
 #define ETIR_DIM_K                      3
+#define ETIR_DIM_CPX                    4
 #define ETIR_DIM_I                      5
 #define ETIR_DIM_J                      6
 
@@ -87,6 +90,13 @@ typedef struct etir_plan_s * etir_plan_t;
  * Touch kernels: first in {ZERO, COPY, ADD, UNDEFINED}, main MADD,
  * last in {RELU, ADD, UNDEFINED} -- the set ContractionBackendTpp accepts
  * (ContractionBackendTpp.cpp:127-163).
+ *
+ * Complex contractions (the reference's CPX kernels, which it runs on its
+ * BLAS backend: BinaryContractionBlas.cpp:68-85): main CPX_MADD, exactly one
+ * loop of type ETIR_DIM_CPX with size 2 whose strides locate the imaginary
+ * parts (0 = real, 1 = imaginary in every tensor), first touch ZERO, CPX_ZERO
+ * or UNDEFINED (accumulate into the output), last touch UNDEFINED; FP32 or
+ * FP64 throughout.
  *
  * The plan owns small device-resident offset tables (allocated here, never
  * during execution).

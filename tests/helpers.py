@@ -17,8 +17,11 @@ def uniform(rng, n, dtype=np.float32):
 
 
 def rel_frobenius(ref, x):
-    ref = np.asarray(ref, dtype=np.float64).ravel()
-    x = np.asarray(x, dtype=np.float64).ravel()
+    """||ref - x||_F / ||ref||_F in double precision (complex arrays compared
+    as complex: both the real and the imaginary parts count)."""
+    cpx = np.iscomplexobj(ref) or np.iscomplexobj(x)
+    ref = np.asarray(ref, dtype=np.complex128 if cpx else np.float64).ravel()
+    x = np.asarray(x, dtype=np.complex128 if cpx else np.float64).ravel()
     nrm = np.linalg.norm(ref)
     if nrm == 0.0:
         return float(np.linalg.norm(x))
