@@ -234,3 +234,157 @@ einsum_ir::err_t einsum_ir::backend::BinaryPrimitives::reorder( backend_t       
   return reorder( l_ord, i_num_dims_left, i_num_dims_right, i_num_dims_out, i_dim_sizes,
                   io_dim_ids_left, io_dim_ids_right, io_dim_ids_out );
 }
+
+namespace {
+  // one tensor walked from its innermost dim outwards: position, dim types
+  // and the stride its next dim needs for contiguous storage
+  struct BlockCursor {
+    int64_t const * ids;
+    std::vector< einsum_ir::dim_t > types;
+    std::map< int64_t, int64_t > const * strides;
+    int64_t pos;
+    int64_t cont = 1;
+
+    bool valid() const { return pos >= 0; }
+    int64_t id() const { return ids[pos]; }
+    einsum_ir::dim_t type() const { return types[pos]; }
+    bool contiguous() const { return strides->at( id() ) == cont; }
+    void step( int64_t i_size ) { cont *= i_size; pos--; }
+  };
+
+  // row-major strides of a dim order
+  void default_strides( int64_t i_num_dims, int64_t const * i_ids, std::map< int64_t, int64_t > const * i_sizes,
+                        std::map< int64_t, int64_t > & o_strides ) {
+    int64_t l_stride = 1;
+    for( int64_t l_di = i_num_dims - 1; l_di >= 0; l_di-- ) {
+      o_strides[ i_ids[l_di] ] = l_stride;
+      l_stride *= i_sizes->at( i_ids[l_di] );
+    }
+  }
+
+  bool fits( int64_t i_block, int64_t i_size, int64_t i_min, int64_t i_max ) {
+    return i_block < i_min || i_block * i_size <= i_max;
+  }
+
+  // blocked C dims: trailing output C dims found at the same position (same id,
+  // contiguous) in all three tensors.  Returns false when the walk has to stop
+  // the whole blocking (a C dim that is not shared contiguously), leaving the
+  // collected dims innermost-first as the reference does on that path.
+  bool block_c( BlockCursor & io_l, BlockCursor & io_r, BlockCursor & io_o,
+                std::map< int64_t, int64_t > const * i_sizes, std::vector< int64_t > & o_cb ) {
+    while( io_o.valid() && io_o.type() == einsum_ir::dim_t::C ) {
+      if( !io_l.valid() || !io_r.valid() ) return false;
+      if( !io_l.contiguous() || !io_r.contiguous() || !io_o.contiguous() ) return false;
+      if( io_o.id() != io_l.id() || io_o.id() != io_r.id() ) return false;
+      int64_t const l_size = i_sizes->at( io_o.id() );
+      o_cb.push_back( io_o.id() );
+      io_l.step( l_size );
+      io_r.step( l_size );
+      io_o.step( l_size );
+    }
+    return true;
+  }
+
+  // blocked dims of one type: the driver tensor's dims of type i_type that sit
+  // at the other tensor's cursor too, both contiguous, within the size targets
+  void block_pair( einsum_ir::dim_t i_type, BlockCursor & io_drv, BlockCursor & io_other,
+                   std::map< int64_t, int64_t > const * i_sizes, int64_t i_min, int64_t i_max,
+                   std::vector< int64_t > & o_block ) {
+    int64_t l_block = 1;
+    while( io_drv.valid() && io_other.valid() && io_drv.type() == i_type ) {
+      if( !io_drv.contiguous() || !io_other.contiguous() ) break;
+      int64_t const l_size = i_sizes->at( io_drv.id() );
+      if( io_drv.id() != io_other.id() || !fits( l_block, l_size, i_min, i_max ) ) break;
+      o_block.push_back( io_drv.id() );
+      l_block *= l_size;
+      io_drv.step( l_size );
+      io_other.step( l_size );
+    }
+  }
+}
+
+einsum_ir::err_t einsum_ir::backend::BinaryPrimitives::blocking( primblo_t                            i_primitive_blocking,
+                                                                 int64_t                              i_num_dims_left,
+                                                                 int64_t                              i_num_dims_right,
+                                                                 int64_t                              i_num_dims_out,
+                                                                 int64_t                      const * i_dim_ids_left,
+                                                                 int64_t                      const * i_dim_ids_right,
+                                                                 int64_t                      const * i_dim_ids_out,
+                                                                 std::map< int64_t, int64_t > const * i_dim_sizes,
+                                                                 std::map< int64_t, int64_t > const * i_strides_left,
+                                                                 std::map< int64_t, int64_t > const * i_strides_right,
+                                                                 std::map< int64_t, int64_t > const * i_strides_out,
+                                                                 std::vector< int64_t >             * o_dim_ids_cb,
+                                                                 std::vector< int64_t >             * o_dim_ids_mb,
+                                                                 std::vector< int64_t >             * o_dim_ids_nb,
+                                                                 std::vector< int64_t >             * o_dim_ids_kb ) const {
+  if(    i_primitive_blocking != primblo_t::LEFT_KB_X_MB_CB_RIGHT_NB_X_KB_CB_OUT_NB_X_MB_CB
+      && i_primitive_blocking != primblo_t::LEFT_X_CB_KB_MB_RIGHT_X_CB_NB_KB_OUT_NB_X_MB_CB ) {
+    return err_t::TENSOR_BLOCKING_FAILED;
+  }
+  o_dim_ids_cb->clear();
+  o_dim_ids_mb->clear();
+  o_dim_ids_nb->clear();
+  o_dim_ids_kb->clear();
+
+  std::map< int64_t, int64_t > l_def_l, l_def_r, l_def_o;
+  if( i_strides_left  == nullptr ) default_strides( i_num_dims_left,  i_dim_ids_left,  i_dim_sizes, l_def_l );
+  if( i_strides_right == nullptr ) default_strides( i_num_dims_right, i_dim_ids_right, i_dim_sizes, l_def_r );
+  if( i_strides_out   == nullptr ) default_strides( i_num_dims_out,   i_dim_ids_out,   i_dim_sizes, l_def_o );
+
+  BlockCursor l_l{ i_dim_ids_left,  {}, i_strides_left  ? i_strides_left  : &l_def_l, i_num_dims_left  - 1 };
+  BlockCursor l_r{ i_dim_ids_right, {}, i_strides_right ? i_strides_right : &l_def_r, i_num_dims_right - 1 };
+  BlockCursor l_o{ i_dim_ids_out,   {}, i_strides_out   ? i_strides_out   : &l_def_o, i_num_dims_out   - 1 };
+  BinaryContraction::dim_types( i_num_dims_left, i_num_dims_right, i_num_dims_out,
+                                i_dim_ids_left, i_dim_ids_right, i_dim_ids_out,
+                                &l_l.types, &l_r.types, &l_o.types );
+  auto size_at = [&]( BlockCursor const & c ) { return i_dim_sizes->at( c.id() ); };
+
+  if( i_primitive_blocking == primblo_t::LEFT_KB_X_MB_CB_RIGHT_NB_X_KB_CB_OUT_NB_X_MB_CB ) {
+    // innermost: C (all three), then M (left/out), K (left/right), N (right/out)
+    if( !block_c( l_l, l_r, l_o, i_dim_sizes, *o_dim_ids_cb ) ) return err_t::SUCCESS;
+    block_pair( dim_t::M, l_o, l_l, i_dim_sizes, m_size_mb_min, m_size_mb_max, *o_dim_ids_mb );
+
+    // K: continue in the left tensor at the right tensor's next dim, measuring
+    // contiguity from that dim's own stride
+    int64_t const l_k_id = l_r.valid() ? l_r.id() : 0;
+    while( l_l.valid() && !( l_l.type() == dim_t::K && l_l.id() == l_k_id ) ) l_l.step( size_at( l_l ) );
+    if( l_l.valid() ) l_l.cont = l_l.strides->at( l_l.id() );
+    block_pair( dim_t::K, l_l, l_r, i_dim_sizes, m_size_kb_min, m_size_kb_max, *o_dim_ids_kb );
+
+    // N: the output's next N dim and the same dim in the right tensor
+    while( l_o.valid() && l_o.type() != dim_t::N ) l_o.step( size_at( l_o ) );
+    int64_t const l_n_id = l_o.valid() ? l_o.id() : 0;
+    while( l_r.valid() && !( l_r.type() == dim_t::N && l_r.id() == l_n_id ) ) l_r.step( size_at( l_r ) );
+    if( l_r.valid() ) l_r.cont = l_r.strides->at( l_r.id() );
+    if( l_o.valid() ) l_o.cont = l_o.strides->at( l_o.id() );
+    block_pair( dim_t::N, l_o, l_r, i_dim_sizes, m_size_nb_min, m_size_nb_max, *o_dim_ids_nb );
+  }
+  else {
+    // the inputs' innermost dims (left M then K, right K then N) are not
+    // blocked; C is found right behind them
+    while( l_l.valid() && l_l.type() == dim_t::M ) l_l.step( size_at( l_l ) );
+    while( l_l.valid() && l_l.type() == dim_t::K ) l_l.step( size_at( l_l ) );
+    while( l_r.valid() && l_r.type() == dim_t::K ) l_r.step( size_at( l_r ) );
+    while( l_r.valid() && l_r.type() == dim_t::N ) l_r.step( size_at( l_r ) );
+    if( !block_c( l_l, l_r, l_o, i_dim_sizes, *o_dim_ids_cb ) ) return err_t::SUCCESS;
+
+    // M, K and N from the inputs' innermost dims again
+    l_l.pos = i_num_dims_left - 1;
+    l_l.cont = 1;
+    l_r.pos = i_num_dims_right - 1;
+    l_r.cont = 1;
+    block_pair( dim_t::M, l_o, l_l, i_dim_sizes, m_size_mb_min, m_size_mb_max, *o_dim_ids_mb );
+    block_pair( dim_t::K, l_l, l_r, i_dim_sizes, m_size_kb_min, m_size_kb_max, *o_dim_ids_kb );
+    while( l_o.valid() && l_o.type() != dim_t::N ) l_o.pos--;
+    if( l_o.valid() ) l_o.cont = l_o.strides->at( l_o.id() );
+    block_pair( dim_t::N, l_o, l_r, i_dim_sizes, m_size_nb_min, m_size_nb_max, *o_dim_ids_nb );
+  }
+
+  // row-major order
+  std::reverse( o_dim_ids_cb->begin(), o_dim_ids_cb->end() );
+  std::reverse( o_dim_ids_mb->begin(), o_dim_ids_mb->end() );
+  std::reverse( o_dim_ids_nb->begin(), o_dim_ids_nb->end() );
+  std::reverse( o_dim_ids_kb->begin(), o_dim_ids_kb->end() );
+  return err_t::SUCCESS;
+}

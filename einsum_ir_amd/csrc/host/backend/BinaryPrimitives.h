@@ -4,9 +4,11 @@
 //                   (reference src/backend/BinaryPrimitives.cpp:87-134);
 //   init         -- block-size targets per dtype/backend (:25-85; HIP added);
 //   reorder      -- internal dimension order of both children for a tensor
-//                   ordering (:833-1711) or a backend (:1713-1768).
-// The blocking_* routines and compileLoopOrder of the reference are not part
-// of the tree path and are not provided.
+//                   ordering (:833-1711) or a backend (:1713-1768);
+//   blocking     -- the blocked C/M/N/K dims a primitive can take directly
+//                   from the tensors' innermost dims (:136-831).
+// compileLoopOrder / splitDimension of the reference (:1770-...) are neither
+// called by the reference nor covered by its tests and are not provided.
 #ifndef EINSUM_IR_BACKEND_BINARY_PRIMITIVES
 #define EINSUM_IR_BACKEND_BINARY_PRIMITIVES
 
@@ -83,6 +85,30 @@ class einsum_ir::backend::BinaryPrimitives {
                    int64_t                            * io_dim_ids_left,
                    int64_t                            * io_dim_ids_right,
                    int64_t                            * io_dim_ids_out ) const;
+
+    /**
+     * Blocked dims for a primitive blocking (reference BinaryPrimitives.cpp:728-831):
+     * walks the tensors from their innermost dims and collects, per type, the
+     * dims that are stored contiguously in every tensor that holds them and
+     * that keep the block within the size targets of init.  Strides default
+     * to the row-major strides of the dim orders when a map is null.
+     * Outputs are in row-major order (outermost first).
+     **/
+    err_t blocking( primblo_t                            i_primitive_blocking,
+                    int64_t                              i_num_dims_left,
+                    int64_t                              i_num_dims_right,
+                    int64_t                              i_num_dims_out,
+                    int64_t                      const * i_dim_ids_left,
+                    int64_t                      const * i_dim_ids_right,
+                    int64_t                      const * i_dim_ids_out,
+                    std::map< int64_t, int64_t > const * i_dim_sizes,
+                    std::map< int64_t, int64_t > const * i_strides_left,
+                    std::map< int64_t, int64_t > const * i_strides_right,
+                    std::map< int64_t, int64_t > const * i_strides_out,
+                    std::vector< int64_t >             * o_dim_ids_cb,
+                    std::vector< int64_t >             * o_dim_ids_mb,
+                    std::vector< int64_t >             * o_dim_ids_nb,
+                    std::vector< int64_t >             * o_dim_ids_kb ) const;
 
     err_t reorder( backend_t                            i_backend_type,
                    int64_t                              i_num_dims_left,

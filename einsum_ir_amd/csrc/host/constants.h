@@ -30,6 +30,12 @@ namespace einsum_ir {
   } tenord_t;
 
   typedef enum {
+    LEFT_KB_X_MB_CB_RIGHT_NB_X_KB_CB_OUT_NB_X_MB_CB = 0,
+    LEFT_X_CB_KB_MB_RIGHT_X_CB_NB_KB_OUT_NB_X_MB_CB = 1,
+    UNDEFINED_PRIMBLO                               = 99
+  } primblo_t;
+
+  typedef enum {
     SUCCESS                   =  0,
     COMPILATION_FAILED        =  1,
     DIMENSION_ORDERING_FAILED =  2,

@@ -6,9 +6,11 @@
 //   unary strides         reference src/backend/Unary.test.cpp:4-36
 //   histogram, substrings, unique path ids
 //                         reference src/frontend/EinsumExpression.test.cpp:4-61
-//   swap_inputs / reorder reference src/backend/BinaryPrimitives.test.cpp:4-62, 627-1198
+//   swap_inputs / blocking / reorder
+//                         reference src/backend/BinaryPrimitives.test.cpp:4-62, 64-626, 627-1198
 //   ASCII parsers         reference src/frontend/EinsumExpressionAscii.test.cpp:4-94
 // plus tests of this library's own planning code (memory arena, tree parser).
+#include <array>
 #include <cstdio>
 #include <cstdlib>
 #include <functional>
@@ -187,6 +189,79 @@ TEST( reorder_known_answers ) {
   // packed GEMM ordering (C blocks outside the K block)
   std::map< int64_t, int64_t > sp = { { 'a', 4 }, { 'b', 4 }, { 'c', 4 }, { 'x', 16 } };
   CHECK( reorder( T3, sp, "abx", "cax", "cbx", 4, 8, 32, 128, 16, 64, 64, 512 ) == "xab|xca|cbx" );
+}
+
+// blocked dims as "cb|mb|nb|kb" (single-character ids)
+static std::string blocking( primblo_t i_pb, std::map< int64_t, int64_t > const & i_sizes,
+                             char const * i_left, char const * i_right, char const * i_out,
+                             std::array< int64_t, 8 > i_targets,
+                             std::map< int64_t, int64_t > const * i_sl = nullptr,
+                             std::map< int64_t, int64_t > const * i_sr = nullptr,
+                             std::map< int64_t, int64_t > const * i_so = nullptr ) {
+  backend::BinaryPrimitives l_bp;
+  l_bp.init( i_targets[0], i_targets[1], i_targets[2], i_targets[3],
+             i_targets[4], i_targets[5], i_targets[6], i_targets[7] );
+  std::vector< int64_t > l_l = ids( i_left ), l_r = ids( i_right ), l_o = ids( i_out );
+  std::vector< int64_t > l_cb, l_mb, l_nb, l_kb;
+  err_t l_err = l_bp.blocking( i_pb, (int64_t) l_l.size(), (int64_t) l_r.size(), (int64_t) l_o.size(),
+                               l_l.data(), l_r.data(), l_o.data(), &i_sizes, i_sl, i_sr, i_so,
+                               &l_cb, &l_mb, &l_nb, &l_kb );
+  if( l_err != err_t::SUCCESS ) return "error";
+  std::string l_s;
+  bool l_first = true;
+  for( auto const * l_v : { &l_cb, &l_mb, &l_nb, &l_kb } ) {
+    if( !l_first ) l_s += "|";
+    l_first = false;
+    for( int64_t l_id : *l_v ) l_s += char( l_id );
+  }
+  return l_s;
+}
+
+// reference src/backend/BinaryPrimitives.test.cpp:64-626
+TEST( blocking_known_answers ) {
+  primblo_t const B1 = primblo_t::LEFT_KB_X_MB_CB_RIGHT_NB_X_KB_CB_OUT_NB_X_MB_CB;
+  primblo_t const B2 = primblo_t::LEFT_X_CB_KB_MB_RIGHT_X_CB_NB_KB_OUT_NB_X_MB_CB;
+  std::array< int64_t, 8 > const small = { 2, 8, 2, 8, 2, 8, 2, 8 };
+  std::array< int64_t, 8 > const tccg = { 4, 8, 32, 128, 16, 64, 64, 512 };
+  std::array< int64_t, 8 > const tccg_large_m = { 4, 8, 32, 4096, 16, 64, 64, 512 };
+  // matrix-matrix multiplication
+  std::map< int64_t, int64_t > s3 = { { 'a', 2 }, { 'b', 2 }, { 'c', 2 } };
+  CHECK( blocking( B1, s3, "ab", "ca", "cb", small ) == "|b|c|a" );
+  // non-contiguous strides: only d (M) and e, f (N) are blocked
+  std::map< int64_t, int64_t > s6 = { { 'a', 2 }, { 'b', 2 }, { 'c', 2 }, { 'd', 2 }, { 'e', 2 }, { 'f', 2 } };
+  std::map< int64_t, int64_t > sl = { { 'd', 1 }, { 'c', 2 }, { 'b', 4 }, { 'a', 8 } };
+  std::map< int64_t, int64_t > sr = { { 'b', 3 }, { 'a', 6 }, { 'f', 12 }, { 'e', 24 } };
+  std::map< int64_t, int64_t > so = { { 'd', 1 }, { 'c', 3 }, { 'f', 6 }, { 'e', 12 } };
+  CHECK( blocking( B1, s6, "abcd", "efab", "efcd", small, &sl, &sr, &so ) == "|d|ef|" );
+  // high-dimensional contraction (integer ids 0..14): one dim per blocked type
+  {
+    std::map< int64_t, int64_t > sz = { { 0, 32 }, { 1, 96 }, { 2, 3 }, { 3, 3 }, { 4, 3 }, { 5, 3 }, { 6, 2 },
+                                        { 7, 2 }, { 8, 64 }, { 9, 2 }, { 10, 2 }, { 11, 64 }, { 12, 2 },
+                                        { 13, 2 }, { 14, 64 } };
+    int64_t const l_l[8] = { 12, 13, 2, 3, 9, 10, 11, 14 };
+    int64_t const l_r[5] = { 0, 9, 10, 1, 11 };
+    int64_t const l_o[5] = { 0, 1, 12, 13, 14 };
+    backend::BinaryPrimitives l_bp;
+    l_bp.init( 4, 16, 32, 128, 12, 64, 32, 512 );
+    std::vector< int64_t > l_cb, l_mb, l_nb, l_kb;
+    CHECK( l_bp.blocking( B1, 8, 5, 5, l_l, l_r, l_o, &sz, nullptr, nullptr, nullptr,
+                          &l_cb, &l_mb, &l_nb, &l_kb ) == err_t::SUCCESS );
+    CHECK( l_cb.size() == 0 && l_mb.size() == 1 && l_nb.size() == 1 && l_kb.size() == 1 );
+  }
+  // TCCG setting #1, plain and reordered, with and without a batch dim
+  std::map< int64_t, int64_t > st = { { 'a', 48 }, { 'b', 36 }, { 'c', 24 }, { 'd', 36 }, { 'e', 48 }, { 'f', 36 },
+                                      { 'x', 16 } };
+  CHECK( blocking( B1, st, "efbad", "cf", "abcde", tccg ) == "||c|f" );
+  CHECK( blocking( B1, st, "fbade", "cf", "abcde", tccg ) == "|e|c|f" );
+  CHECK( blocking( B1, st, "efbadx", "cfx", "abcdex", tccg ) == "x||c|f" );
+  CHECK( blocking( B1, st, "fbadex", "cfx", "abcdex", tccg ) == "x|e|c|f" );
+  CHECK( blocking( B1, st, "fbadex", "cfx", "abcdex", tccg_large_m ) == "x|de|c|f" );
+  CHECK( blocking( B1, st, "fbade", "cf", "abcde", tccg_large_m ) == "|de|c|f" );
+  // batched GEMM: left kb cb mb, right nb cb kb, out nb mb cb
+  std::map< int64_t, int64_t > sb = { { 'a', 2 }, { 'b', 3 }, { 'c', 2 }, { 'd', 2 } };
+  CHECK( blocking( B2, sb, "abc", "adb", "dca", small ) == "a|c|d|b" );
+  // unknown blocking
+  CHECK( blocking( primblo_t::UNDEFINED_PRIMBLO, s3, "ab", "ca", "cb", small ) == "error" );
 }
 
 TEST( ascii_parsers ) {
