@@ -16,17 +16,40 @@ namespace etir {
 namespace {
 
 __global__ __launch_bounds__( 256 ) void split_reduce_kernel( SplitReduceArgs a ) {
-  int64_t const l_total = int64_t( a.C ) * a.M * a.N;
-  int64_t const l_e = int64_t( blockIdx.x ) * 256 + threadIdx.x;
+  // element index -> (c, m, n); 32-bit division when the index range allows
+  // (the common case: 64-bit division is a long instruction sequence)
+  uint64_t const l_total = uint64_t( a.C ) * uint64_t( a.M ) * uint64_t( a.N );
+  uint64_t const l_e = uint64_t( blockIdx.x ) * 256 + threadIdx.x;
   if( l_e >= l_total ) return;
-  int32_t const l_n = int32_t( l_e % a.N );
-  int64_t const l_cm = l_e / a.N;
-  int32_t const l_m = int32_t( l_cm % a.M );
-  int32_t const l_c = int32_t( l_cm / a.M );
+  int32_t l_n, l_m, l_c;
+  if( l_total <= 0xffffffffull ) {
+    uint32_t const l_e32 = uint32_t( l_e );
+    uint32_t const l_cm = l_e32 / uint32_t( a.N );
+    l_n = int32_t( l_e32 - l_cm * uint32_t( a.N ) );
+    l_c = int32_t( l_cm / uint32_t( a.M ) );
+    l_m = int32_t( l_cm - uint32_t( l_c ) * uint32_t( a.M ) );
+  }
+  else {
+    uint64_t const l_cm = l_e / uint64_t( a.N );
+    l_n = int32_t( l_e - l_cm * uint64_t( a.N ) );
+    l_c = int32_t( l_cm / uint64_t( a.M ) );
+    l_m = int32_t( l_cm - uint64_t( l_c ) * uint64_t( a.M ) );
+  }
   int64_t const l_off = a.tc_out[l_c] + a.tm_out[l_m] + a.tn_out[l_n];
 
+  // slices summed in ascending order; the loads of 8 slices are issued
+  // before their additions so that they are in flight together
   float l_v = 0.0f;
-  for( int32_t l_s = 0; l_s < a.S; l_s++ ) l_v += a.ws[l_off + l_s * a.span];
+  float const * l_p = a.ws + l_off;
+  int32_t l_s = 0;
+  for( ; l_s + 8 <= a.S; l_s += 8 ) {
+    float l_x[8];
+#pragma unroll
+    for( int l_i = 0; l_i < 8; l_i++ ) l_x[l_i] = l_p[int64_t( l_s + l_i ) * a.span];
+#pragma unroll
+    for( int l_i = 0; l_i < 8; l_i++ ) l_v += l_x[l_i];
+  }
+  for( ; l_s < a.S; l_s++ ) l_v += l_p[int64_t( l_s ) * a.span];
 
   bool const l_read_out  = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_UNDEFINED );
   bool const l_aux_first = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_COPY );
