@@ -21,7 +21,10 @@ the committed rocprofv3 --pmc summary under profiles/ when present.
 
 `cpu_baseline` times the CPU restatement of the reference algorithm
 (oracle/oracle.c: fused loops, OpenMP tasks, packed fp32 blocked GEMM) on a
-bounded sample of the same workload on the host cores.
+bounded sample of the same workload on the host cores; torch.einsum on the
+host (the comparator the reference's harnesses print) is timed on the same
+sample under extra["cpu_torch_einsum_c3_slice"], next to a probe of the host
+(CPU model, cores, whether libxsmm / OpenBLAS are installed).
 """
 import argparse
 import json
@@ -44,7 +47,7 @@ def parse_args():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", default="", help="comma list of configs to run (c1,c2,c3,c4,c5,mlp)")
+    p.add_argument("--only", default="", help="comma list of configs to run (c1,c2,c3,c4,c5,mlp,samples)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also time a plain 512 MiB device copy (reference for the PMC byte counters)")
     p.add_argument("--settle", type=float, default=1.0,
@@ -192,6 +195,48 @@ def bench_c5(torch, eir, stream, steps, warmup):
     return res
 
 
+def _expression_rate(torch, stream, expr, sizes_arg, path_arg, steps, warmup, seed):
+    """Builds an EinsumExpression of a sample workload (inputs from
+    harness.scaled_randn), times eval_async; returns (num_ops, s per eval)."""
+    from einsum_ir_amd import harness, host
+    ins, out = harness._tensors(expr)
+    sizes = harness._sizes(expr, sizes_arg)
+    path = harness._parse_path(path_arg)
+    data = harness.scaled_randn(torch, ins, out, sizes, seed, torch.float32)
+    dout = torch.empty([sizes[d] for d in out], device="cuda", dtype=torch.float32)
+    e = host.Expression(expr, sizes, path, data + [dout], stream=stream)
+    _, per = time_launches(torch, stream, e.eval_async, steps, warmup)
+    n = e.num_ops()
+    e.close()
+    return n, per
+
+
+def bench_samples(torch, eir, stream):
+    """The reference's sample workloads (tests/golden/einsum_samples.json):
+    the 59 TCCG binary contractions and the four einsum_benchmark networks at
+    full size, fp32, each through EinsumExpression along its recorded path.
+    Rates use num_ops() (the reference harnesses' flop count)."""
+    import math
+    fx = json.load(open(os.path.join(ROOT, "tests", "golden", "einsum_samples.json")))
+    rates = []
+    for c in fx["tccg"]:
+        n, per = _expression_rate(torch, stream, c["expr"], c["sizes"], c["path"], 10, 2,
+                                  sum(map(ord, c["expr"])))
+        rates.append((n / per * 1e-9, c["expr"]))
+    gm = math.exp(sum(math.log(r) for r, _ in rates) / len(rates))
+    lo, hi = min(rates), max(rates)
+    tccg = dict(cases=len(rates), unit="GFLOP/s", geomean=round(gm, 1),
+                frac_fp32_peak_geomean=round(gm / (PEAK_FP32_TFLOPS * 1e3), 4),
+                min=[round(lo[0], 1), lo[1]], max=[round(hi[0], 1), hi[1]])
+    nets = {}
+    for name, c in fx["einsum_benchmark"].items():
+        n, per = _expression_rate(torch, stream, c["expr"], c["sizes"], c["path"], 3, 1, 11)
+        nets[name] = dict(gflop=round(n * 1e-9, 2), ms_per_eval=round(per * 1e3, 3),
+                          value=round(n / per * 1e-9, 1), unit="GFLOP/s",
+                          frac_fp32_peak=round(n / per * 1e-12 / PEAK_FP32_TFLOPS, 4))
+    return tccg, nets
+
+
 def bench_mlp(torch, eir, stream, steps, warmup):
     """The reference's bench_mlp tree (src/bench_mlp.cpp:85-307): 784-512-512-
     512-512-10 MLP on a batch of 18 x 64, built node by node, bias COPY first
@@ -249,6 +294,42 @@ def cpu_baseline_c3():
                 sample=f"config-3 slice z=1,a=16 (M=1024,N=4096,K=1024; {flops/1e9:.2f} GFLOP) x{reps}, "
                        "fp32 math on the bf16-rounded inputs (the reference has no bf16 path); "
                        "oracle/oracle.c oracle_contract_blocked, OpenMP")
+
+
+def cpu_torch_einsum_c3(threads):
+    """torch.einsum on the host (the comparator the reference harnesses print,
+    reference src/bench_binary.cpp:62-87) on the same config-3 slice as
+    cpu_baseline_c3, fp32 on the bf16-rounded inputs."""
+    import torch
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(3)
+    a = (torch.rand(1, 16, 1024, 64, generator=g) * 2 - 1).bfloat16().float()
+    b = (torch.rand(1, 64, 1024, 64, generator=g) * 2 - 1).bfloat16().float()
+    flops = 2 * 1024 * 4096 * 1024
+    torch.einsum("zakm,zbkn->zabmn", a, b)   # warm-up
+    reps, t = 0, 0.0
+    while t < 5.0 and reps < 50:
+        t0 = time.perf_counter()
+        torch.einsum("zakm,zbkn->zabmn", a, b)
+        t += time.perf_counter() - t0
+        reps += 1
+    return dict(value=round(flops * reps / t * 1e-9, 2), unit="GFLOP/s", cores=threads,
+                sample=f"config-3 slice z=1,a=16 (M=1024,N=4096,K=1024) x{reps}, fp32, "
+                       f"torch {torch.__version__} CPU ({'MKL' if torch.backends.mkl.is_available() else 'no MKL'})")
+
+
+def cpu_host_probe():
+    """CPU model, core count and whether the reference's CPU libraries
+    (libxsmm, OpenBLAS) are installed on this host."""
+    import ctypes.util
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+    except OSError:
+        pass
+    return dict(cpu_model=model, nproc=os.cpu_count(),
+                libxsmm=ctypes.util.find_library("xsmm"), openblas=ctypes.util.find_library("openblas"))
 
 
 def main():
@@ -325,10 +406,21 @@ def main():
                                                       "weights locked")
         log(f"mlp: {mlp['per_launch']*1e6:.1f} us/eval")
 
+    if run("samples"):
+        tccg, nets = bench_samples(torch, eir, stream)
+        extra["tccg_fp32"] = tccg
+        extra["einsum_benchmark_fp32"] = nets
+        log(f"tccg: {tccg}")
+        for name, r in nets.items():
+            log(f"{name}: {r}")
+
     cpu = None
     if not args.no_cpu_baseline and run("c3"):
         cpu = cpu_baseline_c3()
         log(f"cpu baseline: {cpu}")
+        extra["cpu_torch_einsum_c3_slice"] = cpu_torch_einsum_c3(cpu["cores"])
+        extra["cpu_host"] = cpu_host_probe()
+        log(f"cpu torch.einsum: {extra['cpu_torch_einsum_c3_slice']}; host: {extra['cpu_host']}")
 
     if c3 is None:
         print(json.dumps({"extra": extra}))

@@ -92,6 +92,61 @@ def _torch_einsum(ins, out, sizes):
     return ",".join("".join(letters[d] for d in t) for t in ins) + "->" + "".join(letters[d] for d in out)
 
 
+def _letters(dims):
+    """Einsum letters for at most 52 distinct dims (torch.einsum's alphabet)."""
+    m = {}
+    for d in dims:
+        if d not in m:
+            n = len(m)
+            m[d] = chr(ord("a") + n) if n < 26 else chr(ord("A") + n - 26)
+    return m
+
+
+def torch_pair(torch, da, a, db, b, dr):
+    """One binary contraction a[da] * b[db] -> [dr] with torch.einsum, letters
+    chosen per contraction so that expressions with more than 52 dims work."""
+    m = _letters(list(da) + list(db))
+    eq = "".join(m[d] for d in da) + "," + "".join(m[d] for d in db) + "->" + "".join(m[d] for d in dr)
+    return torch.einsum(eq, a, b)
+
+
+def torch_path_eval(torch, ins, out, sizes, path, data):
+    """Evaluates an expression along its contraction path (opt_einsum's
+    standard form: the pair is removed, the result appended) with torch.einsum
+    in the dtype of `data`; intermediate dims are those still needed by the
+    remaining tensors or the output."""
+    ts = [(list(t), x) for t, x in zip(ins, data)]
+    for i, j in path:
+        (da, a), (db, b) = ts[i], ts[j]
+        rest = [ts[k] for k in range(len(ts)) if k not in (i, j)]
+        keep = set(out) | {d for t, _ in rest for d in t}
+        dr = [d for d in dict.fromkeys(da + db) if d in keep]
+        ts = rest + [(dr, torch_pair(torch, da, a, db, b, dr))]
+    if len(ts) != 1:
+        raise ValueError("contraction path does not reduce the expression to one tensor")
+    dr, r = ts[0]
+    return r.permute([dr.index(d) for d in out]) if dr != list(out) else r
+
+
+def scaled_randn(torch, ins, out, sizes, seed, dtype):
+    """N(0,1) inputs, tensor t scaled by prod(size of its contracted dims)^-1/4.
+    A contracted dim of size s is shared by two tensors, so the products that
+    its sum adds up have variance 1/s and the s-term sum variance 1: every
+    contraction of a network keeps the values near unit magnitude (long
+    networks leave the fp32 range otherwise)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    outs = set(out)
+    data = []
+    for t in ins:
+        x = torch.randn([sizes[d] for d in t], device="cuda", dtype=torch.float64, generator=g)
+        k = 1
+        for d in t:
+            if d not in outs:
+                k *= sizes[d]
+        data.append((x / k ** 0.25).to(dtype))
+    return data
+
+
 def _close(torch, ref, got, rtol=1e-3, atol=1e-4):
     ok = torch.allclose(ref.to(got.dtype), got, rtol=rtol, atol=atol)
     print("  results are close" if ok else f"  maximal difference is: {(ref.to(got.dtype) - got).abs().max().item()}")
@@ -235,10 +290,15 @@ def bench_expression(argv):
     print(f"  gflops (total): {flops / (t + t_compile) * 1e-9}")
     print(f"CSV_DATA: einsum_ir,\"{expr}\",\"{sizes_arg}\",\"{path_arg}\",{flops},{t_compile},{t},"
           f"{flops / t * 1e-9},{flops / (t + t_compile) * 1e-9}")
-    eq = _torch_einsum(ins, out, sizes)
     hi = torch.complex128 if ctype != host.REAL_ONLY else torch.float64
-    ref = torch.einsum(eq, *[d.to(hi) for d in data])
-    tt = _timed(torch, lambda: torch.einsum(eq, *data))
+    if len(sizes) <= 52:
+        eq = _torch_einsum(ins, out, sizes)
+        ref = torch.einsum(eq, *[d.to(hi) for d in data])
+        tt = _timed(torch, lambda: torch.einsum(eq, *data))
+    else:
+        # more dims than torch.einsum has letters: contract along the path
+        ref = torch_path_eval(torch, ins, out, sizes, path, [d.to(hi) for d in data])
+        tt = _timed(torch, lambda: torch_path_eval(torch, ins, out, sizes, path, data))
     print("torch.einsum:")
     print(f"  time (eval):    {tt}")
     print(f"  gflops (eval):  {flops / tt * 1e-9}")
@@ -291,6 +351,22 @@ def _parse_tree(s):
     return nodes
 
 
+def torch_tree_eval(torch, nodes, tensors, dtype):
+    """Values of every node of a parsed tree (post-order list from
+    _parse_tree), computed node by node with torch.einsum in `dtype`."""
+    vals = []
+    for (dims, kids), t_in in zip(nodes, tensors):
+        if not kids:
+            vals.append(t_in.to(dtype))
+        elif len(kids) == 1:
+            src = nodes[kids[0]][0]
+            vals.append(vals[kids[0]].permute([src.index(d) for d in dims]))
+        else:
+            (da, db) = nodes[kids[0]][0], nodes[kids[1]][0]
+            vals.append(torch_pair(torch, da, vals[kids[0]], db, vals[kids[1]], dims))
+    return vals
+
+
 def bench_tree(argv):
     import torch
     tree, sizes_arg = argv[0], argv[1]
@@ -324,14 +400,7 @@ def bench_tree(argv):
           f"{flops / (t + t_compile) * 1e-9}")
 
     # reference: evaluate the tree with torch.einsum node by node in float64
-    vals = []
-    letters = lambda ds: "".join(chr(ord("a") + d) if d < 26 else chr(ord("A") + d - 26) for d in ds)
-    for (dims, kids), t_in in zip(nodes, tensors):
-        if not kids:
-            vals.append(t_in.double())
-        else:
-            eq = ",".join(letters(nodes[k][0]) for k in kids) + "->" + letters(dims)
-            vals.append(torch.einsum(eq, *[vals[k] for k in kids]))
+    vals = torch_tree_eval(torch, nodes, tensors, torch.float64)
     ok = _close(torch, vals[-1], root)
     tr.close()
     return 0 if ok else 1
