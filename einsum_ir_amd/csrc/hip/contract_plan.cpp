@@ -18,7 +18,8 @@
 //      the output is M-contiguous, so that epilogue stores coalesce;
 //   3. inside each type the loops are ordered so that the operand's
 //      unit-stride loop is innermost (the analogue of choosing the
-//      primitive's unit-stride m/k loops);
+//      primitive's unit-stride m/k loops); kernel rows the A operand is not
+//      contiguous along follow the output's order instead;
 //   4. the tables are enumerated and inspected: runs of consecutive offsets
 //      select 16-byte vector loads along M/N or along K; a single-loop K index
 //      becomes an affine offset (no table reads in the K loop);
@@ -310,9 +311,12 @@ int plan_contraction_impl( int64_t            num_loops,
   int64_t const l_esz = ( dtype_left == ETIR_BF16 ) ? 2 : ( dtype_left == ETIR_FP64 ? 8 : 4 );
   int64_t const l_vk  = 16 / l_esz;   // elements per 16-byte vector
 
-  // ordering
-  order_dims( l_km, l_sa );
-  unit_innermost( l_km, l_sa );
+  // ordering: kernel rows follow A when A is read along them, otherwise the
+  // output (neighbouring tile rows then sit close in memory for the stores)
+  bool l_a_unit_m = false;
+  for( Loop const & l_x : l_km ) if( l_x.s[l_sa] == 1 ) l_a_unit_m = true;
+  order_dims( l_km, l_a_unit_m ? l_sa : T_OUT );
+  if( l_a_unit_m ) unit_innermost( l_km, l_sa );
   order_dims( l_kn, T_OUT );
   if( !unit_innermost( l_kn, T_OUT ) ) unit_innermost( l_kn, l_sb );
   // K: the operand whose unit-stride loop is a K loop decides the order

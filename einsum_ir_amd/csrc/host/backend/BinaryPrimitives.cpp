@@ -222,8 +222,13 @@ einsum_ir::err_t einsum_ir::backend::BinaryPrimitives::reorder( backend_t       
   BinaryContraction::dim_types( i_num_dims_left, i_num_dims_right, i_num_dims_out,
                                 io_dim_ids_left, io_dim_ids_right, io_dim_ids_out,
                                 &l_t_left, &l_t_right, &l_t_out );
+  if( i_backend_type == backend_t::HIP ) {
+    // both children laid out for the GPU kernel (fp32 vector width)
+    return reorder_gpu( false, false, 4, 4, 0, i_num_dims_left, i_num_dims_right, i_num_dims_out,
+                        i_dim_sizes, io_dim_ids_left, io_dim_ids_right, io_dim_ids_out );
+  }
   tenord_t l_ord = tenord_t::LEFT_NATIVE_RIGHT_NATIVE_OUT_NATIVE;
-  if( i_backend_type == backend_t::TPP || i_backend_type == backend_t::TBLIS || i_backend_type == backend_t::HIP ) {
+  if( i_backend_type == backend_t::TPP || i_backend_type == backend_t::TBLIS ) {
     l_ord = tenord_t::LEFT_BC_BM_BK_BI_KB_MB_CB_RIGHT_BC_BN_BK_BJ_NB_KB_CB_OUT_NATIVE;
   }
   else if( i_backend_type == backend_t::BLAS ) {
@@ -233,6 +238,142 @@ einsum_ir::err_t einsum_ir::backend::BinaryPrimitives::reorder( backend_t       
   }
   return reorder( l_ord, i_num_dims_left, i_num_dims_right, i_num_dims_out, i_dim_sizes,
                   io_dim_ids_left, io_dim_ids_right, io_dim_ids_out );
+}
+
+einsum_ir::err_t einsum_ir::backend::BinaryPrimitives::reorder_gpu( bool                                 i_fixed_left,
+                                                                    bool                                 i_fixed_right,
+                                                                    int64_t                              i_vec,
+                                                                    int64_t                              i_bytes_per_element,
+                                                                    int64_t                              i_min_bytes_permute,
+                                                                    int64_t                              i_num_dims_left,
+                                                                    int64_t                              i_num_dims_right,
+                                                                    int64_t                              i_num_dims_out,
+                                                                    std::map< int64_t, int64_t > const * i_dim_sizes,
+                                                                    int64_t                            * io_dim_ids_left,
+                                                                    int64_t                            * io_dim_ids_right,
+                                                                    int64_t                            * io_dim_ids_out ) {
+  std::vector< dim_t > l_t[2], l_t_out;
+  BinaryContraction::dim_types( i_num_dims_left, i_num_dims_right, i_num_dims_out,
+                                io_dim_ids_left, io_dim_ids_right, io_dim_ids_out,
+                                &l_t[0], &l_t[1], &l_t_out );
+  int64_t * l_ids[2] = { io_dim_ids_left, io_dim_ids_right };
+  int64_t const l_nd[2] = { i_num_dims_left, i_num_dims_right };
+  bool const l_fixed[2] = { i_fixed_left, i_fixed_right };
+  dim_t const l_own[2] = { dim_t::M, dim_t::N };
+  auto size_of = [&]( int64_t i_id ) -> int64_t {
+    auto l_it = i_dim_sizes->find( i_id );
+    return l_it != i_dim_sizes->end() ? l_it->second : 1;
+  };
+
+  // the kernel's column side holds the output's unit-stride dim: the left
+  // operand if that dim is an M dim (the planner then swaps the roles)
+  int64_t const l_o_last = i_num_dims_out > 0 ? io_dim_ids_out[i_num_dims_out - 1] : -1;
+  int const l_col_side = ( i_num_dims_out > 0 && l_t_out.back() == dim_t::M ) ? 0 : 1;
+
+  // extents of each child's own M/N dims and of the K dims, and its bytes
+  int64_t l_ext_mn[2] = { 1, 1 };
+  int64_t l_ext_k = 1;
+  int64_t l_bytes[2] = { i_bytes_per_element, i_bytes_per_element };
+  for( int l_s = 0; l_s < 2; l_s++ ) {
+    for( int64_t l_d = 0; l_d < l_nd[l_s]; l_d++ ) {
+      int64_t const l_sz = size_of( l_ids[l_s][l_d] );
+      l_bytes[l_s] *= l_sz;
+      if( l_t[l_s][l_d] == l_own[l_s] ) l_ext_mn[l_s] *= l_sz;
+      if( l_s == 0 && l_t[l_s][l_d] == dim_t::K ) l_ext_k *= l_sz;
+    }
+  }
+
+  // the output's unit-stride run on the column side (its trailing dims of
+  // the column side's type) and its innermost row-side dim: when the run is
+  // shorter than a 32-lane store row, consecutive tile rows have to be
+  // neighbours in memory for the stores to fill whole lines
+  dim_t const l_col_type = l_own[l_col_side];
+  int64_t l_col_run = 1;
+  for( int64_t l_o = i_num_dims_out - 1; l_o >= 0 && l_t_out[l_o] == l_col_type; l_o-- ) {
+    l_col_run *= size_of( io_dim_ids_out[l_o] );
+  }
+  int64_t l_o_row_last = -1;
+  for( int64_t l_o = i_num_dims_out - 1; l_o >= 0; l_o-- ) {
+    if( l_t_out[l_o] == l_own[1 - l_col_side] ) {
+      l_o_row_last = io_dim_ids_out[l_o];
+      break;
+    }
+  }
+
+  // per child: 0 = lay out again, 1 = keep (read along M/N), 2 = keep (read
+  // along K), 3 = keep (gathered: little data)
+  int l_keep[2] = { 0, 0 };
+  for( int l_s = 0; l_s < 2; l_s++ ) {
+    if( !l_fixed[l_s] || l_nd[l_s] == 0 ) continue;
+    int64_t const l_in = l_ids[l_s][l_nd[l_s] - 1];
+    dim_t const l_ty = l_t[l_s][l_nd[l_s] - 1];
+    bool const l_vec_ok = size_of( l_in ) % i_vec == 0;
+    // element gathers of this child are repeated for every tile of the other
+    // side (128 columns or rows per tile)
+    int64_t const l_gathered = l_bytes[l_s] * std::max< int64_t >( 1, l_ext_mn[1 - l_s] / 128 );
+    if( l_vec_ok && l_ty == dim_t::K ) l_keep[l_s] = 2;
+    else if(    l_vec_ok && l_ty == l_own[l_s]
+             && ( l_s == l_col_side ? l_in == l_o_last : ( l_col_run >= 32 || l_in == l_o_row_last ) ) ) {
+      l_keep[l_s] = 1;
+    }
+    else if( l_gathered < i_min_bytes_permute ) l_keep[l_s] = 3;
+  }
+  // two K-read children must agree on the innermost K dim
+  if(    l_keep[0] == 2 && l_keep[1] == 2
+      && io_dim_ids_left[i_num_dims_left - 1] != io_dim_ids_right[i_num_dims_right - 1] ) {
+    l_keep[ l_bytes[0] < l_bytes[1] ? 0 : 1 ] = 0;
+  }
+
+  // shared K order: that of a child read along K as it is, else the left's
+  int l_k_src = 0;
+  if( l_keep[0] != 2 && l_keep[1] == 2 ) l_k_src = 1;
+  std::vector< int64_t > l_k_order;
+  for( int64_t l_d = 0; l_d < l_nd[l_k_src]; l_d++ ) {
+    if( l_t[l_k_src][l_d] == dim_t::K ) l_k_order.push_back( l_ids[l_k_src][l_d] );
+  }
+
+  for( int l_s = 0; l_s < 2; l_s++ ) {
+    if( l_keep[l_s] != 0 ) continue;
+    // the row-side operand M/N-contiguous, the column-side one K-contiguous
+    // (the kernel's fastest pairing), unless the extents rule out 16-byte
+    // vectors that way
+    bool l_mn_inner = ( l_s != l_col_side );
+    if( l_mn_inner && l_ext_mn[l_s] % i_vec != 0 && l_ext_k % i_vec == 0 ) l_mn_inner = false;
+    if( !l_mn_inner && l_ext_k % i_vec != 0 && l_ext_mn[l_s] % i_vec == 0 ) l_mn_inner = true;
+
+    std::vector< int64_t > l_c, l_mn, l_x;
+    for( dim_t l_ty : { dim_t::C, l_own[l_s] } ) {
+      std::vector< int64_t > & l_dst = ( l_ty == dim_t::C ) ? l_c : l_mn;
+      for( int64_t l_o = 0; l_o < i_num_dims_out; l_o++ ) {
+        if( l_t_out[l_o] != l_ty ) continue;
+        for( int64_t l_d = 0; l_d < l_nd[l_s]; l_d++ ) {
+          if( l_ids[l_s][l_d] == io_dim_ids_out[l_o] && l_t[l_s][l_d] == l_ty ) {
+            l_dst.push_back( l_ids[l_s][l_d] );
+            break;
+          }
+        }
+      }
+    }
+    // dims of this child only (I/J), in their order
+    for( int64_t l_d = 0; l_d < l_nd[l_s]; l_d++ ) {
+      if( l_t[l_s][l_d] != dim_t::C && l_t[l_s][l_d] != dim_t::K && l_t[l_s][l_d] != l_own[l_s] ) {
+        l_x.push_back( l_ids[l_s][l_d] );
+      }
+    }
+    std::vector< int64_t > l_new = l_c;
+    l_new.insert( l_new.end(), l_x.begin(), l_x.end() );
+    if( l_mn_inner ) {
+      l_new.insert( l_new.end(), l_k_order.begin(), l_k_order.end() );
+      l_new.insert( l_new.end(), l_mn.begin(), l_mn.end() );
+    }
+    else {
+      l_new.insert( l_new.end(), l_mn.begin(), l_mn.end() );
+      l_new.insert( l_new.end(), l_k_order.begin(), l_k_order.end() );
+    }
+    if( (int64_t) l_new.size() != l_nd[l_s] ) return err_t::DIMENSION_ORDERING_FAILED;
+    std::copy( l_new.begin(), l_new.end(), l_ids[l_s] );
+  }
+  return err_t::SUCCESS;
 }
 
 namespace {

@@ -5,6 +5,7 @@
 //   init         -- block-size targets per dtype/backend (:25-85; HIP added);
 //   reorder      -- internal dimension order of both children for a tensor
 //                   ordering (:833-1711) or a backend (:1713-1768);
+//   reorder_gpu  -- the HIP backend's own child layouts (no counterpart);
 //   blocking     -- the blocked C/M/N/K dims a primitive can take directly
 //                   from the tensors' innermost dims (:136-831).
 // compileLoopOrder / splitDimension of the reference (:1770-...) are neither
@@ -109,6 +110,48 @@ class einsum_ir::backend::BinaryPrimitives {
                     std::vector< int64_t >             * o_dim_ids_mb,
                     std::vector< int64_t >             * o_dim_ids_nb,
                     std::vector< int64_t >             * o_dim_ids_kb ) const;
+
+    /**
+     * Internal dim orders of both children for the HIP backend.  No
+     * counterpart in the reference: its TPP ordering serves libxsmm's
+     * column-major (packed) GEMMs and places the shared C dims innermost,
+     * where the GPU kernel -- which runs C loops in its grid and loads
+     * 16-byte vectors along an operand's unit-stride M/N or K loop -- has to
+     * gather single elements.
+     *   - A child the tree computes (i_fixed_* false) is laid out for the
+     *     kernel's fastest operand pairing: the operand on the kernel's row
+     *     side M/N-contiguous ([C, I/J, K, own M/N]), the one on the column
+     *     side -- the side of the output's unit-stride dim -- K-contiguous
+     *     ([C, own M/N, I/J, K]), unless the extents rule out 16-byte vectors
+     *     that way.  C and M/N dims follow the output's order, K dims one
+     *     order shared by both children, so that they fuse.
+     *   - A child whose layout is given (i_fixed_* true: a leaf) keeps it when
+     *     the kernel reads it with vector loads as it is -- innermost dim a K
+     *     dim, or an M/N dim on the row side (the output's innermost row-side
+     *     dim when the output's unit-stride run is shorter than 32 elements,
+     *     so that neighbouring tile rows are neighbours in memory), or the
+     *     output's innermost dim on the column side, with a size that is a
+     *     multiple of the vector width
+     *     i_vec -- or when the element gathers it needs (its bytes times the
+     *     tiles of the other side) stay below i_min_bytes_permute; otherwise
+     *     it is laid out like a computed child (one permutation of the leaf
+     *     per evaluation, none once locked).  Two given children whose
+     *     innermost K dims differ cannot both be read along K: the smaller one
+     *     is laid out again.
+     * The output keeps its order.
+     **/
+    static err_t reorder_gpu( bool                                 i_fixed_left,
+                              bool                                 i_fixed_right,
+                              int64_t                              i_vec,
+                              int64_t                              i_bytes_per_element,
+                              int64_t                              i_min_bytes_permute,
+                              int64_t                              i_num_dims_left,
+                              int64_t                              i_num_dims_right,
+                              int64_t                              i_num_dims_out,
+                              std::map< int64_t, int64_t > const * i_dim_sizes,
+                              int64_t                            * io_dim_ids_left,
+                              int64_t                            * io_dim_ids_right,
+                              int64_t                            * io_dim_ids_out );
 
     err_t reorder( backend_t                            i_backend_type,
                    int64_t                              i_num_dims_left,

@@ -175,8 +175,22 @@ einsum_ir::err_t einsum_ir::backend::EinsumNode::compile_recursive() {
       std::swap( m_children[0], m_children[1] );
     }
 
-    // internal dim orders of the children for the backend's tensor ordering
-    if( m_reorder_dims ) {
+    // internal dim orders of the children: the GPU kernel's layouts for the
+    // HIP backend (leaves keep theirs when the kernel reads them well as they
+    // are), the backend's tensor ordering otherwise
+    if( m_reorder_dims && m_btype_binary == backend_t::HIP ) {
+      int64_t const l_esz = ce_n_bytes( m_children[0]->m_dtype );
+      l_err = BinaryPrimitives::reorder_gpu( m_children[0]->m_children.empty(),
+                                             m_children[1]->m_children.empty(),
+                                             16 / l_esz, l_esz, int64_t( 2 ) << 20,
+                                             m_children[0]->m_num_dims, m_children[1]->m_num_dims, m_num_dims,
+                                             m_dim_sizes_inner,
+                                             m_children[0]->m_dim_ids_int.data(),
+                                             m_children[1]->m_dim_ids_int.data(),
+                                             m_dim_ids_int.data() );
+      if( l_err != err_t::SUCCESS ) return l_err;
+    }
+    else if( m_reorder_dims ) {
       BinaryPrimitives l_prims;
       l_prims.init( m_dtype, m_btype_binary );
       l_err = l_prims.reorder( m_btype_binary,
