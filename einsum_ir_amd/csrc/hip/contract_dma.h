@@ -612,7 +612,11 @@ void contract_dma_kernel( ContractArgs a ) {
 
   static_assert( EpilogueLds< BM, BN, WM, WN, TM, TN >::BYTES <= int( sizeof( l_lds ) ),
                  "LDS too small for the epilogue" );
-  epilogue< BM, BN, WM, WN, TM, TN, T >( a, l_acc, l_lds, l_c, l_m0, l_n0, l_wm, l_wn, l_lane );
+  // the offset tables are read here, not at the start: the main loop holds
+  // no registers for them
+  EpilogueTabs< BM, BN, T > l_tabs;
+  l_tabs.load( a, l_m0, l_n0 );
+  epilogue< BM, BN, WM, WN, TM, TN, T >( a, l_acc, l_tabs, l_lds, l_c, l_m0, l_n0, l_wm, l_wn, l_lane );
 }
 
 }  // namespace kern

@@ -432,9 +432,61 @@ __device__ __attribute__( ( always_inline ) ) inline void epilogue_fast_f32(
   } );
 }
 
+// The epilogue's output/aux offsets of the tile rows and columns, loaded into
+// registers when the workgroup starts (the loads complete under the main loop
+// instead of adding a memory round trip after it) and staged in LDS at the
+// epilogue.
+template< int BM, int BN, int T >
+struct EpilogueTabs {
+  static constexpr int NM = ( BM + T - 1 ) / T;
+  static constexpr int NN = ( BN + T - 1 ) / T;
+  int32_t m_out[NM], m_aux[NM], n_out[NN], n_aux[NN];
+
+  __device__ inline void load( ContractArgs const & a, int32_t l_m0, int32_t l_n0 ) {
+    bool const l_has_aux = ( a.aux != nullptr );
+#pragma unroll
+    for( int l_i = 0; l_i < NM; l_i++ ) {
+      int const l_x = threadIdx.x + l_i * T;
+      int32_t const l_m = l_m0 + l_x;
+      bool const l_ok = l_x < BM && l_m < a.M;
+      m_out[l_i] = l_ok ? a.tm_out[l_m] : 0;
+      m_aux[l_i] = ( l_ok && l_has_aux ) ? a.tm_aux[l_m] : 0;
+    }
+#pragma unroll
+    for( int l_i = 0; l_i < NN; l_i++ ) {
+      int const l_x = threadIdx.x + l_i * T;
+      int32_t const l_n = l_n0 + l_x;
+      bool const l_ok = l_x < BN && l_n < a.N;
+      n_out[l_i] = l_ok ? a.tn_out[l_n] : 0;
+      n_aux[l_i] = ( l_ok && l_has_aux ) ? a.tn_aux[l_n] : 0;
+    }
+  }
+
+  // LDS layout: m_out[BM], m_aux[BM], n_out[BN], n_aux[BN]
+  __device__ inline void stage( int32_t * lds ) const {
+#pragma unroll
+    for( int l_i = 0; l_i < NM; l_i++ ) {
+      int const l_x = threadIdx.x + l_i * T;
+      if( l_x < BM ) {
+        lds[l_x]      = m_out[l_i];
+        lds[BM + l_x] = m_aux[l_i];
+      }
+    }
+#pragma unroll
+    for( int l_i = 0; l_i < NN; l_i++ ) {
+      int const l_x = threadIdx.x + l_i * T;
+      if( l_x < BN ) {
+        lds[2 * BM + l_x]      = n_out[l_i];
+        lds[2 * BM + BN + l_x] = n_aux[l_i];
+      }
+    }
+  }
+};
+
 template< int BM, int BN, int WM, int WN, int TM, int TN, int T >
 __device__ __attribute__( ( always_inline ) ) inline void epilogue( ContractArgs const & a,
                                                                     f32x16 const ( &l_acc )[TM][TN],
+                                                                    EpilogueTabs< BM, BN, T > const & l_tabs,
                                                                     char * lds, int32_t l_c, int32_t l_m0,
                                                                     int32_t l_n0, int l_wm, int l_wn,
                                                                     int l_lane ) {
@@ -444,16 +496,7 @@ __device__ __attribute__( ( always_inline ) ) inline void epilogue( ContractArgs
   int32_t * l_s_n_out = l_s_m_aux + BM;
   int32_t * l_s_n_aux = l_s_n_out + BN;
   bool const l_has_aux = ( a.aux != nullptr );
-  for( int l_x = threadIdx.x; l_x < BM; l_x += T ) {
-    int32_t const l_m = l_m0 + l_x;
-    l_s_m_out[l_x] = ( l_m < a.M ) ? a.tm_out[l_m] : 0;
-    l_s_m_aux[l_x] = ( l_has_aux && l_m < a.M ) ? a.tm_aux[l_m] : 0;
-  }
-  for( int l_x = threadIdx.x; l_x < BN; l_x += T ) {
-    int32_t const l_n = l_n0 + l_x;
-    l_s_n_out[l_x] = ( l_n < a.N ) ? a.tn_out[l_n] : 0;
-    l_s_n_aux[l_x] = ( l_has_aux && l_n < a.N ) ? a.tn_aux[l_n] : 0;
-  }
+  l_tabs.stage( l_s_m_out );
   __syncthreads();
 
   int64_t const l_coff_out = a.tc_out[l_c];
@@ -570,6 +613,8 @@ void contract_kernel( ContractArgs a ) {
   Loader< BN, BK, T, ESZ, MB > l_ld_b;
   l_ld_a.init( a.tm_a, a.M, l_m0 );
   l_ld_b.init( a.tn_b, a.N, l_n0 );
+  EpilogueTabs< BM, BN, T > l_tabs;
+  l_tabs.load( a, l_m0, l_n0 );
 
   int const l_lane = threadIdx.x & 63;
   int const l_wave = threadIdx.x >> 6;
@@ -659,7 +704,7 @@ void contract_kernel( ContractArgs a ) {
   }
 
   // ---------------------------------------------------------------- epilogue
-  epilogue< BM, BN, WM, WN, TM, TN, T >( a, l_acc, l_lds_raw,
+  epilogue< BM, BN, WM, WN, TM, TN, T >( a, l_acc, l_tabs, l_lds_raw,
                                          l_c, l_m0, l_n0, l_wm, l_wn, l_lane );
 }
 
