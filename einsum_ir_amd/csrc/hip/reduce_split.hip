@@ -37,20 +37,10 @@ __global__ __launch_bounds__( 256 ) void split_reduce_kernel( SplitReduceArgs a 
   }
   int64_t const l_off = a.tc_out[l_c] + a.tm_out[l_m] + a.tn_out[l_n];
 
-  // slices summed in ascending order; the loads of 8 slices are issued
-  // before their additions so that they are in flight together
-  float l_v = 0.0f;
-  float const * l_p = a.ws + l_off;
-  int32_t l_s = 0;
-  for( ; l_s + 8 <= a.S; l_s += 8 ) {
-    float l_x[8];
-#pragma unroll
-    for( int l_i = 0; l_i < 8; l_i++ ) l_x[l_i] = l_p[int64_t( l_s + l_i ) * a.span];
-#pragma unroll
-    for( int l_i = 0; l_i < 8; l_i++ ) l_v += l_x[l_i];
-  }
-  for( ; l_s < a.S; l_s++ ) l_v += l_p[int64_t( l_s ) * a.span];
-
+  // the touch kernels' loads (old output, aux) are issued first, then the
+  // slices in chunks of 8 with every load of a chunk in flight together (a
+  // rolled loop would wait for each slice before loading the next); the
+  // slices are added in ascending order, a fixed order
   bool const l_read_out  = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_UNDEFINED );
   bool const l_aux_first = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_COPY );
   bool const l_need_aux  = ( a.aux != nullptr ) && ( l_aux_first || a.last_touch == ETIR_KTYPE_ADD );
@@ -60,11 +50,26 @@ __global__ __launch_bounds__( 256 ) void split_reduce_kernel( SplitReduceArgs a 
     l_aux = a.out_bf16 ? kern::bf16_to_f32( reinterpret_cast< uint16_t const * >( a.aux )[l_aoff] )
                        : reinterpret_cast< float const * >( a.aux )[l_aoff];
   }
+  float l_old = 0.0f;
   if( l_read_out ) {
-    float const l_old = a.out_bf16 ? kern::bf16_to_f32( reinterpret_cast< uint16_t const * >( a.out )[l_off] )
-                                   : reinterpret_cast< float const * >( a.out )[l_off];
-    l_v = l_old + l_v;
+    l_old = a.out_bf16 ? kern::bf16_to_f32( reinterpret_cast< uint16_t const * >( a.out )[l_off] )
+                       : reinterpret_cast< float const * >( a.out )[l_off];
   }
+
+  float l_v = 0.0f;
+  float const * l_p = a.ws + l_off;
+  for( int32_t l_s = 0; l_s < a.S; l_s += 8 ) {
+    float l_x[8];
+#pragma unroll
+    for( int l_i = 0; l_i < 8; l_i++ ) {
+      l_x[l_i] = ( l_s + l_i < a.S ) ? l_p[int64_t( l_s + l_i ) * a.span] : 0.0f;
+    }
+#pragma unroll
+    for( int l_i = 0; l_i < 8; l_i++ ) {
+      if( l_s + l_i < a.S ) l_v += l_x[l_i];
+    }
+  }
+  if( l_read_out ) l_v = l_old + l_v;
   if( l_aux_first ) l_v = l_aux + l_v;
   if( a.last_touch == ETIR_KTYPE_RELU ) l_v = fmaxf( l_v, 0.0f );
   else if( a.last_touch == ETIR_KTYPE_ADD ) l_v = l_v + l_aux;
