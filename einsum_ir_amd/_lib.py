@@ -57,6 +57,7 @@ _HIP_SIGS = {
     "etir_hip_memset": (ctypes.c_int, [_vp, ctypes.c_int32, ctypes.c_int64]),
     "etir_hip_synchronize": (ctypes.c_int, [_vp]),
     "etir_hip_device_count": (ctypes.c_int, []),
+    "etir_hip_pointer_is_device": (ctypes.c_int, [_vp]),
     "etir_hip_stream_create": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p)]),
     "etir_hip_stream_destroy": (ctypes.c_int, [ctypes.c_void_p]),
     "etir_hip_graph_begin": (ctypes.c_int, [ctypes.c_void_p]),

@@ -222,6 +222,20 @@ int etir_hip_device_count( void ) {
   return l_n;
 }
 
+int etir_hip_pointer_is_device( void const * ptr ) {
+  if( ptr == nullptr ) return 0;
+  hipPointerAttribute_t l_a;
+  if( hipPointerGetAttributes( &l_a, ptr ) != hipSuccess ) {
+    // unknown to the runtime: pageable host memory
+    (void) hipGetLastError();
+    return 0;
+  }
+  if( l_a.type == hipMemoryTypeDevice || l_a.type == hipMemoryTypeManaged ) return 1;
+  // pinned host memory the GPU reaches at the same address
+  if( l_a.type == hipMemoryTypeHost && l_a.devicePointer == ptr ) return 1;
+  return 0;
+}
+
 int etir_hip_stream_create( void ** stream ) {
   if( stream == nullptr ) return fail( ETIR_UNDEFINED_ERROR, "stream_create: invalid arguments" );
   *stream = nullptr;

@@ -1,5 +1,7 @@
 #include <stdexcept>
 #include "BinaryContractionHip.h"
+#include "HostStaging.h"
+#include "Tensor.h"
 #include <cstdio>
 
 einsum_ir::backend::BinaryContractionHip::~BinaryContractionHip() {
@@ -33,6 +35,20 @@ einsum_ir::err_t einsum_ir::backend::BinaryContractionHip::compile() {
     else if( m_ktype_first_touch == kernel_t::ADD || m_ktype_first_touch == kernel_t::COPY ) {
       l_s_aux = l_s_out;
     }
+  }
+  catch( std::out_of_range const & ) {
+    return err_t::COMPILATION_FAILED;
+  }
+
+  // tensor sizes in bytes (for staging host tensors in contract())
+  try {
+    int64_t const l_esz_out = ce_n_bytes( m_dtype_out );
+    m_bytes[0] = Tensor::size( ce_n_bytes( m_dtype_left ), m_num_dims_left, m_dim_ids_left, *m_dim_sizes_outer_left );
+    m_bytes[1] = Tensor::size( ce_n_bytes( m_dtype_right ), m_num_dims_right, m_dim_ids_right, *m_dim_sizes_outer_right );
+    m_bytes[3] = Tensor::size( l_esz_out, m_num_dims_out, m_dim_ids_out, *m_dim_sizes_outer_out );
+    m_bytes[2] = ( m_dim_sizes_outer_out_aux != nullptr )
+               ? Tensor::size( l_esz_out, m_num_dims_out, m_dim_ids_out, *m_dim_sizes_outer_out_aux )
+               : ( l_s_aux.empty() ? l_esz_out : m_bytes[3] );
   }
   catch( std::out_of_range const & ) {
     return err_t::COMPILATION_FAILED;
@@ -110,9 +126,26 @@ void einsum_ir::backend::BinaryContractionHip::contract( void const * i_tensor_l
                                                          void const * i_tensor_right,
                                                          void const * i_tensor_out_aux,
                                                          void       * io_tensor_out ) {
-  m_last_error = contract_async( i_tensor_left, i_tensor_right, i_tensor_out_aux, io_tensor_out );
-  if( m_last_error == err_t::SUCCESS && etir_hip_synchronize( m_stream ) != ETIR_SUCCESS ) {
-    m_last_error = err_t::UNDEFINED_ERROR;
+  if( !m_compiled ) {
+    m_last_error = err_t::CALLED_BEFORE_COMPILATION;
+  }
+  else {
+    // host tensors (the reference's callers pass them) go through device copies
+    HostStaging l_st;
+    void const * l_left  = l_st.stage( i_tensor_left,    m_bytes[0], true, false );
+    void const * l_right = l_st.stage( i_tensor_right,   m_bytes[1], true, false );
+    void const * l_aux   = l_st.stage( i_tensor_out_aux, m_bytes[2], true, false );
+    void       * l_out   = l_st.stage( io_tensor_out,    m_bytes[3], true, true );
+    m_last_error = l_st.error();
+    if( m_last_error == err_t::SUCCESS ) {
+      m_last_error = contract_async( l_left, l_right, l_aux, l_out );
+    }
+    if( m_last_error == err_t::SUCCESS && etir_hip_synchronize( m_stream ) != ETIR_SUCCESS ) {
+      m_last_error = err_t::UNDEFINED_ERROR;
+    }
+    if( m_last_error == err_t::SUCCESS && l_st.active() ) {
+      m_last_error = l_st.finish();
+    }
   }
   if( m_last_error != err_t::SUCCESS ) {
     std::fprintf( stderr, "einsum_ir: contraction failed (%d): %s\n", (int) m_last_error,

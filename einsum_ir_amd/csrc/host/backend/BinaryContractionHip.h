@@ -5,9 +5,10 @@
 // Sibling of the reference's BinaryContractionTpp
 // (reference src/backend/BinaryContractionTpp.{h,cpp}); the lowering follows
 // BinaryContractionTpp::compile (reference src/backend/BinaryContractionTpp.cpp:4-127).
-// All tensor pointers are device pointers.  contract() is synchronous like
-// the reference's; contract_async() only enqueues on the plan's stream (used
-// by EinsumNode to run a whole tree on one stream).
+// contract() is synchronous like the reference's and accepts host tensors
+// too (staged through device copies, HostStaging.h); contract_async() only
+// enqueues on the plan's stream and takes device pointers (used by EinsumNode
+// to run a whole tree on one stream).
 #ifndef EINSUM_IR_BACKEND_BINARY_CONTRACTION_HIP
 #define EINSUM_IR_BACKEND_BINARY_CONTRACTION_HIP
 
@@ -25,6 +26,8 @@ class einsum_ir::backend::BinaryContractionHip : public BinaryContraction {
     etir_plan_t m_plan = nullptr;
     void * m_stream = nullptr;
     err_t m_last_error = err_t::SUCCESS;
+    //! bytes of the left, right, auxiliary and output tensors (outer sizes)
+    int64_t m_bytes[4] = { 0, 0, 0, 0 };
 
   public:
     ~BinaryContractionHip();

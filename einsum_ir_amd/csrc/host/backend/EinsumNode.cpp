@@ -12,6 +12,7 @@
 #include "BinaryContractionFactory.h"
 #include "BinaryContractionHip.h"
 #include "BinaryPrimitives.h"
+#include "HostStaging.h"
 #include "Tensor.h"
 #include "UnaryHip.h"
 #include "einsum_ir_hip.h"
@@ -315,11 +316,61 @@ einsum_ir::err_t einsum_ir::backend::EinsumNode::store_and_lock_data() {
     if( etir_hip_malloc( &m_data_ptr_int, m_size ) != ETIR_SUCCESS ) return err_t::UNDEFINED_ERROR;
   }
   UnaryHip * l_unary = static_cast< UnaryHip * >( m_unary );
-  err_t l_err = l_unary->eval_async( m_data_ptr_ext, m_data_ptr_int );
+  HostStaging l_st;   // a host tensor is read through a device copy
+  void const * l_src = l_st.stage( m_data_ptr_ext, m_size, true, false );
+  if( l_st.error() != err_t::SUCCESS ) return l_st.error();
+  err_t l_err = l_unary->eval_async( l_src, m_data_ptr_int );
   if( l_err != err_t::SUCCESS ) return l_err;
   if( etir_hip_synchronize( m_stream ) != ETIR_SUCCESS ) return err_t::UNDEFINED_ERROR;
   m_data_locked = true;
   return err_t::SUCCESS;
+}
+
+void einsum_ir::backend::EinsumNode::stage_ext( HostStaging & io_staging,
+                                                std::vector< std::pair< void **, void * > > & io_saved ) {
+  for( EinsumNode * l_ch : m_children ) l_ch->stage_ext( io_staging, io_saved );
+  // a locked node reads its device copy, not the external tensor
+  if( m_data_ptr_ext != nullptr && !m_data_locked ) {
+    // inputs are read; a computed tensor is written, and copied in as well
+    // (accumulating touches read it, elements outside the node's view keep
+    // their values)
+    bool const l_written = !m_children.empty();
+    void * l_dev = io_staging.stage( m_data_ptr_ext, m_size, true, l_written );
+    if( l_dev != m_data_ptr_ext ) {
+      io_saved.emplace_back( &m_data_ptr_ext, m_data_ptr_ext );
+      m_data_ptr_ext = l_dev;
+    }
+  }
+  if( m_data_ptr_aux_ext != nullptr ) {
+    int64_t l_bytes = m_size;
+    if( m_dim_sizes_aux_outer != nullptr ) {
+      try {
+        l_bytes = Tensor::size( ce_n_bytes( m_dtype ), m_num_dims, m_dim_ids_ext, *m_dim_sizes_aux_outer );
+      }
+      catch( std::out_of_range const & ) {
+        l_bytes = m_size;
+      }
+    }
+    void * l_dev = io_staging.stage( m_data_ptr_aux_ext, l_bytes, true, false );
+    if( l_dev != m_data_ptr_aux_ext ) {
+      io_saved.emplace_back( &m_data_ptr_aux_ext, m_data_ptr_aux_ext );
+      m_data_ptr_aux_ext = l_dev;
+    }
+  }
+}
+
+void einsum_ir::backend::EinsumNode::restore_ext( std::vector< std::pair< void **, void * > > const & i_saved ) {
+  for( auto const & l_s : i_saved ) *l_s.first = l_s.second;
+}
+
+bool einsum_ir::backend::EinsumNode::has_host_ext() const {
+  for( EinsumNode const * l_ch : m_children ) {
+    if( l_ch->has_host_ext() ) return true;
+  }
+  if( m_data_ptr_ext != nullptr && !m_data_locked && etir_hip_pointer_is_device( m_data_ptr_ext ) != 1 ) {
+    return true;
+  }
+  return m_data_ptr_aux_ext != nullptr && etir_hip_pointer_is_device( m_data_ptr_aux_ext ) != 1;
 }
 
 einsum_ir::err_t einsum_ir::backend::EinsumNode::unlock_data() {
@@ -374,11 +425,25 @@ einsum_ir::err_t einsum_ir::backend::EinsumNode::eval_async() {
   return err_t::SUCCESS;
 }
 
-void einsum_ir::backend::EinsumNode::eval() {
-  err_t l_err = eval_async();
+einsum_ir::err_t einsum_ir::backend::EinsumNode::eval_sync() {
+  if( !m_compiled ) return err_t::CALLED_BEFORE_COMPILATION;
+  // host tensors (the reference's callers pass them) take part through device
+  // copies made for this evaluation
+  HostStaging l_st;
+  std::vector< std::pair< void **, void * > > l_saved;
+  stage_ext( l_st, l_saved );
+  err_t l_err = l_st.error();
+  if( l_err == err_t::SUCCESS ) l_err = eval_async();
   if( l_err == err_t::SUCCESS && etir_hip_synchronize( m_stream ) != ETIR_SUCCESS ) {
     l_err = err_t::UNDEFINED_ERROR;
   }
+  if( l_err == err_t::SUCCESS && l_st.active() ) l_err = l_st.finish();
+  restore_ext( l_saved );
+  return l_err;
+}
+
+void einsum_ir::backend::EinsumNode::eval() {
+  err_t const l_err = eval_sync();
   if( l_err != err_t::SUCCESS ) {
     std::fprintf( stderr, "einsum_ir: tree evaluation failed (%d): %s\n", (int) l_err, etir_hip_last_error() );
   }

@@ -21,6 +21,7 @@ namespace einsum_ir {
   namespace backend {
     class EinsumNode;
     class BinaryContractionHip;
+    class HostStaging;
     class UnaryHip;
   }
 }
@@ -145,6 +146,27 @@ class einsum_ir::backend::EinsumNode {
 
     /** Evaluates the tree and waits for the result. **/
     void eval();
+
+    /**
+     * eval() with its error: stages host tensors through device copies,
+     * enqueues the tree, waits for it and copies computed host tensors back.
+     **/
+    err_t eval_sync();
+
+    /**
+     * Replaces the external pointers of this subtree that point to host
+     * memory by device copies from io_staging (inputs copied in, computed
+     * tensors copied back by io_staging.finish()); the replaced pointers are
+     * appended to io_saved for restore_ext().
+     **/
+    void stage_ext( HostStaging & io_staging,
+                    std::vector< std::pair< void **, void * > > & io_saved );
+
+    //! restores the external pointers saved by stage_ext
+    static void restore_ext( std::vector< std::pair< void **, void * > > const & i_saved );
+
+    //! true if an external pointer of this subtree is host memory the GPU cannot reach
+    bool has_host_ext() const;
 
     /** Enqueues the evaluation of the tree on the stream without waiting. **/
     err_t eval_async();

@@ -1,7 +1,8 @@
 // Unary operator on the MI355X: one device permutation plan per operator
 // (etir_hip_permute_create), sibling of the reference's UnaryTpp
-// (reference src/backend/UnaryTpp.cpp:4-54).  eval() is synchronous;
-// eval_async() only enqueues on the stream.  Pointers are device pointers.
+// (reference src/backend/UnaryTpp.cpp:4-54).  eval() is synchronous and
+// accepts host tensors too (staged through device copies, HostStaging.h);
+// eval_async() only enqueues on the stream and takes device pointers.
 #ifndef EINSUM_IR_BACKEND_UNARY_HIP
 #define EINSUM_IR_BACKEND_UNARY_HIP
 
@@ -20,6 +21,9 @@ class einsum_ir::backend::UnaryHip : public Unary {
     void * m_stream = nullptr;
     bool m_compiled = false;
     err_t m_last_error = err_t::SUCCESS;
+    //! bytes spanned by the input and the output (for staging host tensors)
+    int64_t m_bytes_in = 0;
+    int64_t m_bytes_out = 0;
 
   public:
     ~UnaryHip();

@@ -265,9 +265,7 @@ int etir_expression_create_ctype( char const        * expr,
 
 int etir_expression_eval( etir_expression_t handle ) {
   if( handle == nullptr || !handle->expr.m_compiled ) return err_t::CALLED_BEFORE_COMPILATION;
-  err_t l_err = handle->expr.m_nodes.back().eval_async();
-  if( l_err != err_t::SUCCESS ) return l_err;
-  return etir_hip_synchronize( handle->expr.m_stream ) == ETIR_SUCCESS ? err_t::SUCCESS : err_t::UNDEFINED_ERROR;
+  return handle->expr.m_nodes.back().eval_sync();
 }
 
 int etir_expression_eval_async( etir_expression_t handle ) {
@@ -342,10 +340,8 @@ int etir_tree_create( char const * tree, char const * dim_sizes, int32_t dtype,
 }
 
 int etir_tree_eval( etir_tree_t handle ) {
-  if( handle == nullptr ) return err_t::CALLED_BEFORE_COMPILATION;
-  err_t l_err = handle->tree.m_nodes.back().eval_async();
-  if( l_err != err_t::SUCCESS ) return l_err;
-  return etir_hip_synchronize( handle->tree.m_stream ) == ETIR_SUCCESS ? err_t::SUCCESS : err_t::UNDEFINED_ERROR;
+  if( handle == nullptr || handle->tree.m_nodes.empty() ) return err_t::CALLED_BEFORE_COMPILATION;
+  return handle->tree.m_nodes.back().eval_sync();
 }
 
 int64_t etir_tree_num_ops( etir_tree_t handle ) {
@@ -458,9 +454,8 @@ int etir_nodes_eval_async( etir_nodes_t handle ) {
 }
 
 int etir_nodes_eval( etir_nodes_t handle ) {
-  err_t l_err = (err_t) etir_nodes_eval_async( handle );
-  if( l_err != err_t::SUCCESS ) return l_err;
-  return etir_hip_synchronize( handle->stream ) == ETIR_SUCCESS ? err_t::SUCCESS : err_t::UNDEFINED_ERROR;
+  if( handle == nullptr || handle->root < 0 ) return err_t::CALLED_BEFORE_COMPILATION;
+  return handle->nodes[ handle->root ].eval_sync();
 }
 
 int64_t etir_nodes_num_ops( etir_nodes_t handle ) {

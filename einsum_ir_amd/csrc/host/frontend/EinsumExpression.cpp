@@ -223,6 +223,9 @@ einsum_ir::err_t einsum_ir::frontend::EinsumExpression::eval_graph_async() {
   if( !m_compiled ) return err_t::CALLED_BEFORE_COMPILATION;
   if( m_stream == nullptr ) return err_t::UNDEFINED_ERROR;
   if( m_graph == nullptr ) {
+    // a recording keeps the pointers it saw: host tensors (which eval() stages
+    // through temporary device copies) cannot take part
+    if( m_nodes.back().has_host_ext() ) return err_t::NO_DATA_PTR_PROVIDED;
     if( etir_hip_graph_begin( m_stream ) != ETIR_SUCCESS ) return err_t::UNDEFINED_ERROR;
     err_t l_err = m_nodes.back().eval_async();
     if( l_err != err_t::SUCCESS ) {

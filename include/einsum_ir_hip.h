@@ -201,6 +201,13 @@ int etir_hip_synchronize( void * stream );
 /* Number of visible HIP devices (0 on a machine without a GPU). */
 int etir_hip_device_count( void );
 
+/* 1 if the GPU can access ptr directly (device, managed, or mapped pinned
+ * host memory), 0 if it cannot (pageable host memory, NULL).  No counterpart
+ * in the reference, whose tensors are host memory: the synchronous operator
+ * calls (BinaryContractionHip::contract, UnaryHip::eval, EinsumNode::eval,
+ * store_and_lock_data) use it to stage host tensors through device copies. */
+int etir_hip_pointer_is_device( void const * ptr );
+
 /* Streams and graphs for repeated tree evaluation.  These have no
  * counterpart in the reference (its EinsumNode::eval, reference
  * src/backend/EinsumNode.cpp:496-540, calls the backends directly each
