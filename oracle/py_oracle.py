@@ -133,12 +133,16 @@ def _names_sorted(names):
     return sorted(names, key=key)
 
 
-def contract_path(expr, sizes, path, arrays, dtype=FP64):
+def contract_path(expr, sizes, path, arrays, dtype=FP64, round_bf16=False):
     """Einsum expression evaluated pairwise along a contraction path
     (opt_einsum standard form) with oracle_contract for every step; each
     intermediate keeps the dims still needed later in ascending name order,
     as EinsumExpression::substring_out does (reference
     src/frontend/EinsumExpression.cpp:25-70).  Returns the output as float64.
+    round_bf16: every step's result is rounded to bfloat16 (RNE), as a tree
+    whose tensors are bf16 stores its intermediates and output.
+    Pinned by tests/test_oracle.py: numpy.einsum in float64, and for
+    round_bf16 numpy.einsum steps with torch's bfloat16 conversion between.
 
     arrays: flat numpy arrays of the inputs in their expression layouts."""
     lhs, out = expr.replace(" ", "").split("->")
@@ -168,5 +172,7 @@ def contract_path(expr, sizes, path, arrays, dtype=FP64):
                      strides_out=[so.get(d, 0) for d in alld])
         o = np.zeros(int(np.prod([sizes[d] for d in res])) if res else 1, dtype=np.float64)
         contract(loops, al, ar, o, dtype_left=FP64, dtype_right=FP64, dtype_out=FP64)
+        if round_bf16:
+            o = bf16_to_f32(f32_to_bf16(o.astype(np.float32))).astype(np.float64)
         live = [t for k, t in enumerate(live) if k not in (i, j)] + [(res, o)]
     return live[0][1]

@@ -240,3 +240,26 @@ def test_unsupported_backend_is_reported(torch_cuda, monkeypatch):
     with pytest.raises(eir.EinsumIrError) as err:
         host.Expression("ab,bc->ac", dict(a=2, b=2, c=2), [(0, 1)], dev)
     assert err.value.code == eir.INVALID_BACKEND
+
+
+@pytest.mark.parametrize("idx", [1, 3, 4])
+def test_expression_bf16(torch_cuda, oracle, idx):
+    """A bf16 tree: bf16 inputs, intermediates and output (RNE), fp32
+    accumulation in every node.  Checker: the path oracle with every step's
+    result rounded to bf16 on the same bf16-rounded inputs; bar 2e-3 relative
+    Frobenius (fp32 against fp64 accumulation can move a rounding by one bf16
+    step)."""
+    torch = torch_cuda
+    expr, sizes, path = EXPRESSIONS[idx]
+    rng = np.random.default_rng(40 + idx)
+    ins = expr.split("->")[0].split(",")
+    out = expr.split("->")[1]
+    arrays = [oracle.f32_to_bf16(rng.uniform(-1, 1, tensor_numel(t, sizes)).astype(np.float32)) for t in ins]
+    dev = [_dev(torch, a) for a in arrays]
+    dout = torch.zeros(tensor_numel(out, sizes), dtype=torch.int16, device="cuda")
+    e = host.Expression(expr, sizes, path, dev + [dout], dtype=eir.BF16)
+    e.eval()
+    got = oracle.bf16_to_f32(dout.cpu().numpy().view(np.uint16))
+    ref = oracle.contract_path(expr, sizes, path, [oracle.bf16_to_f32(a) for a in arrays], round_bf16=True)
+    assert rel_frobenius(ref, got) <= TOL_BF16
+    e.close()

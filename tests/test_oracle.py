@@ -228,3 +228,27 @@ def test_contract_path_matches_numpy(oracle):
     got = oracle.contract_path(expr, sizes, [(1, 2), (0, 1)], arrs)
     ref = np.einsum(expr, *[a.reshape([sizes[d] for d in t]) for a, t in zip(arrs, ins)])
     np.testing.assert_allclose(got, ref.ravel(), rtol=1e-12, atol=1e-12)
+
+
+def test_contract_path_bf16_rounding(oracle):
+    # round_bf16 rounds every step's result: equal to numpy.einsum steps with
+    # torch's own bfloat16 conversion (round to nearest even) in between
+    torch = pytest.importorskip("torch")
+    expr = "da,dce,bec->abc"
+    sizes = dict(a=3, b=4, c=5, d=2, e=3)
+    rng = np.random.default_rng(12)
+    ins = expr.split("->")[0].split(",")
+    arrs = [rng.uniform(-1, 1, tensor_numel(t, sizes)) for t in ins]
+    got = oracle.contract_path(expr, sizes, [(1, 2), (0, 1)], arrs, round_bf16=True)
+
+    def rnd(x):
+        return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).bfloat16().float().double().numpy()
+
+    sh = lambda a, t: a.reshape([sizes[d] for d in t])
+    # step 1: dce,bec -> intermediate dims {b, c, d} in ascending name order
+    t1 = rnd(np.einsum("dce,bec->bcd", sh(arrs[1], "dce"), sh(arrs[2], "bec")))
+    ref = rnd(np.einsum("da,bcd->abc", sh(arrs[0], "da"), t1))
+    assert np.array_equal(got, ref.ravel())
+    # without rounding the same path differs from the rounded one
+    plain = oracle.contract_path(expr, sizes, [(1, 2), (0, 1)], arrs)
+    assert not np.array_equal(plain, got)
