@@ -24,7 +24,8 @@ the committed rocprofv3 --pmc summary under profiles/ when present.
 bounded sample of the same workload on the host cores; torch.einsum on the
 host (the comparator the reference's harnesses print) is timed on the same
 sample under extra["cpu_torch_einsum_c3_slice"], next to a probe of the host
-(CPU model, cores, whether libxsmm / OpenBLAS are installed).
+(CPU model, cores, whether libxsmm / OpenBLAS are installed) and CPU rows for
+configs 1, 2, 4 and 5 (extra["cpu_rows"]).
 """
 import argparse
 import json
@@ -318,6 +319,80 @@ def cpu_torch_einsum_c3(threads):
                        f"torch {torch.__version__} CPU ({'MKL' if torch.backends.mkl.is_available() else 'no MKL'})")
 
 
+def _cpu_rate(fn, work, budget=3.0, max_reps=20):
+    """Average rate of fn() on the host: work / seconds, after one warm-up."""
+    fn()
+    reps, t = 0, 0.0
+    while t < budget and reps < max_reps:
+        t0 = time.perf_counter()
+        fn()
+        t += time.perf_counter() - t0
+        reps += 1
+    return work * reps / t, reps
+
+
+def cpu_rows(threads):
+    """CPU rows beside the GPU rows of configs 1, 2, 4 and 5 (baseline only):
+    the reference algorithm restated (oracle: blocked contraction on all
+    cores, blocked permute on one thread as the reference runs it) where it
+    exists, and torch on the host, which the reference's
+    harnesses print next to einsum_ir (src/bench_binary.cpp:62-87,
+    src/bench_unary.cpp:311-323, src/bench_expression.cpp:381-422).  Full
+    config sizes, about 3 s of work per row."""
+    import numpy as np
+    import torch
+    import einsum_ir_amd as eir
+    from oracle import py_oracle as orc
+    torch.set_num_threads(threads)
+    rows = {}
+    g = torch.Generator().manual_seed(1)
+    # config 1
+    sizes = dict(a=32, b=16, c=32, d=16, k=32, l=16)
+    loops = eir.binary_loops("abkl,cdkl->abcd", sizes)
+    a = (torch.rand(512 * 512, generator=g) * 2 - 1).numpy()
+    b = (torch.rand(512 * 512, generator=g) * 2 - 1).numpy()
+    o = np.empty(512 * 512, np.float32)
+    fl = 2 * 512 ** 3
+    r1, n1 = _cpu_rate(lambda: orc.contract_blocked(loops, a, b, o, num_threads=threads), fl)
+    ta, tb = torch.from_numpy(a).view(32, 16, 32, 16), torch.from_numpy(b).view(32, 16, 32, 16)
+    r2, n2 = _cpu_rate(lambda: torch.einsum("abkl,cdkl->abcd", ta, tb), fl)
+    rows["c1"] = dict(unit="GFLOP/s", port=round(r1 * 1e-9, 1), torch=round(r2 * 1e-9, 1), reps=[n1, n2])
+    # config 2
+    u = eir.unary_dims("abcd->dbca", dict(a=64, b=64, c=64, d=64))
+    x = (torch.rand(64 ** 4, generator=g) * 2 - 1).numpy()
+    y = np.empty_like(x)
+    by = 2 * 4 * 64 ** 4
+    r1, n1 = _cpu_rate(lambda: orc.permute_blocked(u["sizes"], u["strides_in"], u["strides_out"], x, y), by)
+    tx = torch.from_numpy(x).view(64, 64, 64, 64)
+    r2, n2 = _cpu_rate(lambda: tx.permute(3, 1, 2, 0).contiguous(), by)
+    # the reference runs its unary loop nest on one thread
+    rows["c2"] = dict(unit="GB/s", port=round(r1 * 1e-9, 1), port_cores=1, torch=round(r2 * 1e-9, 1),
+                      reps=[n1, n2])
+    # config 4: the MLP tree along its path
+    w = 2048
+    xs = torch.randn(4096, w, generator=g)
+    ws = [torch.randn(w, w, generator=g) / w ** 0.5 for _ in range(4)]
+
+    def mlp():
+        h = xs
+        for m in ws:
+            h = torch.einsum("bi,ih->bh", h, m)
+        return h
+    r2, n2 = _cpu_rate(mlp, 4 * 2 * 4096 * w * w, max_reps=5)
+    rows["c4"] = dict(unit="GFLOP/s", torch=round(r2 * 1e-9, 1), reps=[n2])
+    # config 5: the committed network along its path
+    from einsum_ir_amd import harness
+    fx = json.load(open(os.path.join(ROOT, "tests", "golden", "c5_network.json")))
+    ins, out = harness._tensors(fx["expr"])
+    ts = [torch.rand([fx["sizes"][d] for d in t], generator=g) * 2 - 1 for t in ins]
+    r2, n2 = _cpu_rate(lambda: harness.torch_path_eval(torch, ins, out, fx["sizes"],
+                                                       [tuple(p) for p in fx["path"]], ts),
+                       fx["flops"], max_reps=5)
+    rows["c5"] = dict(unit="GFLOP/s", torch=round(r2 * 1e-9, 1), reps=[n2])
+    rows["cores"] = threads
+    return rows
+
+
 def cpu_host_probe():
     """CPU model, core count and whether the reference's CPU libraries
     (libxsmm, OpenBLAS) are installed on this host."""
@@ -420,6 +495,8 @@ def main():
         log(f"cpu baseline: {cpu}")
         extra["cpu_torch_einsum_c3_slice"] = cpu_torch_einsum_c3(cpu["cores"])
         extra["cpu_host"] = cpu_host_probe()
+        extra["cpu_rows"] = cpu_rows(cpu["cores"])
+        log(f"cpu rows: {extra['cpu_rows']}")
         log(f"cpu torch.einsum: {extra['cpu_torch_einsum_c3_slice']}; host: {extra['cpu_host']}")
 
     if c3 is None:

@@ -41,6 +41,11 @@
  *                          Pinned by tests/test_oracle.py: numpy.transpose bit-exact, zero fill,
  *                          addition.
  *
+ *  oracle_permute_blocked  The permutation CPU baseline: the reference's sequential unary loop nest
+ *                          around a 2-D transpose primitive (UnaryBackend.cpp:106-226,
+ *                          UnaryBackendTpp.cpp:45-93) with a 64 x 64 blocked transpose.  Pinned by
+ *                          tests/test_oracle.py against oracle_permute (bit-exact).
+ *
  *  oracle_f32_to_bf16 /    bf16 round-to-nearest-even / widening, from the IEEE-754 binary32 and
  *  oracle_bf16_to_f32      bfloat16 definitions (the reference has no bf16).  Pinned by
  *                          tests/test_oracle.py against hand-computed tie cases and torch.bfloat16.
@@ -383,6 +388,62 @@ int oracle_permute( int64_t         num_dims,
       }
       if( d < 1 ) break;
     }
+  }
+  return 0;
+}
+
+/* The CPU baseline of a permutation: the reference's unary loop nest restated
+ * (UnaryBackend::eval / eval_iter, src/basic/unary/UnaryBackend.cpp:106-226:
+ * sequential loops, no OpenMP, around a 2-D transpose primitive of the
+ * input's and the output's unit-stride dims, UnaryBackendTpp.cpp:45-93) with a
+ * 64 x 64 blocked transpose as the primitive.  fp32 COPY; single thread, as
+ * the reference runs it.  Pinned by tests/test_oracle.py against
+ * oracle_permute (bit-exact).  Returns 2 for layouts it does not cover (no
+ * distinct unit-stride dims in input and output). */
+int oracle_permute_blocked( int64_t         num_dims,
+                            int64_t const * sizes,
+                            int64_t const * s_in,
+                            int64_t const * s_out,
+                            float const   * in,
+                            float         * out ) {
+  int64_t di = -1, dout = -1;
+  if( num_dims > OR_MAX_LOOPS ) return 1;
+  for( int64_t d = 0; d < num_dims; d++ ) {
+    if( sizes[d] == 0 ) return 0;
+    if( s_in[d] == 1 && di < 0 ) di = d;
+    if( s_out[d] == 1 && dout < 0 ) dout = d;
+  }
+  if( di < 0 || dout < 0 || di == dout ) return 2;
+  int64_t const ni = sizes[di], no = sizes[dout];
+  int64_t const si_o = s_in[dout], so_i = s_out[di];
+  /* batch dims: every other dim, outer -> inner */
+  int64_t bsz[OR_MAX_LOOPS], bsi[OR_MAX_LOOPS], bso[OR_MAX_LOOPS], idx[OR_MAX_LOOPS];
+  int nb = 0;
+  for( int64_t d = 0; d < num_dims; d++ ) {
+    if( d == di || d == dout ) continue;
+    bsz[nb] = sizes[d]; bsi[nb] = s_in[d]; bso[nb] = s_out[d]; idx[nb] = 0; nb++;
+  }
+  for( ;; ) {
+    int64_t bi = 0, bo = 0;
+    for( int b = 0; b < nb; b++ ) { bi += idx[b] * bsi[b]; bo += idx[b] * bso[b]; }
+    for( int64_t o0 = 0; o0 < no; o0 += 64 ) {
+      int64_t const o1 = o0 + 64 < no ? o0 + 64 : no;
+      for( int64_t i0 = 0; i0 < ni; i0 += 64 ) {
+        int64_t const i1 = i0 + 64 < ni ? i0 + 64 : ni;
+        for( int64_t x = i0; x < i1; x++ ) {
+          float const * src = in + bi + x;
+          float * dst = out + bo + x * so_i;
+          for( int64_t y = o0; y < o1; y++ ) dst[y] = src[y * si_o];
+        }
+      }
+    }
+    int b = nb - 1;
+    while( b >= 0 ) {
+      if( ++idx[b] < bsz[b] ) break;
+      idx[b] = 0;
+      b--;
+    }
+    if( b < 0 ) break;
   }
   return 0;
 }

@@ -41,6 +41,8 @@ def lib():
         l.oracle_contract_blocked.argtypes = [ctypes.c_int64, _i32p, _i64p, _i64p, _i64p, _i64p, _i64p,
                                               ctypes.c_int32, ctypes.c_int32, _vp, _vp, _vp, _vp,
                                               ctypes.c_int32]
+        l.oracle_permute_blocked.restype = ctypes.c_int
+        l.oracle_permute_blocked.argtypes = [ctypes.c_int64, _i64p, _i64p, _i64p, _vp, _vp]
         l.oracle_permute.restype = ctypes.c_int
         l.oracle_permute.argtypes = [ctypes.c_int64, _i64p, _i64p, _i64p, ctypes.c_int32,
                                      ctypes.c_int32, _vp, _vp, ctypes.c_int32]
@@ -108,6 +110,15 @@ def permute(sizes, strides_in, strides_out, inp, out, dtype=FP32, ktype=COPY, nu
                               dtype, ktype, _np_ptr(inp), _np_ptr(out), num_threads)
     assert rc == 0
     return out
+
+
+def permute_blocked(sizes, strides_in, strides_out, inp, out):
+    """fp32 COPY permutation by the blocked CPU baseline (dims in output
+    order); returns False for layouts it does not cover."""
+    rc = lib().oracle_permute_blocked(len(sizes), _a64(sizes), _a64(strides_in), _a64(strides_out),
+                                      _np_ptr(inp), _np_ptr(out))
+    assert rc in (0, 2)
+    return rc == 0
 
 
 def f32_to_bf16(x):

@@ -252,3 +252,28 @@ def test_contract_path_bf16_rounding(oracle):
     # without rounding the same path differs from the rounded one
     plain = oracle.contract_path(expr, sizes, [(1, 2), (0, 1)], arrs)
     assert not np.array_equal(plain, got)
+
+
+@pytest.mark.parametrize("expr,sizes", [
+    ("abcd->dbca", dict(a=7, b=5, c=9, d=70)),
+    ("abc->cba", dict(a=65, b=3, c=130)),
+    ("ab->ba", dict(a=129, b=64)),
+    ("abcd->acdb", dict(a=3, b=66, c=4, d=5)),
+])
+def test_permute_blocked_matches_permute(oracle, expr, sizes):
+    # the blocked CPU baseline equals the reference-semantics permutation bit for bit
+    from einsum_ir_amd import unary_dims
+    u = unary_dims(expr, sizes)
+    n = int(np.prod(list(sizes.values())))
+    x = np.random.default_rng(5).uniform(-1, 1, n).astype(np.float32)
+    y1, y2 = np.zeros_like(x), np.full_like(x, np.nan)
+    oracle.permute(u["sizes"], u["strides_in"], u["strides_out"], x, y1)
+    assert oracle.permute_blocked(u["sizes"], u["strides_in"], u["strides_out"], x, y2)
+    assert np.array_equal(y1, y2)
+
+
+def test_permute_blocked_declines_same_unit_dim(oracle):
+    from einsum_ir_amd import unary_dims
+    u = unary_dims("abc->bac", dict(a=4, b=5, c=6))
+    x = np.zeros(120, np.float32)
+    assert not oracle.permute_blocked(u["sizes"], u["strides_in"], u["strides_out"], x, x.copy())
