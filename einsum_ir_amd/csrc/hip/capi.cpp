@@ -125,6 +125,7 @@ int etir_hip_permute_execute( etir_plan_t  plan,
 int etir_hip_plan_destroy( etir_plan_t plan ) {
   if( plan == nullptr ) return ETIR_SUCCESS;
   if( plan->kind == 1 ) etir::release_contraction( plan->cont );
+  if( plan->kind == 2 ) etir::release_permute( plan->perm );
   delete plan;
   return ETIR_SUCCESS;
 }
@@ -138,12 +139,19 @@ int etir_hip_plan_describe( etir_plan_t plan, char * buf, int64_t len ) {
     l_s = plan->cont.desc;
   }
   else {
-    static char const * l_modes[] = { "fill", "transpose", "copy_vec", "gather" };
+    static char const * l_modes[] = { "fill", "transpose", "copy_vec", "gather", "tiled" };
     etir::PermutePlan const & p = plan->perm;
     char l_tmp[256];
     std::snprintf( l_tmp, sizeof( l_tmp ), "permute %s dims=%d elems=%lld vec=%d",
                    l_modes[ (int) p.mode ], p.num_dims, (long long) p.num_elements, p.args.vec_ok );
     l_s = l_tmp;
+    if( p.mode == etir::PermMode::TILED ) {
+      l_s += " tile=[";
+      for( int l_k = 0; l_k < p.args.tile_nd; l_k++ ) {
+        l_s += ( l_k ? "," : "" ) + std::to_string( p.args.tile_ext[l_k] );
+      }
+      l_s += "] pad=" + std::to_string( p.args.tile_pad );
+    }
   }
   std::strncpy( buf, l_s.c_str(), (std::size_t) len - 1 );
   buf[len - 1] = '\0';

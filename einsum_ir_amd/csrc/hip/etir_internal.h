@@ -45,8 +45,11 @@ enum class PermMode : int32_t {
   FILL      = 0,  // ZERO: out = 0 over the output's strides
   TRANSPOSE = 1,  // LDS-tiled 2-D transpose of (in-unit dim, out-unit dim) + batch
   COPY_VEC  = 2,  // both innermost dims unit-stride: vectorised strided copy
-  GATHER    = 3   // anything else: one thread per output element
+  GATHER    = 3,  // anything else: one thread per output element
+  TILED     = 4   // small unit-stride dims: tiles over both tensors' innermost runs
 };
+
+constexpr int kPermTileDims = 4;   // dims of a TILED tile (2 per run at most)
 
 struct PermArgs {
   void const * in;
@@ -65,6 +68,22 @@ struct PermArgs {
   int64_t  num_elements;
   int32_t  add;       // ktype ADD: out += in
   int32_t  vec_ok;    // 16-byte vector accesses are legal (sizes/strides/alignment)
+  // TILED: tile dims (size, extent, strides, tiles along it), tile element
+  // count, LDS padding (elements after every 64) and the offset tables:
+  // tab_r per entry (V consecutive elements in input order) {input offset,
+  // packed coordinates}, tab_w per entry (V consecutive elements in output
+  // order) {output offset, packed coordinates, LDS index of each element,
+  // padded to 4 or 8 ints}; coordinates are 8 bits per tile dim
+  int32_t  tile_nd;
+  int32_t  tile_n;
+  int32_t  tile_pad;
+  int64_t  tile_size[kPermTileDims];
+  int64_t  tile_ext[kPermTileDims];
+  int64_t  tile_s_in[kPermTileDims];
+  int64_t  tile_s_out[kPermTileDims];
+  int64_t  tile_nblk[kPermTileDims];
+  int32_t const * tab_r;
+  int32_t const * tab_w;
 };
 
 struct PermutePlan {
@@ -78,7 +97,12 @@ struct PermutePlan {
   int64_t  s_in[kPermMaxDims];
   int64_t  s_out[kPermMaxDims];
   PermArgs args{};                       // pointers filled at execute time
+  void *   d_tables = nullptr;           // TILED: device offset tables (owned)
+  int32_t  tile_vw = 1;                  // TILED: elements per table entry (1 or 4)
 };
+
+// frees the device memory of a permutation plan
+void release_permute( PermutePlan & plan );
 
 int  plan_permute( int64_t         num_dims,
                    int64_t const * sizes,

@@ -97,3 +97,28 @@ def test_permute_rejects_bad_ktype(torch_cuda):
     with pytest.raises(eir.EinsumIrError) as e:
         eir.PermutePlan([4, 4], [4, 1], [1, 4], ktype=eir.RELU)
     assert e.value.code == eir.INVALID_KTYPE
+
+
+# both unit-stride dims shorter than a 64-wide tile: tiles over the innermost
+# runs of both tensors (shared middle dims, 2-dim runs, ragged edges, 5-D)
+TILED_CASES = [
+    ("abcd->dbca", dict(a=8, b=64, c=96, d=8)),       # runs (d,c) and (a,c): shared c
+    ("abcd->dbca", dict(a=16, b=40, c=48, d=16)),
+    ("abcd->dbca", dict(a=5, b=9, c=70, d=13)),       # ragged everywhere
+    ("abcd->acdb", dict(a=7, b=13, c=11, d=5)),
+    ("abcde->bdaec", dict(a=12, b=9, c=9, d=12, e=16)),
+    ("abcde->bdaec", dict(a=3, b=5, c=6, d=7, e=4)),    # many short dims
+    ("abc->cba", dict(a=40, b=2, c=20)),               # runs of two dims each
+]
+
+
+@pytest.mark.parametrize("expr,sizes", TILED_CASES)
+@pytest.mark.parametrize("dtype", [eir.FP32, eir.FP64, eir.BF16])
+def test_permute_tiled(torch_cuda, oracle, expr, sizes, dtype):
+    desc = _check(torch_cuda, oracle, expr, sizes, dtype=dtype, seed=len(expr))
+    assert "tiled" in desc
+
+
+@pytest.mark.parametrize("expr,sizes", [TILED_CASES[0], TILED_CASES[2]])
+def test_permute_tiled_add(torch_cuda, oracle, expr, sizes):
+    _check(torch_cuda, oracle, expr, sizes, dtype=eir.FP32, ktype=eir.ADD)
