@@ -137,6 +137,33 @@ def bench_c2(torch, eir, stream, steps, warmup):
     return res
 
 
+PERMUTES_4D = [
+    ("abcd->dbca", (64, 64, 64, 64)), ("abcd->dbca", (16, 256, 256, 16)), ("abcd->dbca", (8, 512, 512, 8)),
+    ("abcd->dcba", (32, 32, 128, 128)), ("abcd->acdb", (128, 16, 64, 128)), ("abcd->bdac", (36, 48, 36, 512)),
+    ("abcd->cabd", (48, 36, 512, 36)),
+]
+
+
+def bench_permutes_4d(torch, eir, stream):
+    """Config 2's permutation kind over other 4-D shapes (fp32 COPY, 16.8-31.9 M
+    elements, unit-stride dims from 8 to 512 wide): GB/s per shape."""
+    rows = []
+    for expr, shape in PERMUTES_4D:
+        sizes = dict(zip("abcd", shape))
+        u = eir.unary_dims(expr, sizes)
+        n = shape[0] * shape[1] * shape[2] * shape[3]
+        x = torch.rand(n, device="cuda")
+        y = torch.empty_like(x)
+        plan = eir.PermutePlan(u["sizes"], u["strides_in"], u["strides_out"], dtype=eir.FP32, ktype=eir.COPY)
+        _, per = time_launches(torch, stream, lambda: plan.execute(x, y, stream=stream), 20, 3)
+        gbs = 8 * n / per * 1e-9
+        rows.append(dict(expr=expr, sizes=list(shape), gbs=round(gbs, 1), frac_hbm_peak=round(gbs / PEAK_HBM_GBS, 4),
+                         kernel=plan.describe().split(" dims")[0]))
+        plan.close()
+        del x, y
+    return rows
+
+
 def bench_c1(torch, eir, stream, steps, warmup):
     sizes = dict(a=32, b=16, c=32, d=16, k=32, l=16)
     loops = eir.binary_loops("abkl,cdkl->abcd", sizes)
@@ -442,6 +469,10 @@ def main():
             value=round(gbs, 1), unit="GB/s", us_per_launch=round(c2["per_launch"] * 1e6, 2),
             frac_hbm_peak=round(gbs / PEAK_HBM_GBS, 4), bytes_per_launch=c2["bytes"], kernel=c2["desc"])
         log(f"c2: {c2['desc']}  {c2['per_launch']*1e6:.2f} us/launch  {gbs:.0f} GB/s")
+        p4 = bench_permutes_4d(torch, eir, stream)
+        extra["permutes_4d_fp32"] = dict(unit="GB/s", min_frac_hbm_peak=min(r["frac_hbm_peak"] for r in p4),
+                                         cases=p4)
+        log("permutes 4-D: " + ", ".join(f"{r['expr']}{r['sizes']} {r['gbs']:.0f}" for r in p4))
     if run("c1"):
         c1 = bench_c1(torch, eir, stream, max(args.steps, 20), args.warmup)
         gf = c1["flops"] / c1["per_launch"] * 1e-9
