@@ -72,11 +72,12 @@ struct PermArgs {
   // count, LDS padding (elements after every 64) and the offset tables:
   // tab_r per entry (V consecutive elements in input order) {input offset,
   // packed coordinates}, tab_w per entry (V consecutive elements in output
-  // order) {output offset, packed coordinates, LDS index of each element,
-  // padded to 4 or 8 ints}; coordinates are 8 bits per tile dim
+  // order) {output offset, packed coordinates, input-order index of the first
+  // element, 0}, the others tile_t_step apart; coordinates 8 bits per tile dim
   int32_t  tile_nd;
   int32_t  tile_n;
   int32_t  tile_pad;
+  int32_t  tile_t_step;
   int64_t  tile_size[kPermTileDims];
   int64_t  tile_ext[kPermTileDims];
   int64_t  tile_s_in[kPermTileDims];

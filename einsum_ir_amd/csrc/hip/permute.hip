@@ -228,26 +228,20 @@ void perm_tiled_kernel( PermArgs a ) {
   }
   __syncthreads();
   // write: entry j = output-order elements V j .. V j + V - 1, contiguous in
-  // the output; {output offset, coordinates, LDS index of each element}
-  int32_t const * l_tw = a.tab_w;
-  constexpr int W = ( V == 1 ) ? 4 : 8;
+  // the output; {output offset, coordinates, input-order index of the first
+  // element}: the others follow at tile_t_step (they differ only in the
+  // output's unit-stride dim)
+  int4 const * l_tw = reinterpret_cast< int4 const * >( a.tab_w );
   for( int l_j = threadIdx.x; l_j < l_nv; l_j += kThreads ) {
-    int32_t l_e[W];
-    if constexpr( V == 1 ) {
-      int4 const l_x = reinterpret_cast< int4 const * >( l_tw )[l_j];
-      l_e[0] = l_x.x; l_e[1] = l_x.y; l_e[2] = l_x.z; l_e[3] = l_x.w;
-    }
-    else {
-      int4 const l_x0 = reinterpret_cast< int4 const * >( l_tw )[2 * l_j];
-      int4 const l_x1 = reinterpret_cast< int4 const * >( l_tw )[2 * l_j + 1];
-      l_e[0] = l_x0.x; l_e[1] = l_x0.y; l_e[2] = l_x0.z; l_e[3] = l_x0.w;
-      l_e[4] = l_x1.x; l_e[5] = l_x1.y; l_e[6] = l_x1.z; l_e[7] = l_x1.w;
-    }
-    if( !( l_full || perm_tile_inside( uint32_t( l_e[1] ), l_lim, a.tile_nd ) ) ) continue;
+    int4 const l_e = l_tw[l_j];
+    if( !( l_full || perm_tile_inside( uint32_t( l_e.y ), l_lim, a.tile_nd ) ) ) continue;
     T l_v[V];
 #pragma unroll
-    for( int l_q = 0; l_q < V; l_q++ ) l_v[l_q] = l_tile[l_e[2 + l_q]];
-    T * l_ptr = l_out + l_e[0];
+    for( int l_q = 0; l_q < V; l_q++ ) {
+      int const l_t = l_e.z + l_q * a.tile_t_step;
+      l_v[l_q] = l_tile[l_t + ( l_t >> 6 ) * a.tile_pad];
+    }
+    T * l_ptr = l_out + l_e.x;
     if( l_vec ) {
       Vec4< T > l_x;
       if( a.add ) {
@@ -422,23 +416,34 @@ bool plan_tiled( PermutePlan & plan, int dim_i, int dim_o ) {
     for( int64_t l_x : l_e ) l_t *= l_x;
     return l_t;
   };
-  // at least 1024 elements per tile (grow the outermost run dims), at most 4096
+  // tiles of kPermTileMax elements where the dims allow (grow the outermost
+  // run dims): small tiles leave each workgroup too little work
+  // first the run needs alone may exceed the limit: halve the largest extent,
+  // the unit-stride dims' last (their multiples of 4 keep 16-byte accesses)
+  int const l_ui = (int) ( std::find( l_td.begin(), l_td.end(), dim_i ) - l_td.begin() );
+  int const l_uo = (int) ( std::find( l_td.begin(), l_td.end(), dim_o ) - l_td.begin() );
+  while( tile_n() > kPermTileMax ) {
+    int l_big = -1;
+    for( int l_k = 0; l_k < l_nt; l_k++ ) {
+      if( l_k == l_ui || l_k == l_uo || l_e[l_k] <= 1 ) continue;
+      if( l_big < 0 || l_e[l_k] > l_e[l_big] ) l_big = l_k;
+    }
+    if( l_big < 0 ) l_big = ( l_e[l_ui] >= l_e[l_uo] ) ? l_ui : l_uo;
+    if( l_e[l_big] <= 1 ) return false;
+    l_e[l_big] = ( l_e[l_big] + 1 ) / 2;
+  }
+  // then grow the outermost run dims while the tile stays within the limit
   bool l_grew = true;
-  while( tile_n() < 1024 && l_grew ) {
+  while( l_grew ) {
     l_grew = false;
-    for( int l_k = l_nt - 1; l_k >= 0 && tile_n() < 1024; l_k-- ) {
+    for( int l_k = l_nt - 1; l_k >= 0; l_k-- ) {
       int64_t const l_cap = std::min< int64_t >( plan.size[l_td[l_k]], 128 );
-      if( l_e[l_k] < l_cap ) {
-        l_e[l_k] = std::min( l_cap, 2 * l_e[l_k] );
+      int64_t const l_new = std::min( l_cap, 2 * l_e[l_k] );
+      if( l_new > l_e[l_k] && tile_n() / l_e[l_k] * l_new <= kPermTileMax ) {
+        l_e[l_k] = l_new;
         l_grew = true;
       }
     }
-  }
-  while( tile_n() > kPermTileMax ) {
-    int l_big = 0;
-    for( int l_k = 1; l_k < l_nt; l_k++ ) if( l_e[l_k] > l_e[l_big] ) l_big = l_k;
-    if( l_e[l_big] <= 1 ) return false;
-    l_e[l_big] = ( l_e[l_big] + 1 ) / 2;
   }
   int64_t const l_tn = tile_n();
 
@@ -501,8 +506,14 @@ bool plan_tiled( PermutePlan & plan, int dim_i, int dim_o ) {
   int const l_ko = (int) ( std::find( l_td.begin(), l_td.end(), dim_o ) - l_td.begin() );
   int const l_vw = (    l_e[l_ki] % 4 == 0 && plan.size[dim_i] % 4 == 0
                      && l_e[l_ko] % 4 == 0 && plan.size[dim_o] % 4 == 0 ) ? 4 : 1;
-  int const l_ww = ( l_vw == 1 ) ? 4 : 8;   // ints per write entry
+  int const l_ww = 4;   // ints per write entry
   int64_t const l_nv = l_tn / l_vw;
+  // input-order step between neighbours along the output's unit-stride dim
+  int64_t l_tstep = 1;
+  for( int l_k : l_oin ) {
+    if( l_k == l_ko ) break;
+    l_tstep *= l_e[l_k];
+  }
 
   // tables
   std::vector< int32_t > l_r( 2 * l_nv ), l_w( l_ww * l_nv, 0 );
@@ -532,10 +543,7 @@ bool plan_tiled( PermutePlan & plan, int dim_i, int dim_o ) {
     if( l_off > std::numeric_limits< int32_t >::max() ) return false;
     l_w[l_ww * l_j] = (int32_t) l_off;
     l_w[l_ww * l_j + 1] = (int32_t) l_pack;
-    for( int l_q = 0; l_q < l_vw; l_q++ ) {
-      int64_t const l_t = l_tw[l_vw * l_j + l_q];
-      l_w[l_ww * l_j + 2 + l_q] = (int32_t) ( l_t + ( l_t >> 6 ) * l_pad );
-    }
+    l_w[l_ww * l_j + 2] = (int32_t) l_tw[l_vw * l_j];
   }
   std::size_t const l_bytes_r = l_r.size() * sizeof( int32_t );
   std::size_t const l_bytes_w = l_w.size() * sizeof( int32_t );
@@ -559,6 +567,7 @@ bool plan_tiled( PermutePlan & plan, int dim_i, int dim_o ) {
   a.tile_nd = l_nt;
   a.tile_n = (int32_t) l_tn;
   a.tile_pad = l_pad;
+  a.tile_t_step = (int32_t) l_tstep;
   for( int l_k = 0; l_k < l_nt; l_k++ ) {
     int const l_d = l_td[l_k];
     a.tile_size[l_k]  = plan.size[l_d];
