@@ -21,7 +21,9 @@
 //     two dims each, grown to at least 64 elements): reads run along the
 //     input's run, writes along the output's, LDS reorders, and per-element
 //     tile-relative offsets come from tables built once per plan (TILED);
-//   - if both innermost dims coincide the copy is vectorised along them;
+//     the same holds when both tensors share one short unit-stride dim
+//     (the tile then spans both tensors' next dims);
+//   - if both innermost dims coincide otherwise the copy is vectorised along them;
 //   - anything else is a one-thread-per-element gather.
 #include "etir_internal.h"
 #include <algorithm>
@@ -712,11 +714,13 @@ int plan_permute( int64_t         num_dims,
     return ETIR_SUCCESS;
   }
 
-  if(    l_dim_i >= 0 && l_dim_o >= 0 && l_dim_i != l_dim_o
+  if(    l_dim_i >= 0 && l_dim_o >= 0 && l_n > 1
       && plan.size[l_dim_i] < kTile && plan.size[l_dim_o] < kTile
       && plan_tiled( plan, l_dim_i, l_dim_o ) ) {
     // both unit-stride dims shorter than a tile side (with one long side the
-    // 64 x 64 transpose is faster: measured 4.8-6.4 against 3.9-5.5 TB/s)
+    // 64 x 64 transpose is faster: measured 4.8-6.4 against 3.9-5.5 TB/s);
+    // also when both are the same short dim, where a plain vector copy
+    // reads or writes runs of that dim's length only
     return ETIR_SUCCESS;
   }
 

@@ -109,6 +109,8 @@ TILED_CASES = [
     ("abcde->bdaec", dict(a=12, b=9, c=9, d=12, e=16)),
     ("abcde->bdaec", dict(a=3, b=5, c=6, d=7, e=4)),    # many short dims
     ("abc->cba", dict(a=40, b=2, c=20)),               # runs of two dims each
+    ("abcd->cabd", dict(a=6, b=5, c=70, d=36)),        # same short unit dim d in both
+    ("abcd->cabd", dict(a=3, b=7, c=9, d=5)),          # same unit dim, ragged
 ]
 
 
@@ -119,6 +121,6 @@ def test_permute_tiled(torch_cuda, oracle, expr, sizes, dtype):
     assert "tiled" in desc
 
 
-@pytest.mark.parametrize("expr,sizes", [TILED_CASES[0], TILED_CASES[2]])
+@pytest.mark.parametrize("expr,sizes", [TILED_CASES[0], TILED_CASES[2], TILED_CASES[7]])
 def test_permute_tiled_add(torch_cuda, oracle, expr, sizes):
     _check(torch_cuda, oracle, expr, sizes, dtype=eir.FP32, ktype=eir.ADD)
