@@ -78,6 +78,57 @@ def test_random_binary(torch_cuda, oracle, seed):
              dtype_out=dtype_out)
 
 
+# tiles a test may force through the planner's diagnostic override; the
+# planner ignores a forced tile that does not fit the contraction (dtype, load
+# modes, alignment), and the case then runs its default
+FORCE_TILES = {eir.FP32: [0, 1], eir.BF16: [2, 3, 4, 6, 7, 8]}
+
+
+@pytest.mark.parametrize("seed", range(80))
+def test_random_binary_forced_tile(torch_cuda, oracle, monkeypatch, seed):
+    """Random contractions on every kernel instantiation, not only on the one
+    the planner would choose for the shape."""
+    expr, sizes, dtype, dtype_out, first, last = _binary_case(500 + seed)
+    if dtype == eir.FP64:
+        dtype = eir.BF16 if seed % 2 else eir.FP32
+    tiles = FORCE_TILES[dtype]
+    tile = tiles[seed % len(tiles)]
+    monkeypatch.setenv("ETIR_TILE", str(tile))
+    if tile in (7, 8):
+        monkeypatch.setenv("ETIR_DMA_VARIANT", str(seed % 2))
+    print(f"random forced tile {seed}: {expr} {sizes} dtype {dtype}/{dtype_out} touch {first}/{last} "
+          f"tile {tile}", flush=True)
+    _, desc = run_case(torch_cuda, oracle, expr, sizes, dtype=dtype, first=first, last=last, seed=seed,
+                       dtype_out=dtype_out)
+    print(f"  ran: {desc}", flush=True)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_binary_large(torch_cuda, oracle, seed):
+    """Random layouts with at least 256 output tiles of 256 x 256 (the size at
+    which the planner chooses its largest tiles) and a short K."""
+    rng = np.random.default_rng(4000 + seed)
+    letters = list(string.ascii_lowercase)
+    rng.shuffle(letters)
+    c, m, n, k = letters[0:1], letters[1:3], letters[3:5], letters[5:6 + seed % 2]
+    sizes = {c[0]: int(rng.choice([1, 2, 4]))}
+    mn = (1 << 24) // sizes[c[0]]
+    m0 = int(rng.choice([16, 32, 64, 128, 256]))
+    sizes.update({m[0]: m0, m[1]: int(np.sqrt(mn)) // m0})
+    n0 = int(rng.choice([16, 32, 64, 128, 256]))
+    sizes.update({n[0]: n0, n[1]: int(np.sqrt(mn)) // n0})
+    for d in k:
+        sizes[d] = int(rng.choice([4, 8, 16, 24])) if len(k) == 1 else int(rng.choice([2, 4, 6]))
+    left = list(rng.permutation(c + m + k))
+    right = list(rng.permutation(c + n + k))
+    out = list(rng.permutation(c + m + n))
+    expr = "".join(left) + "," + "".join(right) + "->" + "".join(out)
+    dtype = [eir.BF16, eir.FP32][seed % 2]
+    print(f"random large {seed}: {expr} {sizes} dtype {dtype}", flush=True)
+    _, desc = run_case(torch_cuda, oracle, expr, sizes, dtype=dtype, seed=seed)
+    print(f"  ran: {desc}", flush=True)
+
+
 @pytest.mark.parametrize("seed", range(100))
 def test_random_permute(torch_cuda, oracle, seed):
     rng = np.random.default_rng(2000 + seed)
