@@ -111,6 +111,9 @@ TILED_CASES = [
     ("abc->cba", dict(a=40, b=2, c=20)),               # runs of two dims each
     ("abcd->cabd", dict(a=6, b=5, c=70, d=36)),        # same short unit dim d in both
     ("abcd->cabd", dict(a=3, b=7, c=9, d=5)),          # same unit dim, ragged
+    ("abcd->acdb", dict(a=6, b=8, c=10, d=150)),       # one long unit dim, one of 8
+    ("abc->cba", dict(a=4, b=100, c=130)),             # one long unit dim, one of 4
+    ("abc->cba", dict(a=3, b=70, c=300)),              # ... of 3 (no 16-byte entries)
 ]
 
 
