@@ -407,7 +407,9 @@ bool plan_tiled( PermutePlan & plan, int dim_i, int dim_o ) {
   for( int l_d : l_ri ) l_td.push_back( l_d );
   for( int l_d : l_ro ) if( std::find( l_td.begin(), l_td.end(), l_d ) == l_td.end() ) l_td.push_back( l_d );
   int const l_nt = (int) l_td.size();
-  if( l_nt > kPermTileDims ) return false;
+  // one tile dim (a shared unit-stride dim that no run extends): the
+  // vectorised copy moves the same runs without the tables
+  if( l_nt < 2 || l_nt > kPermTileDims ) return false;
   std::vector< int64_t > l_e( l_nt );
   for( int l_k = 0; l_k < l_nt; l_k++ ) {
     l_e[l_k] = std::max( need( l_ri, l_td[l_k] ), need( l_ro, l_td[l_k] ) );

@@ -127,3 +127,31 @@ def test_permute_tiled(torch_cuda, oracle, expr, sizes, dtype):
 @pytest.mark.parametrize("expr,sizes", [TILED_CASES[0], TILED_CASES[2], TILED_CASES[7]])
 def test_permute_tiled_add(torch_cuda, oracle, expr, sizes):
     _check(torch_cuda, oracle, expr, sizes, dtype=eir.FP32, ktype=eir.ADD)
+
+
+@pytest.mark.parametrize("pad", [0, 4])
+def test_permute_padded_shared_unit_dim(torch_cuda, oracle, pad):
+    """A shared unit-stride dim of 36 (b a d <- a b d) whose neighbours sit
+    36 + pad elements apart in both tensors: packed, the tile spans b and a;
+    padded, no run extends past d and the vectorised copy moves it.  Gaps of
+    the output keep their initial values."""
+    torch = torch_cuda
+    a, b, d = 5, 7, 36
+    row = d + pad
+    sizes = [b, a, d]                                   # output order
+    s_in = [row, row * b, 1]
+    s_out = [row * a, row, 1]
+    n = row * a * b
+    rng = np.random.default_rng(11 + pad)
+    x = rng.uniform(-1, 1, n).astype(np.float32)
+    o0 = rng.uniform(-1, 1, n).astype(np.float32)
+    ref = o0.copy()
+    oracle.permute(sizes, s_in, s_out, x, ref)
+    plan = eir.PermutePlan(sizes, s_in, s_out, dtype=eir.FP32, ktype=eir.COPY)
+    dx, do = _to_dev(torch, x), _to_dev(torch, o0)
+    plan.execute(dx, do, stream=torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    desc = plan.describe()
+    plan.close()
+    np.testing.assert_array_equal(do.cpu().numpy(), ref, err_msg=desc)
+    assert ("tiled" in desc) == (pad == 0), desc
