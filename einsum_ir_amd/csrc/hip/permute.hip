@@ -16,8 +16,9 @@
 //     o, 65-element LDS rows so both the row-wise writes and the column-wise
 //     reads hit 64 distinct banks; every other dim is a batch dim decoded once
 //     per workgroup;
-//   - if both of those unit-stride dims are shorter than a tile side, or one
-//     of them is at most 8 long, the tile instead covers the innermost contiguous run of each tensor (up to
+//   - if both of those unit-stride dims are shorter than a tile side, one of
+//     them is at most 8 long or the input's is at most 16 long, the tile
+//     instead covers the innermost contiguous run of each tensor (up to
 //     two dims each, grown to at least 64 elements): reads run along the
 //     input's run, writes along the output's, LDS reorders, and per-element
 //     tile-relative offsets come from tables built once per plan (TILED);
@@ -718,14 +719,17 @@ int plan_permute( int64_t         num_dims,
 
   if(    l_dim_i >= 0 && l_dim_o >= 0 && l_n > 1
       && (    ( plan.size[l_dim_i] < kTile && plan.size[l_dim_o] < kTile )
-           || std::min( plan.size[l_dim_i], plan.size[l_dim_o] ) <= 8 )
+           || std::min( plan.size[l_dim_i], plan.size[l_dim_o] ) <= 8
+           || plan.size[l_dim_i] <= 16 )
       && plan_tiled( plan, l_dim_i, l_dim_o ) ) {
     // both unit-stride dims shorter than a tile side, or one of them at most
     // 8 long (a 64 x 64 transpose tile would hold 8 of 64 rows: abc->cba at
-    // 4,2048,2048 ran at 1.6 against 4.9 TB/s tiled); with one long side and
-    // the other 16 or more the transpose is faster (5.1-6.3 against 4.6-5.3
-    // TB/s); also when both are the same short dim, where a plain vector
-    // copy reads or writes runs of that dim's length only
+    // 4,2048,2048 ran at 1.6 against 4.9 TB/s tiled), or the input's at most
+    // 16 long (abcde->eabcd with e = 16: 3.6 against 4.2 TB/s); with one long
+    // side and the other 16 or more (the output's) or 32 or more the
+    // transpose is faster (5.1-6.3 against 4.6-5.3 TB/s); also when both are
+    // the same short dim, where a plain vector copy reads or writes runs of
+    // that dim's length only
     return ETIR_SUCCESS;
   }
 
