@@ -495,8 +495,8 @@ void contract_dma_kernel( ContractArgs a ) {
   int32_t const l_nblk   = gridDim.x;
   int32_t l_bid = blockIdx.x;
   if( ( l_nblk & 7 ) == 0 ) l_bid = ( l_bid & 7 ) * ( l_nblk >> 3 ) + ( l_bid >> 3 );
-  int32_t const l_c      = l_bid / l_ntiles;
-  int32_t const l_tile   = l_bid - l_c * l_ntiles;
+  int32_t const l_c      = a.c_inner ? l_bid % a.C : l_bid / l_ntiles;
+  int32_t const l_tile   = a.c_inner ? l_bid / a.C : l_bid - l_c * l_ntiles;
   constexpr int32_t kGroupM = 8;
   int32_t const l_in_grp = kGroupM * a.tiles_n;
   int32_t const l_grp    = l_tile / l_in_grp;

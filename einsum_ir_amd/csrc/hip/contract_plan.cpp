@@ -650,6 +650,21 @@ int plan_contraction_impl( int64_t            num_loops,
   a.N = (int32_t) l_kern_n;
   a.K = (int32_t) l_size_k;
   a.C = (int32_t) l_size_c;
+  {
+    // a C dim innermost in the output: each workgroup (one C index) would
+    // write every C-th element, and the workgroups holding the other C
+    // indices of the same output lines would run far apart in time; with C
+    // fastest in the workgroup order they run side by side (same XCD, same
+    // L2) and complete those lines there
+    int64_t l_min_c = std::numeric_limits< int64_t >::max();
+    int64_t l_min_mn = std::numeric_limits< int64_t >::max();
+    for( Loop const & l_x : l_c ) if( l_x.size > 1 ) l_min_c = std::min( l_min_c, l_x.s[T_OUT] );
+    for( auto const * l_set : { &l_m, &l_n } ) {
+      for( Loop const & l_x : *l_set ) if( l_x.size > 1 ) l_min_mn = std::min( l_min_mn, l_x.s[T_OUT] );
+    }
+    a.c_inner = ( l_size_c > 1 && l_min_c < l_min_mn ) ? 1 : 0;
+    if( a.c_inner ) plan.desc += " c_inner";
+  }
   a.tiles_m = (int32_t) ( ( l_kern_m + l_bm - 1 ) / l_bm );
   a.tiles_n = (int32_t) ( ( l_kern_n + l_bn - 1 ) / l_bn );
   a.k_affine = l_k_affine ? 1 : 0;

@@ -171,6 +171,7 @@ struct ContractArgs {
   int32_t k_full;         // K % BK == 0: no K masking needed
   int32_t out_bf16;       // output stored as bf16 (RNE)
   int32_t out_off32;      // every output byte offset (M part + N part, C part excluded) is < 2^32
+  int32_t c_inner;        // workgroup ids walk C fastest (the output's unit-stride dim is a C dim)
   // complex contractions: element offsets of the imaginary parts (A, B, out)
   int64_t cpx_a, cpx_b, cpx_out;
 };

@@ -222,3 +222,15 @@ def test_every_tile(torch_cuda, oracle, monkeypatch, tile, expr, sizes):
     names = {0: "f32_128x128", 1: "f32_64x64", 2: "bf16_256x256", 6: "bf16_256x128",
              3: "bf16_128x128", 4: "bf16_64x64"}
     assert names[tile] in desc
+
+
+@pytest.mark.parametrize("expr,sizes", [
+    ("efbadx,cfx->abcdex", dict(e=6, f=8, b=5, a=4, d=6, c=7, x=16)),
+    ("eax,ebcdx->abcdx", dict(e=12, a=9, b=5, c=6, d=7, x=8)),
+])
+@pytest.mark.parametrize("dtype", [eir.FP32, eir.BF16, eir.FP64])
+def test_batch_innermost_output(torch_cuda, oracle, expr, sizes, dtype):
+    """A C dim innermost in the output (TCCG's x-batch cases): workgroups walk
+    C fastest; results as for any other order."""
+    _, desc = run_case(torch_cuda, oracle, expr, sizes, dtype=dtype, seed=5)
+    assert "c_inner" in desc, desc
