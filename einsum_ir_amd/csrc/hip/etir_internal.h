@@ -69,11 +69,12 @@ struct PermArgs {
   int32_t  add;       // ktype ADD: out += in
   int32_t  vec_ok;    // 16-byte vector accesses are legal (sizes/strides/alignment)
   // TILED: tile dims (size, extent, strides, tiles along it), tile element
-  // count, LDS padding (elements after every 64) and the offset tables:
-  // tab_r per entry (V consecutive elements in input order) {input offset,
-  // packed coordinates}, tab_w per entry (V consecutive elements in output
-  // order) {output offset, packed coordinates, input-order index of the first
-  // element, 0}, the others tile_t_step apart; coordinates 8 bits per tile dim
+  // count, LDS padding (elements after every 64) and the offset tables, one
+  // entry per V consecutive elements: tab_r the input offset of an entry in
+  // input order, tab_w {output offset, input-order index of the first
+  // element} of an entry in output order (the others tile_t_step apart), and
+  // for edge tiles only tab_rc / tab_wc the entries' packed coordinates
+  // (8 bits per tile dim)
   int32_t  tile_nd;
   int32_t  tile_n;
   int32_t  tile_pad;
@@ -85,6 +86,8 @@ struct PermArgs {
   int64_t  tile_nblk[kPermTileDims];
   int32_t const * tab_r;
   int32_t const * tab_w;
+  int32_t const * tab_rc;
+  int32_t const * tab_wc;
 };
 
 struct PermutePlan {

@@ -211,19 +211,18 @@ void perm_tiled_kernel( PermArgs a ) {
   bool const l_vec = ( V > 1 ) && a.vec_ok;
 
   // read: entry j = input-order elements V j .. V j + V - 1, contiguous in the input
-  int2 const * l_tr = reinterpret_cast< int2 const * >( a.tab_r );
   for( int l_j = threadIdx.x; l_j < l_nv; l_j += kThreads ) {
-    int2 const l_e = l_tr[l_j];
-    if( !( l_full || perm_tile_inside( uint32_t( l_e.y ), l_lim, a.tile_nd ) ) ) continue;
+    if( !( l_full || perm_tile_inside( uint32_t( a.tab_rc[l_j] ), l_lim, a.tile_nd ) ) ) continue;
+    int32_t const l_off = a.tab_r[l_j];
     T l_v[V];
     if( l_vec ) {
-      Vec4< T > const l_x = *reinterpret_cast< Vec4< T > const * >( l_in + l_e.x );
+      Vec4< T > const l_x = *reinterpret_cast< Vec4< T > const * >( l_in + l_off );
 #pragma unroll
       for( int l_q = 0; l_q < V; l_q++ ) l_v[l_q] = l_x.v[l_q];
     }
     else {
 #pragma unroll
-      for( int l_q = 0; l_q < V; l_q++ ) l_v[l_q] = l_in[l_e.x + l_q];
+      for( int l_q = 0; l_q < V; l_q++ ) l_v[l_q] = l_in[l_off + l_q];
     }
     int const l_t = V * l_j;
 #pragma unroll
@@ -231,17 +230,17 @@ void perm_tiled_kernel( PermArgs a ) {
   }
   __syncthreads();
   // write: entry j = output-order elements V j .. V j + V - 1, contiguous in
-  // the output; {output offset, coordinates, input-order index of the first
-  // element}: the others follow at tile_t_step (they differ only in the
-  // output's unit-stride dim)
-  int4 const * l_tw = reinterpret_cast< int4 const * >( a.tab_w );
+  // the output; {output offset, input-order index of the first element}: the
+  // others follow at tile_t_step (they differ only in the output's
+  // unit-stride dim)
+  int2 const * l_tw = reinterpret_cast< int2 const * >( a.tab_w );
   for( int l_j = threadIdx.x; l_j < l_nv; l_j += kThreads ) {
-    int4 const l_e = l_tw[l_j];
-    if( !( l_full || perm_tile_inside( uint32_t( l_e.y ), l_lim, a.tile_nd ) ) ) continue;
+    if( !( l_full || perm_tile_inside( uint32_t( a.tab_wc[l_j] ), l_lim, a.tile_nd ) ) ) continue;
+    int2 const l_e = l_tw[l_j];
     T l_v[V];
 #pragma unroll
     for( int l_q = 0; l_q < V; l_q++ ) {
-      int const l_t = l_e.z + l_q * a.tile_t_step;
+      int const l_t = l_e.y + l_q * a.tile_t_step;
       l_v[l_q] = l_tile[l_t + ( l_t >> 6 ) * a.tile_pad];
     }
     T * l_ptr = l_out + l_e.x;
@@ -511,7 +510,6 @@ bool plan_tiled( PermutePlan & plan, int dim_i, int dim_o ) {
   int const l_ko = (int) ( std::find( l_td.begin(), l_td.end(), dim_o ) - l_td.begin() );
   int const l_vw = (    l_e[l_ki] % 4 == 0 && plan.size[dim_i] % 4 == 0
                      && l_e[l_ko] % 4 == 0 && plan.size[dim_o] % 4 == 0 ) ? 4 : 1;
-  int const l_ww = 4;   // ints per write entry
   int64_t const l_nv = l_tn / l_vw;
   // input-order step between neighbours along the output's unit-stride dim
   int64_t l_tstep = 1;
@@ -520,8 +518,9 @@ bool plan_tiled( PermutePlan & plan, int dim_i, int dim_o ) {
     l_tstep *= l_e[l_k];
   }
 
-  // tables
-  std::vector< int32_t > l_r( 2 * l_nv ), l_w( l_ww * l_nv, 0 );
+  // tables: write entries {output offset, first input-order index} (int2),
+  // read offsets, and the packed coordinates of both (edge tiles only)
+  std::vector< int32_t > l_w( 2 * l_nv ), l_r( l_nv ), l_rc( l_nv ), l_wc( l_nv );
   int64_t l_c[kPermTileDims];
   auto offset_pack = [&]( int64_t const * st, int64_t & off, uint32_t & pack ) {
     off = 0;
@@ -537,8 +536,8 @@ bool plan_tiled( PermutePlan & plan, int dim_i, int dim_o ) {
     uint32_t l_pack;
     offset_pack( plan.s_in, l_off, l_pack );
     if( l_off > std::numeric_limits< int32_t >::max() ) return false;
-    l_r[2 * l_j] = (int32_t) l_off;
-    l_r[2 * l_j + 1] = (int32_t) l_pack;
+    l_r[l_j]  = (int32_t) l_off;
+    l_rc[l_j] = (int32_t) l_pack;
   }
   for( int64_t l_j = 0; l_j < l_nv; l_j++ ) {
     coords_of( l_vw * l_j, l_oout, l_c );
@@ -546,20 +545,21 @@ bool plan_tiled( PermutePlan & plan, int dim_i, int dim_o ) {
     uint32_t l_pack;
     offset_pack( plan.s_out, l_off, l_pack );
     if( l_off > std::numeric_limits< int32_t >::max() ) return false;
-    l_w[l_ww * l_j] = (int32_t) l_off;
-    l_w[l_ww * l_j + 1] = (int32_t) l_pack;
-    l_w[l_ww * l_j + 2] = (int32_t) l_tw[l_vw * l_j];
+    l_w[2 * l_j]     = (int32_t) l_off;
+    l_w[2 * l_j + 1] = (int32_t) l_tw[l_vw * l_j];
+    l_wc[l_j]        = (int32_t) l_pack;
   }
-  std::size_t const l_bytes_r = l_r.size() * sizeof( int32_t );
-  std::size_t const l_bytes_w = l_w.size() * sizeof( int32_t );
+  // one blob: write entries first (8-byte aligned), then the int32 arrays
+  std::vector< int32_t > l_blob;
+  l_blob.reserve( 5 * l_nv );
+  for( auto const * l_v : { &l_w, &l_r, &l_rc, &l_wc } ) l_blob.insert( l_blob.end(), l_v->begin(), l_v->end() );
+  std::size_t const l_bytes = l_blob.size() * sizeof( int32_t );
   void * l_dev = nullptr;
-  if( hipMalloc( &l_dev, l_bytes_r + l_bytes_w ) != hipSuccess ) {
+  if( hipMalloc( &l_dev, l_bytes ) != hipSuccess ) {
     (void) hipGetLastError();
     return false;
   }
-  if(    hipMemcpy( l_dev, l_r.data(), l_bytes_r, hipMemcpyHostToDevice ) != hipSuccess
-      || hipMemcpy( static_cast< char * >( l_dev ) + l_bytes_r, l_w.data(), l_bytes_w,
-                    hipMemcpyHostToDevice ) != hipSuccess ) {
+  if( hipMemcpy( l_dev, l_blob.data(), l_bytes, hipMemcpyHostToDevice ) != hipSuccess ) {
     (void) hipGetLastError();
     (void) hipFree( l_dev );
     return false;
@@ -581,8 +581,11 @@ bool plan_tiled( PermutePlan & plan, int dim_i, int dim_o ) {
     a.tile_s_out[l_k] = plan.s_out[l_d];
     a.tile_nblk[l_k]  = ( plan.size[l_d] + l_e[l_k] - 1 ) / l_e[l_k];
   }
-  a.tab_r = static_cast< int32_t const * >( l_dev );
-  a.tab_w = reinterpret_cast< int32_t const * >( static_cast< char * >( l_dev ) + l_bytes_r );
+  int32_t const * l_tabs = static_cast< int32_t const * >( l_dev );
+  a.tab_w  = l_tabs;
+  a.tab_r  = l_tabs + 2 * l_nv;
+  a.tab_rc = l_tabs + 3 * l_nv;
+  a.tab_wc = l_tabs + 4 * l_nv;
   a.num_batch = 0;
   a.num_batch_total = 1;
   for( int l_d = 0; l_d < l_n; l_d++ ) {
