@@ -121,9 +121,19 @@ struct DmaLoader< R, BK, W, LOAD_VEC_MN > {
 
   uint32_t m_off[NJ];
   int32_t  m_kk[NJ];
+  uint32_t m_valid;    // bit j: chunk j's row is inside the operand
 
   __device__ inline void init( int32_t const * tab_rows, int32_t rows, int32_t row0, int32_t sk,
                                int wave, int lane ) {
+    load_rows( tab_rows, rows, row0, wave, lane );
+    finalize( sk );
+  }
+
+  // first half of init: reads the row offsets (clamped index, unconditional)
+  // into m_off without using them, so the loads can be issued long before
+  // finalize() without forcing a wait
+  __device__ inline void load_rows( int32_t const * tab_rows, int32_t rows, int32_t row0, int wave, int lane ) {
+    m_valid = 0;
 #pragma unroll
     for( int l_j = 0; l_j < NJ; l_j++ ) {
       int const l_chunk = wave * NJ + l_j;
@@ -132,7 +142,16 @@ struct DmaLoader< R, BK, W, LOAD_VEC_MN > {
       int const l_g  = l_p ^ int( swz_mn( l_kk ) );
       int32_t const l_row = row0 + 8 * l_g;
       m_kk[l_j] = l_kk;
-      m_off[l_j] = ( l_row < rows ) ? uint32_t( 2 * ( tab_rows[l_row] + l_kk * sk ) ) : kDmaOob;
+      if( l_row < rows ) m_valid |= 1u << l_j;
+      m_off[l_j] = uint32_t( tab_rows[min( l_row, rows - 1 )] );
+    }
+  }
+
+  // second half: byte offsets of the lane's 16-byte segment in k-step 0
+  __device__ inline void finalize( int32_t sk ) {
+#pragma unroll
+    for( int l_j = 0; l_j < NJ; l_j++ ) {
+      m_off[l_j] = ( ( m_valid >> l_j ) & 1u ) ? uint32_t( 2 * ( int32_t( m_off[l_j] ) + m_kk[l_j] * sk ) ) : kDmaOob;
     }
   }
 
@@ -344,9 +363,34 @@ struct ReadOrder {
 // The last three steps issue no DMA (vmcnt(0) before the barrier) and the
 // final step has no barrier.
 // ---------------------------------------------------------------------------
-template< int BM, int BN, int BK, int WM, int WN, int MA, int MB, int STAGES, typename LdA, typename LdB,
-          typename FrA, typename FrB, int TM, int TN >
-__device__ __attribute__( ( always_inline ) ) inline void mainloop_scheduled(
+// prologue of the main loop: the loads of k-steps 0 .. STAGES-2 (steps >= nk
+// load zeros) into stage buffers 0 .. STAGES-2
+template< int BK, int STAGES, typename LdA, typename LdB >
+__device__ __attribute__( ( always_inline ) ) inline void prologue_issue( char * l_lds, LdA & l_lda, LdB & l_ldb,
+                                                                          i32x4 l_ra, i32x4 l_rb, int l_wave,
+                                                                          int32_t l_K, uint32_t l_kb_a,
+                                                                          uint32_t l_kb_b ) {
+  constexpr int SA = LdA::STAGE_BYTES;
+  constexpr int SB = LdB::STAGE_BYTES;
+  uint32_t const l_lds0 = lds_addr( l_lds );
+#pragma unroll
+  for( int l_t = 0; l_t < STAGES - 1; l_t++ ) {
+    uint32_t const l_st = l_lds0 + uint32_t( l_t ) * ( SA + SB );
+    l_lda.issue( l_ra, l_st, l_wave, l_t * BK, l_K, uint32_t( l_t ) * l_kb_a );
+    l_ldb.issue( l_rb, l_st + SA, l_wave, l_t * BK, l_K, uint32_t( l_t ) * l_kb_b );
+  }
+}
+
+// Main loop after the prologue's loads were issued.  FIRST_VMCNT: loads or
+// stores that may still be in flight beyond the prologue's when the loop
+// starts (-1: none, the wait for step 0 counts only the prologue; otherwise
+// the loop waits for everything, vmcnt(0)).  Ends after the last step's
+// MFMAs are issued; the stage buffers may still be read by other waves.
+// SWAPAB: the MFMA takes the B fragment as its first operand, so the
+// accumulators hold the tile transposed (see epilogue_fast_f32_t).
+template< int BM, int BN, int BK, int WM, int WN, int MA, int MB, int STAGES, int FIRST_VMCNT, bool SWAPAB,
+          typename LdA, typename LdB, typename FrA, typename FrB, int TM, int TN >
+__device__ __attribute__( ( always_inline ) ) inline void mainloop_body(
     f32x16 ( &l_acc )[TM][TN], char * l_lds, LdA & l_lda, LdB & l_ldb, FrA const & l_fra, FrB const & l_frb,
     i32x4 l_ra, i32x4 l_rb, int l_wave, int32_t l_K, int32_t l_nk, uint32_t l_kb_a, uint32_t l_kb_b ) {
   constexpr int SA  = LdA::STAGE_BYTES;
@@ -370,15 +414,9 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_scheduled(
   typename FrA::Part l_pa[2][TM];
   typename FrB::Part l_pb[2][TN];
 
-  // prologue: steps 0 .. STAGES-2 (steps >= nk load zeros), then fragments
-  // of step 0, substep 0
-#pragma unroll
-  for( int l_t = 0; l_t < STAGES - 1; l_t++ ) {
-    uint32_t const l_st = l_lds0 + uint32_t( l_t ) * ( SA + SB );
-    l_lda.issue( l_ra, l_st, l_wave, l_t * BK, l_K, uint32_t( l_t ) * l_kb_a );
-    l_ldb.issue( l_rb, l_st + SA, l_wave, l_t * BK, l_K, uint32_t( l_t ) * l_kb_b );
-  }
-  wait_vmcnt< ( STAGES - 2 ) * NJW >();
+  // step 0 has landed, then fragments of step 0, substep 0
+  if constexpr( FIRST_VMCNT < 0 ) wait_vmcnt< ( STAGES - 2 ) * NJW >();
+  else                            wait_vmcnt< 0 >();
   barrier_lds();
   static_for< U >( [&]( auto rc ) __attribute__( ( always_inline ) ) {
     constexpr int l_r = decltype( rc )::value;
@@ -404,9 +442,16 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_scheduled(
       constexpr int l_p = l_q % NMF;                 // MFMA within the substep
       constexpr int l_i = kMo.i[l_p];
       constexpr int l_j = kMo.j[l_p];
-      l_acc[l_i][l_j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16( FrA::value( l_pa[l_s][l_i] ),
-                                                                 FrB::value( l_pb[l_s][l_j] ),
-                                                                 l_acc[l_i][l_j], 0, 0, 0 );
+      if constexpr( SWAPAB ) {
+        l_acc[l_i][l_j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16( FrB::value( l_pb[l_s][l_j] ),
+                                                                   FrA::value( l_pa[l_s][l_i] ),
+                                                                   l_acc[l_i][l_j], 0, 0, 0 );
+      }
+      else {
+        l_acc[l_i][l_j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16( FrA::value( l_pa[l_s][l_i] ),
+                                                                   FrB::value( l_pb[l_s][l_j] ),
+                                                                   l_acc[l_i][l_j], 0, 0, 0 );
+      }
       if constexpr( l_s == 0 ) {
         // fragments of substep 1 of this step
         static_for< U >( [&]( auto rc ) __attribute__( ( always_inline ) ) {
@@ -463,10 +508,44 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_scheduled(
   for( ; l_t < l_nk - ( STAGES - 1 ); l_t++ ) iteration( l_t, l_yes, l_yes );
   for( ; l_t < l_nk - 1; l_t++ ) iteration( l_t, l_no, l_yes );
   iteration( l_nk - 1, l_no, l_no );
+}
+
+template< int BM, int BN, int BK, int WM, int WN, int MA, int MB, int STAGES, typename LdA, typename LdB,
+          typename FrA, typename FrB, int TM, int TN >
+__device__ __attribute__( ( always_inline ) ) inline void mainloop_scheduled(
+    f32x16 ( &l_acc )[TM][TN], char * l_lds, LdA & l_lda, LdB & l_ldb, FrA const & l_fra, FrB const & l_frb,
+    i32x4 l_ra, i32x4 l_rb, int l_wave, int32_t l_K, int32_t l_nk, uint32_t l_kb_a, uint32_t l_kb_b ) {
+  prologue_issue< BK, STAGES >( l_lds, l_lda, l_ldb, l_ra, l_rb, l_wave, l_K, l_kb_a, l_kb_b );
+  mainloop_body< BM, BN, BK, WM, WN, MA, MB, STAGES, -1, false >( l_acc, l_lds, l_lda, l_ldb, l_fra, l_frb, l_ra,
+                                                                l_rb, l_wave, l_K, l_nk, l_kb_a, l_kb_b );
   // the prologue's loads past the last step (zeros) still target LDS: drain
   // them before the epilogue reuses it
   wait_vmcnt< 0 >();
   barrier_lds();
+}
+
+// ---------------------------------------------------------------------------
+// tile order: linear tile id -> (c, first row, first column).  C outermost
+// (or innermost for c_inner), and within one C index groups of 8 tile rows
+// walked column by column, so the workgroups running side by side on one XCD
+// share their A rows and B columns in that XCD's L2.
+// ---------------------------------------------------------------------------
+template< int BM, int BN >
+__device__ inline void decode_tile( ContractArgs const & a, int32_t l_lin, int32_t & o_c, int32_t & o_m0,
+                                    int32_t & o_n0 ) {
+  int32_t const l_ntiles = a.tiles_m * a.tiles_n;
+  int32_t const l_c      = a.c_inner ? l_lin % a.C : l_lin / l_ntiles;
+  int32_t const l_tile   = a.c_inner ? l_lin / a.C : l_lin - l_c * l_ntiles;
+  constexpr int32_t kGroupM = 8;
+  int32_t const l_in_grp = kGroupM * a.tiles_n;
+  int32_t const l_grp    = l_tile / l_in_grp;
+  int32_t const l_fm     = l_grp * kGroupM;
+  int32_t const l_gsz    = min( a.tiles_m - l_fm, kGroupM );
+  int32_t const l_tm     = l_fm + ( l_tile - l_grp * l_in_grp ) % l_gsz;
+  int32_t const l_tn     = ( l_tile - l_grp * l_in_grp ) / l_gsz;
+  o_c  = l_c;
+  o_m0 = l_tm * BM;
+  o_n0 = l_tn * BN;
 }
 
 // ---------------------------------------------------------------------------
@@ -491,21 +570,11 @@ void contract_dma_kernel( ContractArgs a ) {
   __shared__ __attribute__( ( aligned( 1024 ) ) ) char l_lds[STAGES * ( SA + SB )];
 
   // tile order: see contract_kernel (XCD-contiguous ranges, groups of 8 tile rows)
-  int32_t const l_ntiles = a.tiles_m * a.tiles_n;
-  int32_t const l_nblk   = gridDim.x;
+  int32_t const l_nblk = gridDim.x;
   int32_t l_bid = blockIdx.x;
   if( ( l_nblk & 7 ) == 0 ) l_bid = ( l_bid & 7 ) * ( l_nblk >> 3 ) + ( l_bid >> 3 );
-  int32_t const l_c      = a.c_inner ? l_bid % a.C : l_bid / l_ntiles;
-  int32_t const l_tile   = a.c_inner ? l_bid / a.C : l_bid - l_c * l_ntiles;
-  constexpr int32_t kGroupM = 8;
-  int32_t const l_in_grp = kGroupM * a.tiles_n;
-  int32_t const l_grp    = l_tile / l_in_grp;
-  int32_t const l_fm     = l_grp * kGroupM;
-  int32_t const l_gsz    = min( a.tiles_m - l_fm, kGroupM );
-  int32_t const l_tm     = l_fm + ( l_tile - l_grp * l_in_grp ) % l_gsz;
-  int32_t const l_tn     = ( l_tile - l_grp * l_in_grp ) / l_gsz;
-  int32_t const l_m0     = l_tm * BM;
-  int32_t const l_n0     = l_tn * BN;
+  int32_t l_c, l_m0, l_n0;
+  decode_tile< BM, BN >( a, l_bid, l_c, l_m0, l_n0 );
 
   int const l_lane = threadIdx.x & 63;
   int const l_wave = __builtin_amdgcn_readfirstlane( threadIdx.x >> 6 );
@@ -617,6 +686,189 @@ void contract_dma_kernel( ContractArgs a ) {
   EpilogueTabs< BM, BN, T > l_tabs;
   l_tabs.load( a, l_m0, l_n0 );
   epilogue< BM, BN, WM, WN, TM, TN, T >( a, l_acc, l_tabs, l_lds, l_c, l_m0, l_n0, l_wm, l_wn, l_lane );
+}
+
+
+// ---------------------------------------------------------------------------
+// Persistent variant (VEC_MN x VEC_MN, scheduled BK 32 loop): one workgroup
+// per CU walks its share of the tiles.  Per tile it
+//   * reads the NEXT task's loader offsets and epilogue tables (global loads
+//     that land during this tile's main loop),
+//   * runs the main loop,
+//   * issues the next task's first STAGES-1 k-steps before its own output
+//     stores (the loads land while the stores drain; the epilogue's tables
+//     live in their own LDS region), then stores the output.
+// Tiles are split into XCD-contiguous ranges exactly as in the one-tile-per-
+// workgroup kernel (workgroup w runs on XCD w % 8 and takes every
+// (gridDim / 8)-th tile of XCD w % 8's range), so the L2 sharing is the same.
+//
+// Staggered start (dma_phases P > 1): workgroup w waits (w / 8) % P times
+// dma_stagger sleep units of about 1 us before its first tile.  Workgroups
+// that finish their tiles at the same moment store at the same moment, and
+// the 32 CUs of one XCD storing 256 KB each at once are bounded by that
+// XCD's share of the write bandwidth while their matrix cores idle; with the
+// phases offset, part of one phase's stores overlap another's main loop.
+// (Offsets between whole XCDs do not help: each XCD's own write path is the
+// bound.)
+//
+// Runs only contractions whose tiles are all full and take the plain fast
+// epilogue: fp32 output, 32-bit output offsets, ZERO first touch, no last
+// touch (persistent_dma_eligible; a second store variant in the kernel makes
+// the compiler copy the accumulators into VGPRs); the others use
+// contract_dma_kernel.
+// ---------------------------------------------------------------------------
+__host__ __device__ inline bool persistent_dma_eligible( ContractArgs const & a, int BM, int BN ) {
+  return a.M % BM == 0 && a.N % BN == 0 && a.out_off32 && !a.out_bf16 && a.first_touch == ETIR_KTYPE_ZERO
+      && a.last_touch == ETIR_KTYPE_UNDEFINED;
+}
+
+template< int BM, int BN, int BK, int WM, int WN, int STAGES >
+__global__ __launch_bounds__( 64 * WM * WN, 1 )
+void contract_dma_persistent_kernel( ContractArgs a ) {
+  constexpr int MA  = LOAD_VEC_MN;
+  constexpr int MB  = LOAD_VEC_MN;
+  constexpr int W   = WM * WN;
+  constexpr int T   = 64 * W;
+  constexpr int TM  = BM / WM / 32;
+  constexpr int TN  = BN / WN / 32;
+  typedef DmaLoader< BM, BK, W, MA > LdA;
+  typedef DmaLoader< BN, BK, W, MB > LdB;
+  typedef EpilogueTabs< BM, BN, T > Tabs;
+  constexpr int SA  = LdA::STAGE_BYTES;
+  constexpr int SB  = LdB::STAGE_BYTES;
+  constexpr int OPS = STAGES * ( SA + SB );              // operand stage buffers
+  constexpr int TABS = EpilogueLds< BM, BN, WM, WN, TM, TN >::TABS;
+  static_assert( BK == 32 && STAGES >= 3, "persistent kernel runs the scheduled BK 32 loop" );
+
+  __shared__ __attribute__( ( aligned( 1024 ) ) ) char l_lds[OPS + TABS];
+  int32_t * l_tabs_lds = reinterpret_cast< int32_t * >( l_lds + OPS );
+
+  // this workgroup's tiles: linear ids l_first, l_first + l_step, ... < l_end
+  int32_t const l_ntiles_all = a.C * a.tiles_m * a.tiles_n;
+  int32_t const l_nwg = gridDim.x;
+  int32_t l_first, l_step, l_end;
+  if( ( l_nwg & 7 ) == 0 && ( l_ntiles_all & 7 ) == 0 ) {
+    int32_t const l_x  = blockIdx.x & 7;
+    int32_t const l_t8 = l_ntiles_all >> 3;
+    l_first = l_x * l_t8 + ( blockIdx.x >> 3 );
+    l_step  = l_nwg >> 3;
+    l_end   = ( l_x + 1 ) * l_t8;
+  }
+  else {
+    l_first = blockIdx.x;
+    l_step  = l_nwg;
+    l_end   = l_ntiles_all;
+  }
+  if( l_first >= l_end ) return;
+  int32_t const l_ntiles = ( l_end - l_first + l_step - 1 ) / l_step;
+
+  int const l_lane = threadIdx.x & 63;
+  int const l_wave = __builtin_amdgcn_readfirstlane( threadIdx.x >> 6 );
+  int const l_wm   = l_wave / WN;
+  int const l_wn   = l_wave - l_wm * WN;
+
+  if( a.dma_phases > 1 ) {
+    int32_t const l_ph = ( blockIdx.x >> 3 ) % a.dma_phases;
+    for( int32_t l_z = 0; l_z < l_ph * a.dma_stagger; l_z++ ) __builtin_amdgcn_s_sleep( 32 );
+  }
+
+  DmaFrag< BM, BK, TM, MA > l_fra;
+  DmaFrag< BN, BK, TN, MB > l_frb;
+  l_fra.init( l_wm * TM * 32, l_lane );
+  l_frb.init( l_wn * TN * 32, l_lane );
+
+  int32_t const l_K  = a.K;
+  int32_t const l_nk = ( l_K + BK - 1 ) / BK;
+  uint32_t const l_kb_a = uint32_t( 2 * BK * a.sk_a );
+  uint32_t const l_kb_b = uint32_t( 2 * BK * a.sk_b );
+  uint16_t const * l_pa0 = reinterpret_cast< uint16_t const * >( a.a );
+  uint16_t const * l_pb0 = reinterpret_cast< uint16_t const * >( a.b );
+
+  int32_t const l_ntasks = l_ntiles;
+  auto task_tile = [&]( int32_t t ) { return l_first + t * l_step; };
+
+  // current task
+  int32_t l_c, l_m0, l_n0;
+  decode_tile< BM, BN >( a, task_tile( 0 ), l_c, l_m0, l_n0 );
+  LdA l_lda;
+  LdB l_ldb;
+  l_lda.init( a.tm_a, a.M, l_m0, a.sk_a, l_wave, l_lane );
+  l_ldb.init( a.tn_b, a.N, l_n0, a.sk_b, l_wave, l_lane );
+  i32x4 l_ra = make_rsrc( l_pa0 + a.tc_a[l_c], kDmaOob );
+  i32x4 l_rb = make_rsrc( l_pb0 + a.tc_b[l_c], kDmaOob );
+  Tabs l_tabs;
+  l_tabs.load( a, l_m0, l_n0 );
+  prologue_issue< BK, STAGES >( l_lds, l_lda, l_ldb, l_ra, l_rb, l_wave, l_K, l_kb_a, l_kb_b );
+
+  for( int32_t l_t = 0; l_t < l_ntasks; l_t++ ) {
+    bool const l_has_next = l_t + 1 < l_ntasks;
+
+    // the next task's offsets: read now, used after this task's main loop
+    int32_t l_nc = l_c, l_nm0 = l_m0, l_nn0 = l_n0;
+    LdA l_nlda = l_lda;
+    LdB l_nldb = l_ldb;
+    Tabs l_ntabs = l_tabs;
+    if( l_has_next ) {
+      // loads only: their values are first used after the main loop, so
+      // nothing waits for them (or for the stores issued before them) here
+      decode_tile< BM, BN >( a, task_tile( l_t + 1 ), l_nc, l_nm0, l_nn0 );
+      l_nlda.load_rows( a.tm_a, a.M, l_nm0, l_wave, l_lane );
+      l_nldb.load_rows( a.tn_b, a.N, l_nn0, l_wave, l_lane );
+      l_ntabs.load( a, l_nm0, l_nn0 );
+    }
+
+    f32x16 l_acc[TM][TN];
+#pragma unroll
+    for( int l_i = 0; l_i < TM; l_i++ )
+#pragma unroll
+      for( int l_j = 0; l_j < TN; l_j++ )
+        l_acc[l_i][l_j] = f32x16( 0.0f );
+    if( l_nk > 0 ) {
+      // the previous task's output stores may still be in flight behind this
+      // task's prologue loads: the first wait is for everything
+      mainloop_body< BM, BN, BK, WM, WN, MA, MB, STAGES, 0, false >( l_acc, l_lds, l_lda, l_ldb, l_fra, l_frb, l_ra,
+                                                                   l_rb, l_wave, l_K, l_nk, l_kb_a, l_kb_b );
+    }
+    // every wave is done with the operand buffers (and nothing of this task
+    // is still loading into them)
+    wait_vmcnt< 0 >();
+    wait_lgkmcnt0();
+    barrier_lds();
+
+    if( l_has_next ) {
+      l_nlda.finalize( a.sk_a );
+      l_nldb.finalize( a.sk_b );
+    }
+    i32x4 const l_nra = make_rsrc( l_pa0 + a.tc_a[l_nc], kDmaOob );
+    i32x4 const l_nrb = make_rsrc( l_pb0 + a.tc_b[l_nc], kDmaOob );
+    if( l_has_next ) {
+      prologue_issue< BK, STAGES >( l_lds, l_nlda, l_nldb, l_nra, l_nrb, l_wave, l_K, l_kb_a, l_kb_b );
+    }
+    l_tabs.stage( l_tabs_lds );
+    wait_lgkmcnt0();
+    barrier_lds();
+    {
+      float * l_base = reinterpret_cast< float * >( a.out ) + a.tc_out[l_c];
+      int const l_row0 = l_wm * TM * 32;
+      int const l_col0 = l_wn * TN * 32;
+      int32_t const * l_so_m = l_tabs_lds;
+      int32_t const * l_so_n = l_tabs_lds + 2 * BM;
+      epilogue_fast_f32< TM, TN, false >( l_base, l_acc, l_so_m, l_so_n, l_row0, l_col0, l_lane );
+      // the staged tables are rewritten at the next task's epilogue, a whole
+      // main loop (and its barriers) later
+    }
+
+    l_c = l_nc;
+    l_m0 = l_nm0;
+    l_n0 = l_nn0;
+    l_lda = l_nlda;
+    l_ldb = l_nldb;
+    l_tabs = l_ntabs;
+    l_ra = l_nra;
+    l_rb = l_nrb;
+  }
+  // nothing may still write LDS when the workgroup ends
+  wait_vmcnt< 0 >();
 }
 
 }  // namespace kern

@@ -187,7 +187,8 @@ struct Loader< R, BK, T, ESZ, LOAD_SCALAR > {
 #pragma unroll
       for( int l_e = 0; l_e < V; l_e++ ) {
         l_v[l_e] = TE( 0 );
-        if( l_kok[l_e] && m_row_off[l_i] >= 0 ) l_v[l_e] = base[ m_row_off[l_i] + l_koff[l_e] ];
+        // row and k offsets each fit int32 (planner), their sum need not
+        if( l_kok[l_e] && m_row_off[l_i] >= 0 ) l_v[l_e] = base[ int64_t( m_row_off[l_i] ) + l_koff[l_e] ];
       }
       m_reg[l_i] = *reinterpret_cast< u32x4 * >( l_v );
     }
@@ -441,43 +442,53 @@ struct EpilogueTabs {
   static constexpr int NM = ( BM + T - 1 ) / T;
   static constexpr int NN = ( BN + T - 1 ) / T;
   int32_t m_out[NM], m_aux[NM], n_out[NN], n_aux[NN];
+  uint32_t m_valid;   // bit i: entry i of the m tables is a row inside M; bit 16 + i: n likewise
 
+  // The loads read clamped indices unconditionally and nothing here uses
+  // their values: a caller may issue them long before the tables are
+  // staged without a wait for them (or for anything issued before them).
   __device__ inline void load( ContractArgs const & a, int32_t l_m0, int32_t l_n0 ) {
-    bool const l_has_aux = ( a.aux != nullptr );
+    static_assert( NM <= 16 && NN <= 16, "validity mask" );
+    m_valid = 0;
 #pragma unroll
     for( int l_i = 0; l_i < NM; l_i++ ) {
       int const l_x = threadIdx.x + l_i * T;
       int32_t const l_m = l_m0 + l_x;
-      bool const l_ok = l_x < BM && l_m < a.M;
-      m_out[l_i] = l_ok ? a.tm_out[l_m] : 0;
-      m_aux[l_i] = ( l_ok && l_has_aux ) ? a.tm_aux[l_m] : 0;
+      if( l_x < BM && l_m < a.M ) m_valid |= 1u << l_i;
+      int32_t const l_mc = min( l_m, a.M - 1 );
+      m_out[l_i] = a.tm_out[l_mc];
+      m_aux[l_i] = a.tm_aux[l_mc];
     }
 #pragma unroll
     for( int l_i = 0; l_i < NN; l_i++ ) {
       int const l_x = threadIdx.x + l_i * T;
       int32_t const l_n = l_n0 + l_x;
-      bool const l_ok = l_x < BN && l_n < a.N;
-      n_out[l_i] = l_ok ? a.tn_out[l_n] : 0;
-      n_aux[l_i] = ( l_ok && l_has_aux ) ? a.tn_aux[l_n] : 0;
+      if( l_x < BN && l_n < a.N ) m_valid |= 1u << ( 16 + l_i );
+      int32_t const l_nc = min( l_n, a.N - 1 );
+      n_out[l_i] = a.tn_out[l_nc];
+      n_aux[l_i] = a.tn_aux[l_nc];
     }
   }
 
-  // LDS layout: m_out[BM], m_aux[BM], n_out[BN], n_aux[BN]
+  // LDS layout: m_out[BM], m_aux[BM], n_out[BN], n_aux[BN]; entries outside
+  // the tensor are 0
   __device__ inline void stage( int32_t * lds ) const {
 #pragma unroll
     for( int l_i = 0; l_i < NM; l_i++ ) {
       int const l_x = threadIdx.x + l_i * T;
       if( l_x < BM ) {
-        lds[l_x]      = m_out[l_i];
-        lds[BM + l_x] = m_aux[l_i];
+        bool const l_ok = ( m_valid >> l_i ) & 1u;
+        lds[l_x]      = l_ok ? m_out[l_i] : 0;
+        lds[BM + l_x] = l_ok ? m_aux[l_i] : 0;
       }
     }
 #pragma unroll
     for( int l_i = 0; l_i < NN; l_i++ ) {
       int const l_x = threadIdx.x + l_i * T;
       if( l_x < BN ) {
-        lds[2 * BM + l_x]      = n_out[l_i];
-        lds[2 * BM + BN + l_x] = n_aux[l_i];
+        bool const l_ok = ( m_valid >> ( 16 + l_i ) ) & 1u;
+        lds[2 * BM + l_x]      = l_ok ? n_out[l_i] : 0;
+        lds[2 * BM + BN + l_x] = l_ok ? n_aux[l_i] : 0;
       }
     }
   }

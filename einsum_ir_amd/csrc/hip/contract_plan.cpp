@@ -455,11 +455,17 @@ int plan_contraction_impl( int64_t            num_loops,
   }
   // VEC_MN x VEC_MN runs the explicitly scheduled BK 32 / 4-stage main loop;
   // the other pairings (VEC_K needs 64-wide k rows) the generic BK 64 / 2-stage one
-  plan.dma_variant = ( plan.mode_a == LOAD_VEC_MN && plan.mode_b == LOAD_VEC_MN ) ? 1 : 0;
+  // (3: the persistent variant of the scheduled loop, for contractions it
+  // runs -- all tiles full, plain fp32 stores -- decided at launch)
+  plan.dma_variant = ( plan.mode_a == LOAD_VEC_MN && plan.mode_b == LOAD_VEC_MN ) ? 3 : 0;
   if( char const * l_env = std::getenv( "ETIR_DMA_VARIANT" ) ) {
-    // diagnostic override: 0 forces the generic BK 64 / 2-stage loop
-    if( std::atoi( l_env ) == 0 ) plan.dma_variant = 0;
+    // diagnostic override: 0 forces the generic BK 64 / 2-stage loop,
+    // 3 the persistent scheduled loop (VEC_MN x VEC_MN only)
+    int32_t const l_v = std::atoi( l_env );
+    if( l_v == 0 ) plan.dma_variant = 0;
+    if( l_v >= 1 && plan.dma_variant == 3 ) plan.dma_variant = l_v;
   }
+
   int64_t l_bm, l_bn;
   tile_shape( plan.tile, l_bm, l_bn );
 
@@ -673,6 +679,12 @@ int plan_contraction_impl( int64_t            num_loops,
   a.first_touch = ktype_first_touch;
   a.last_touch  = ktype_last_touch;
   a.out_bf16 = ( dtype_out == ETIR_BF16 ) ? 1 : 0;
+  // start-time stagger of the persistent direct-to-LDS kernel: 4 phases, 3
+  // units (~3 us) apart (measured on config 3; diagnostic override by env)
+  a.dma_phases = 4;
+  a.dma_stagger = 3;
+  if( char const * l_env = std::getenv( "ETIR_DMA_PHASES" ) ) a.dma_phases = std::atoi( l_env );
+  if( char const * l_env = std::getenv( "ETIR_DMA_STAGGER" ) ) a.dma_stagger = std::atoi( l_env );
   if( l_cpx ) {
     a.cpx_a   = l_x[0].s[l_sa];
     a.cpx_b   = l_x[0].s[l_sb];
@@ -683,6 +695,10 @@ int plan_contraction_impl( int64_t            num_loops,
     for( int64_t l_v : l_tm_out ) l_mo = std::max( l_mo, l_v );
     for( int64_t l_v : l_tn_out ) l_no = std::max( l_no, l_v );
     a.out_off32 = ( 4 * ( l_mo + l_no ) + 4 < ( int64_t( 1 ) << 32 ) ) ? 1 : 0;
+  }
+  if(    plan.tile == TILE_BF16_DMA_256x256 && plan.dma_variant == 3 && a.M % 256 == 0 && a.N % 256 == 0
+      && a.out_off32 && !a.out_bf16 && a.first_touch == ETIR_KTYPE_ZERO && a.last_touch == ETIR_KTYPE_UNDEFINED ) {
+    plan.desc += " persistent";
   }
   return ETIR_SUCCESS;
 }
@@ -780,6 +796,7 @@ int launch_contraction( ContractionPlan const & plan,
   };
   if( uintptr_t( a.a ) % align_of( l_ma ) != 0 ) l_ma = LOAD_SCALAR;
   if( uintptr_t( a.b ) % align_of( l_mb ) != 0 ) l_mb = LOAD_SCALAR;
+  int32_t l_dma_variant = plan.dma_variant;
   int32_t l_tile = plan.tile;
   if(    ( l_tile == TILE_BF16_DMA_256x256 || l_tile == TILE_BF16_DMA_256x128 )
       && ( l_ma != plan.mode_a || l_mb != plan.mode_b ) ) {
@@ -810,7 +827,7 @@ int launch_contraction( ContractionPlan const & plan,
     case TILE_CPX_F32_64x64: l_err = launch_contract_cpx( false, l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_CPX_F64_64x64: l_err = launch_contract_cpx( true, l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_BF16_DMA_256x256:
-      l_err = launch_contract_bf16_dma( l_ma, l_mb, plan.dma_variant, a, l_g, stream );
+      l_err = launch_contract_bf16_dma( l_ma, l_mb, l_dma_variant, a, l_g, stream );
       break;
     case TILE_BF16_DMA_256x128:
       l_err = launch_contract_bf16_dma( l_ma, l_mb, 2, a, l_g, stream );

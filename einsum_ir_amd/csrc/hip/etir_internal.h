@@ -177,6 +177,9 @@ struct ContractArgs {
   int32_t c_inner;        // workgroup ids walk C fastest (the output's unit-stride dim is a C dim)
   // complex contractions: element offsets of the imaginary parts (A, B, out)
   int64_t cpx_a, cpx_b, cpx_out;
+  // persistent direct-to-LDS kernel: start-time stagger, dma_phases groups of
+  // workgroups, group p starts p * dma_stagger sleep units (~1 us) late
+  int32_t dma_phases, dma_stagger;
 };
 
 struct ContractionPlan {
@@ -192,7 +195,8 @@ struct ContractionPlan {
   int32_t mode_b = LOAD_SCALAR;
   int32_t tile = TILE_F32_128x128;
   int32_t tile_fallback = TILE_BF16_256x128;  // used when the DMA kernel's alignment needs fail at launch
-  int32_t dma_variant = 0;                    // 0: BK 64, 2 stages; 1: BK 32, 4 stages, scheduled (VEC_MN x VEC_MN)
+  int32_t dma_variant = 0;                    // 0: BK 64, 2 stages; 1: BK 32, 4 stages, scheduled (VEC_MN x VEC_MN);
+                                              // 3: its persistent variant where eligible (else 1)
   int64_t flops = 0;
   int64_t bytes = 0;
   // fused loops per kernel role (outer -> inner) for diagnostics

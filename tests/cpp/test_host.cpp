@@ -334,6 +334,58 @@ TEST( memory_arena_two_sided_stack ) {
   l_mm.remove_reservation( l_d );
 }
 
+// host stand-ins for the arena allocator, counting live allocations
+static int g_live_allocs = 0;
+static int host_alloc( void ** o_ptr, int64_t i_bytes ) {
+  *o_ptr = std::malloc( std::size_t( i_bytes ) );
+  if( *o_ptr != nullptr ) g_live_allocs++;
+  return *o_ptr == nullptr;
+}
+static int host_free( void * i_ptr ) {
+  std::free( i_ptr );
+  g_live_allocs--;
+  return 0;
+}
+
+TEST( memory_arena_grows_with_a_later_plan ) {
+  {
+    backend::MemoryManager l_mm;
+    l_mm.set_allocator( host_alloc, host_free );
+    // first plan: peak 1024 + 512
+    l_mm.m_layer_id = 0;
+    int64_t l_a = l_mm.reserve_memory( 1024 );
+    l_mm.m_layer_id = 1;
+    int64_t l_b = l_mm.reserve_memory( 512 );
+    CHECK( l_mm.alloc_all_memory() == err_t::SUCCESS );
+    CHECK( l_mm.get_allocated_memory() == 1536 && l_mm.get_required_memory() == 1536 );
+    char * l_base = static_cast< char * >( l_mm.get_mem_ptr( l_a ) );
+    CHECK( static_cast< char * >( l_mm.get_mem_ptr( l_b ) ) == l_base + 1024 );
+    l_mm.remove_reservation( l_a );
+    l_mm.remove_reservation( l_b );
+    // second plan on the same manager with a larger peak: every pointer it
+    // hands out must stay inside the (grown) allocation
+    l_mm.m_layer_id = 0;
+    int64_t l_c = l_mm.reserve_memory( 4096 );
+    l_mm.m_layer_id = 1;
+    int64_t l_d = l_mm.reserve_memory( 2048 );
+    CHECK( l_mm.get_required_memory() == 6144 );
+    CHECK( l_mm.alloc_all_memory() == err_t::SUCCESS );
+    CHECK( l_mm.get_allocated_memory() >= l_mm.get_required_memory() );
+    CHECK( g_live_allocs == 1 );
+    char * l_lo = static_cast< char * >( l_mm.get_mem_ptr( l_c ) );
+    char * l_hi = static_cast< char * >( l_mm.get_mem_ptr( l_d ) );
+    CHECK( l_hi - l_lo == 4096 );
+    CHECK( l_hi + 2048 - l_lo <= l_mm.get_allocated_memory() );
+    // a smaller plan afterwards keeps the allocation
+    l_mm.remove_reservation( l_c );
+    l_mm.remove_reservation( l_d );
+    l_mm.m_layer_id = 0;
+    l_mm.reserve_memory( 256 );
+    CHECK( l_mm.alloc_all_memory() == err_t::SUCCESS && g_live_allocs == 1 );
+  }
+  CHECK( g_live_allocs == 0 );
+}
+
 int main() {
   for( Case const & l_c : cases() ) {
     int const l_before = g_failures;

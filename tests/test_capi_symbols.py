@@ -9,6 +9,7 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADERS = {
     "einsum_ir_hip.h": os.path.join(ROOT, "einsum_ir_amd", "libeinsum_ir_hip.so"),
+    "einsum_ir.h": os.path.join(ROOT, "einsum_ir_amd", "libeinsum_ir.so"),
 }
 
 
@@ -22,7 +23,7 @@ def declared_functions(header):
 def test_library_exports_every_declared_symbol(header):
     lib = ctypes.CDLL(HEADERS[header])
     names = declared_functions(header)
-    assert names, "no declarations found"
+    assert len(names) >= 10, f"only {len(names)} declarations found in {header}"
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, f"{HEADERS[header]} lacks {missing}"
 

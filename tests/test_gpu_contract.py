@@ -83,8 +83,17 @@ def test_c3_scaled_bf16(torch_cuda, oracle):
     assert "vec_mn" in desc
 
 
-def test_c3_full_size_spot_check(torch_cuda, oracle):
-    """BASELINE config 3 at full size: 4096 sampled outputs against fp64 dot products."""
+def test_c3_full_size_every_output(torch_cuda, oracle):
+    """BASELINE config 3 at full size, every one of the 134M outputs checked.
+
+    The output starts as NaN, so an element no tile writes fails.  Two fp64
+    invariants over all outputs catch a tile, row or column written to the
+    wrong place or with the wrong operands:
+      sum_n out[z,a,b,m,n] = sum_k A[z,a,k,m] * (sum_n B[z,b,k,n])
+      sum_m out[z,a,b,m,n] = sum_k (sum_m A[z,a,k,m]) * B[z,b,k,n]
+    each compared element by element (deviation <= 1e-4 of the invariant's
+    RMS; the fp32 accumulation error is ~1e-6 of it, one misplaced row ~1).
+    4096 sampled outputs are also checked against fp64 dot products."""
     torch = torch_cuda
     sizes = dict(z=8, a=64, m=64, b=64, n=64, k=1024)
     loops = loops_for("zakm,zbkn->zabmn", sizes)
@@ -94,19 +103,39 @@ def test_c3_full_size_spot_check(torch_cuda, oracle):
     plan = eir.ContractionPlan(loops["dim_types"], loops["sizes"], loops["strides_left"],
                                loops["strides_right"], loops["strides_out"], dtype_left=eir.BF16,
                                dtype_right=eir.BF16)
-    out = torch.empty(8 * 64 * 64 * 64 * 64, dtype=torch.float32, device="cuda")
+    assert "bf16_dma_256x256" in plan.describe()
+    out = torch.full((8 * 64 * 64 * 64 * 64,), float("nan"), dtype=torch.float32, device="cuda")
     plan.execute(_dev(torch, a), _dev(torch, b), out, stream=torch.cuda.current_stream())
     torch.cuda.synchronize()
     plan.close()
     got = out.cpu().numpy().reshape(8, 64, 64, 64, 64)
+    del out
+    assert np.all(np.isfinite(got)), "unwritten or non-finite outputs"
     A = oracle.bf16_to_f32(a).reshape(8, 64, 1024, 64).astype(np.float64)
     B = oracle.bf16_to_f32(b).reshape(8, 64, 1024, 64).astype(np.float64)
+
+    def check(inv_got, inv_ref, what):
+        dev = np.abs(inv_got - inv_ref)
+        scale = np.sqrt(np.mean(inv_ref ** 2))
+        worst = np.unravel_index(np.argmax(dev), dev.shape)
+        assert dev[worst] <= 1e-4 * scale, f"{what}: deviation {dev[worst]:.3e} at {worst} (RMS {scale:.3e})"
+
+    # sum over n: [z,a,b,m]
+    bs = B.sum(axis=3)                                        # [z,b,k]
+    ref_n = np.einsum("zakm,zbk->zabm", A, bs, optimize=True)
+    check(got.sum(axis=4, dtype=np.float64), ref_n, "sum over n")
+    del ref_n, bs
+    # sum over m: [z,a,b,n]
+    as_ = A.sum(axis=3)                                       # [z,a,k]
+    ref_m = np.einsum("zak,zbkn->zabn", as_, B, optimize=True)
+    check(got.sum(axis=3, dtype=np.float64), ref_m, "sum over m")
+    del ref_m, as_
+
     idx = [rng.integers(0, s, 4096) for s in (8, 64, 64, 64, 64)]
     z, ia, ib, im, inn = idx
     ref = np.einsum("sk,sk->s", A[z, ia, :, im], B[z, ib, :, inn])
     g = got[z, ia, ib, im, inn]
     assert rel_frobenius(ref, g) <= TOL_BF16
-    assert np.all(np.isfinite(got))
 
 
 def test_mlp_layer_fp32(torch_cuda, oracle):

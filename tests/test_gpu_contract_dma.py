@@ -65,3 +65,40 @@ def test_dma_is_the_default_for_c3(torch_cuda):
     desc = plan.describe()
     plan.close()
     assert "bf16_dma_256x256" in desc, desc
+
+
+PERSISTENT_SHAPES = [
+    # fewer tiles than CUs, not a multiple of 8: one tile per workgroup, plain tile order
+    ("km,kn->mn", dict(k=136, m=512, n=768)),
+    ("zakm,zbkn->zabmn", dict(z=3, a=4, m=64, b=8, n=64, k=72)),
+    # 320 tiles over 256 workgroups (XCD ranges of 40 tiles, 32 workgroups
+    # each: some workgroups run two tiles), K not a multiple of the k step
+    ("zkm,zkn->zmn", dict(z=5, k=40, m=2048, n=2048)),
+]
+
+
+@pytest.mark.parametrize("expr,sizes", PERSISTENT_SHAPES)
+def test_dma_persistent(torch_cuda, oracle, monkeypatch, expr, sizes):
+    """The persistent variant (default for VEC_MN x VEC_MN with all tiles
+    full, ZERO first touch, no last touch) against the oracle, and bit for bit
+    against the one-tile-per-workgroup kernel: both sum each output in the
+    same order, so any tile placed or walked wrongly shows up exactly."""
+    monkeypatch.setenv("ETIR_TILE", "7")
+    monkeypatch.delenv("ETIR_DMA_VARIANT", raising=False)
+    got_p, desc = run_case(torch_cuda, oracle, expr, sizes, dtype=eir.BF16, seed=23)
+    assert "bf16_dma_256x256" in desc and "persistent" in desc, desc
+    monkeypatch.setenv("ETIR_DMA_VARIANT", "1")
+    got_1, desc1 = run_case(torch_cuda, oracle, expr, sizes, dtype=eir.BF16, seed=23, check=False)
+    assert "persistent" not in desc1, desc1
+    assert (got_p == got_1).all(), "persistent and one-tile-per-workgroup kernels differ"
+
+
+@pytest.mark.parametrize("phases,stagger", [("1", "0"), ("8", "2")])
+def test_dma_persistent_stagger(torch_cuda, oracle, monkeypatch, phases, stagger):
+    """Start stagger settings other than the default do not change results."""
+    monkeypatch.setenv("ETIR_TILE", "7")
+    monkeypatch.setenv("ETIR_DMA_PHASES", phases)
+    monkeypatch.setenv("ETIR_DMA_STAGGER", stagger)
+    _, desc = run_case(torch_cuda, oracle, "zkm,zkn->zmn", dict(z=2, k=64, m=512, n=1024), dtype=eir.BF16,
+                       seed=29)
+    assert "persistent" in desc, desc
