@@ -182,6 +182,19 @@ void tile_shape( int32_t t, int64_t & bm, int64_t & bn ) {
 
 namespace {
 
+// next 256-byte aligned piece of the caller's region, or a clear error
+int place_take( DevicePlacement & place, std::size_t bytes, void ** out, char const * what ) {
+  std::size_t const l_start = ( place.used + 255 ) & ~std::size_t( 255 );
+  if( l_start + bytes > place.capacity ) {
+    return fail( ETIR_UNDEFINED_ERROR, std::string( "contraction: the " ) + what + " need "
+                                        + std::to_string( l_start + bytes ) + " bytes of scratch, more than the "
+                                        + std::to_string( place.capacity ) + " the allocation-free entry point has" );
+  }
+  *out = place.base + l_start;
+  place.used = l_start + bytes;
+  return ETIR_SUCCESS;
+}
+
 int plan_contraction_impl( int64_t            num_loops,
                            int32_t const    * dim_types,
                            int64_t const    * sizes,
@@ -197,8 +210,10 @@ int plan_contraction_impl( int64_t            num_loops,
                            int32_t            ktype_main,
                            int32_t            ktype_last_touch,
                            bool               allow_split,
-                           ContractionPlan  & plan ) {
+                           ContractionPlan  & plan,
+                           DevicePlacement  * place ) {
   plan = ContractionPlan();
+  plan.placed = ( place != nullptr );
 
   // ---------------------------------------------------------------- checks
   bool const l_f32  = dtype_left == ETIR_FP32 && dtype_right == ETIR_FP32
@@ -544,17 +559,26 @@ int plan_contraction_impl( int64_t            num_loops,
         int l_err = plan_contraction_impl( (int64_t) l_pt.size(), l_pt.data(), l_psz.data(), l_pl.data(),
                                            l_pr.data(), l_pa.data(), l_po.data(), dtype_left, dtype_right,
                                            ETIR_FP32, ETIR_FP32, ETIR_KTYPE_ZERO, ETIR_KTYPE_MADD,
-                                           ETIR_KTYPE_UNDEFINED, false, *l_part );
+                                           ETIR_KTYPE_UNDEFINED, false, *l_part, place );
         if( l_err != ETIR_SUCCESS ) {
           release_contraction( *l_part );
           return l_err;
         }
-        hipError_t l_he = hipMalloc( &plan.d_ws, (std::size_t) l_ws_bytes );
-        if( l_he != hipSuccess ) {
-          plan.d_ws = nullptr;
-          release_contraction( *l_part );
-          return fail( ETIR_UNDEFINED_ERROR, std::string( "contraction: workspace allocation failed: " )
-                                             + hipGetErrorString( l_he ) );
+        if( place != nullptr ) {
+          l_err = place_take( *place, (std::size_t) l_ws_bytes, &plan.d_ws, "split-K workspace" );
+          if( l_err != ETIR_SUCCESS ) {
+            release_contraction( *l_part );
+            return l_err;
+          }
+        }
+        else {
+          hipError_t l_he = hipMalloc( &plan.d_ws, (std::size_t) l_ws_bytes );
+          if( l_he != hipSuccess ) {
+            plan.d_ws = nullptr;
+            release_contraction( *l_part );
+            return fail( ETIR_UNDEFINED_ERROR, std::string( "contraction: workspace allocation failed: " )
+                                               + hipGetErrorString( l_he ) );
+          }
         }
         plan.split    = (int32_t) l_sf;
         plan.out_span = l_span;
@@ -624,16 +648,65 @@ int plan_contraction_impl( int64_t            num_loops,
   std::size_t const l_bytes64 = l_c64.size() * sizeof( int64_t );
   std::size_t const l_bytes32 = l_t32.size() * sizeof( int32_t );
   std::size_t const l_total = l_bytes64 + l_bytes32 + 256;
-  ETIR_HIP_CHECK( hipMalloc( &plan.d_tables, l_total ) );
-  char * l_base = reinterpret_cast< char * >( plan.d_tables );
-  hipError_t l_e1 = hipMemcpy( l_base, l_c64.data(), l_bytes64, hipMemcpyHostToDevice );
-  hipError_t l_e2 = l_bytes32 > 0
-                  ? hipMemcpy( l_base + l_bytes64, l_t32.data(), l_bytes32, hipMemcpyHostToDevice )
-                  : hipSuccess;
-  if( l_e1 != hipSuccess || l_e2 != hipSuccess ) {
-    (void) hipFree( plan.d_tables );
-    plan.d_tables = nullptr;
-    return fail( ETIR_UNDEFINED_ERROR, "contraction: copying offset tables to the device failed" );
+  char * l_base = nullptr;
+  if( place != nullptr ) {
+    // caller's region: the tables are generated there by a kernel from the
+    // same loops (and slots) the host enumerated them from above
+    int l_err = place_take( *place, l_total, &plan.d_tables, "offset tables" );
+    if( l_err != ETIR_SUCCESS ) return l_err;
+    l_base = reinterpret_cast< char * >( plan.d_tables );
+    int64_t const l_b = int64_t( l_base - place->base );
+    int64_t const l_o32 = l_b + int64_t( l_bytes64 );
+    auto fill = [&]( std::vector< Loop > const & dims, std::initializer_list< int > slots,
+                     std::initializer_list< int64_t > dst, bool is64 ) -> int {
+      if( (int) dims.size() > kFillMaxDims ) {
+        return fail( ETIR_COMPILATION_FAILED, "contraction: too many fused loops of one type for the "
+                                              "allocation-free entry point" );
+      }
+      TableFill l_f{};
+      l_f.count = 1;
+      for( Loop const & l_x : dims ) l_f.count *= l_x.size;
+      l_f.ndims = (int32_t) dims.size();
+      l_f.ntab = (int32_t) slots.size();
+      l_f.is64 = is64 ? 1 : 0;
+      for( int l_d = 0; l_d < l_f.ndims; l_d++ ) l_f.sizes[l_d] = dims[l_d].size;
+      int l_t = 0;
+      for( int l_sl : slots ) {
+        for( int l_d = 0; l_d < l_f.ndims; l_d++ ) l_f.strides[l_t][l_d] = dims[l_d].s[l_sl];
+        l_t++;
+      }
+      l_t = 0;
+      for( int64_t l_o : dst ) l_f.dst[l_t++] = l_o;
+      if( l_f.count == 0 ) return ETIR_SUCCESS;
+      return launch_fill_tables( l_f, place->base, place->stream );
+    };
+    int64_t const l_cs = int64_t( sizeof( int64_t ) ) * l_size_c;
+    int l_err2 = fill( l_c, { l_sa, l_sb, T_AUX, T_OUT }, { l_b, l_b + l_cs, l_b + 2 * l_cs, l_b + 3 * l_cs }, true );
+    if( l_err2 == ETIR_SUCCESS ) {
+      l_err2 = fill( l_km, { l_sa, T_AUX, T_OUT }, { l_o32 + 4 * int64_t( l_o_tm_a ), l_o32 + 4 * int64_t( l_o_tm_x ),
+                                                    l_o32 + 4 * int64_t( l_o_tm_o ) }, false );
+    }
+    if( l_err2 == ETIR_SUCCESS ) {
+      l_err2 = fill( l_kn, { l_sb, T_AUX, T_OUT }, { l_o32 + 4 * int64_t( l_o_tn_b ), l_o32 + 4 * int64_t( l_o_tn_x ),
+                                                    l_o32 + 4 * int64_t( l_o_tn_o ) }, false );
+    }
+    if( l_err2 == ETIR_SUCCESS ) {
+      l_err2 = fill( l_k, { l_sa, l_sb }, { l_o32 + 4 * int64_t( l_o_tk_a ), l_o32 + 4 * int64_t( l_o_tk_b ) }, false );
+    }
+    if( l_err2 != ETIR_SUCCESS ) return l_err2;
+  }
+  else {
+    ETIR_HIP_CHECK( hipMalloc( &plan.d_tables, l_total ) );
+    l_base = reinterpret_cast< char * >( plan.d_tables );
+    hipError_t l_e1 = hipMemcpy( l_base, l_c64.data(), l_bytes64, hipMemcpyHostToDevice );
+    hipError_t l_e2 = l_bytes32 > 0
+                    ? hipMemcpy( l_base + l_bytes64, l_t32.data(), l_bytes32, hipMemcpyHostToDevice )
+                    : hipSuccess;
+    if( l_e1 != hipSuccess || l_e2 != hipSuccess ) {
+      (void) hipFree( plan.d_tables );
+      plan.d_tables = nullptr;
+      return fail( ETIR_UNDEFINED_ERROR, "contraction: copying offset tables to the device failed" );
+    }
   }
 
   ContractArgs & a = plan.args;
@@ -719,16 +792,17 @@ int plan_contraction( int64_t            num_loops,
                       int32_t            ktype_first_touch,
                       int32_t            ktype_main,
                       int32_t            ktype_last_touch,
-                      ContractionPlan  & plan ) {
+                      ContractionPlan  & plan,
+                      DevicePlacement  * place ) {
   return plan_contraction_impl( num_loops, dim_types, sizes, strides_left, strides_right, strides_out_aux,
                                 strides_out, dtype_left, dtype_right, dtype_comp, dtype_out,
                                 ktype_first_touch, ktype_main, ktype_last_touch,
-                                std::getenv( "ETIR_NO_SPLIT_K" ) == nullptr, plan );
+                                std::getenv( "ETIR_NO_SPLIT_K" ) == nullptr, plan, place );
 }
 
 void release_contraction( ContractionPlan & plan ) {
-  if( plan.d_tables != nullptr ) (void) hipFree( plan.d_tables );
-  if( plan.d_ws != nullptr ) (void) hipFree( plan.d_ws );
+  if( !plan.placed && plan.d_tables != nullptr ) (void) hipFree( plan.d_tables );
+  if( !plan.placed && plan.d_ws != nullptr ) (void) hipFree( plan.d_ws );
   plan.d_tables = nullptr;
   plan.d_ws = nullptr;
   if( plan.partial ) {

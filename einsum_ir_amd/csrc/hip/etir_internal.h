@@ -212,7 +212,38 @@ struct ContractionPlan {
   int64_t out_span = 0;
   void *  d_ws = nullptr;
   std::shared_ptr< ContractionPlan > partial;
+  // tables and workspace live in a caller's region (DevicePlacement), not in
+  // memory the plan allocated and frees
+  bool    placed = false;
 };
+
+// Where a plan's device memory comes from when it may not allocate: a
+// region the caller provides (the scratch array of the allocation-free entry
+// point), handed out front to back in 256-byte aligned pieces.  The offset
+// tables are then written by a kernel on `stream` from the loop sizes and
+// strides (no host-to-device copy).
+struct DevicePlacement {
+  char *      base     = nullptr;
+  std::size_t capacity = 0;
+  std::size_t used     = 0;
+  hipStream_t stream   = nullptr;
+};
+
+// One group of offset tables over the same loops (outer -> inner): entry e
+// of table t is sum_d digit_d(e) * strides[t][d], the mixed-radix digits of e
+// with the innermost loop fastest.  Written as int64 (is64) or int32 at byte
+// offset dst[t] from the region's base.
+constexpr int kFillMaxDims = 16;
+struct TableFill {
+  int64_t count;
+  int64_t dst[4];
+  int64_t sizes[kFillMaxDims];
+  int64_t strides[4][kFillMaxDims];
+  int32_t ndims;
+  int32_t ntab;
+  int32_t is64;
+};
+int launch_fill_tables( TableFill const & f, char * base, hipStream_t stream );
 
 // frees the device memory of a contraction plan (tables, workspace, partial plan)
 void release_contraction( ContractionPlan & plan );
@@ -250,7 +281,8 @@ int  plan_contraction( int64_t            num_loops,
                        int32_t            ktype_first_touch,
                        int32_t            ktype_main,
                        int32_t            ktype_last_touch,
-                       ContractionPlan  & plan );
+                       ContractionPlan  & plan,
+                       DevicePlacement  * place = nullptr );
 int  launch_contraction( ContractionPlan const & plan,
                          void const            * left,
                          void const            * right,

@@ -132,6 +132,38 @@ int etir_hip_contraction_execute( etir_plan_t  plan,
                                   void       * stream );
 
 /*
+ * Plans and executes one contraction without allocating device memory: the
+ * arguments of etir_hip_contraction_create followed by those of
+ * etir_hip_contraction_execute, with the same results.  No counterpart in
+ * the reference: it is for callers that cannot allocate (code under stream
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * offset tables and any split-K workspace live in a fixed 64 MiB device
+ * array per GPU (held until the process ends); a contraction that needs more
+ * fails with an error naming both sizes.  All calls on one GPU share that
+ * array: calls that overlap on one GPU (other streams, other host threads)
+ * race.  Enqueued on `stream`; no host synchronisation.
+ */
+int etir_hip_contraction_execute_noalloc( int64_t         num_loops,
+                                          int32_t const * dim_types,
+                                          int64_t const * sizes,
+                                          int64_t const * strides_left,
+                                          int64_t const * strides_right,
+                                          int64_t const * strides_out_aux,
+                                          int64_t const * strides_out,
+                                          int32_t         dtype_left,
+                                          int32_t         dtype_right,
+                                          int32_t         dtype_comp,
+                                          int32_t         dtype_out,
+                                          int32_t         ktype_first_touch,
+                                          int32_t         ktype_main,
+                                          int32_t         ktype_last_touch,
+                                          void const    * left,
+                                          void const    * right,
+                                          void const    * out_aux,
+                                          void          * out,
+                                          void          * stream );
+
+/*
  * Creates a permutation plan (the unary COPY/ZERO/ADD operator).
  * Replaces
  *   UnaryTpp::compile                  (reference src/backend/UnaryTpp.cpp:4-50)
