@@ -51,6 +51,8 @@ int launch_contract_bf16_64x64( int32_t ma, int32_t mb, bool kaff, ContractArgs 
                                 uint32_t grid, hipStream_t stream );
 int launch_contract_bf16_dma( int32_t ma, int32_t mb, int32_t variant, ContractArgs const & a,
                               uint32_t grid, hipStream_t stream );
+int launch_contract_kwave( int32_t waves, int32_t kw, ContractArgs const & a, uint32_t grid,
+                           hipStream_t stream );
 
 namespace {
 
@@ -161,6 +163,7 @@ char const * tile_str( int32_t t ) {
     case TILE_F64_64x64:    return "f64_64x64x16";
     case TILE_CPX_F32_64x64: return "cpx_f32_64x64x16";
     case TILE_CPX_F64_64x64: return "cpx_f64_64x64x16";
+    case TILE_F32_KWAVE_32x32: return "f32_kwave_32x32";
     default:                return "?";
   }
 }
@@ -173,6 +176,7 @@ void tile_shape( int32_t t, int64_t & bm, int64_t & bn ) {
     case TILE_BF16_256x128: bm = 256; bn = 128; break;
     case TILE_BF16_DMA_256x256: bm = 256; bn = 256; break;
     case TILE_BF16_DMA_256x128: bm = 256; bn = 128; break;
+    case TILE_F32_KWAVE_32x32: bm = 32; bn = 32; break;
     case TILE_BF16_128x128: bm = 128; bn = 128; break;
     default:                bm = 64;  bn = 64;  break;
   }
@@ -484,12 +488,40 @@ int plan_contraction_impl( int64_t            num_loops,
   int64_t l_bm, l_bn;
   tile_shape( plan.tile, l_bm, l_bn );
 
+  // --------------------------------------------- K split inside a workgroup
+  // Few output tiles, both operands K-contiguous fp32, K up to 4096: 32 x 32
+  // tiles (4x the workgroups of 64 x 64) with K divided over the 16 waves of
+  // each workgroup, whose partial tiles are added in LDS -- one launch, no
+  // workspace (the alternative below, split K, sends S partial outputs
+  // through memory to a second kernel)
+  {
+    int64_t const l_t32 = n_tiles( TILE_F32_KWAVE_32x32 );
+    bool const l_kw_ok = l_f32 && plan.mode_a == LOAD_VEC_K && plan.mode_b == LOAD_VEC_K && l_k_affine
+                      && l_sk_a == 1 && l_sk_b == 1 && l_size_k % 16 == 0 && l_size_k >= 256
+                      && l_size_k <= 4096 && n_tiles( plan.tile ) < l_cus && l_t32 >= l_cus / 2
+                      && std::getenv( "ETIR_NO_KWAVE" ) == nullptr;
+    if( l_kw_ok ) {
+      // 16 waves (4 per SIMD) measured fastest for K = 256 .. 1024 (config 1:
+      // 7.4 us against 8.0 with 8 waves and 9.0 with 4)
+      int32_t l_w = 16;
+      if( char const * l_env = std::getenv( "ETIR_KWAVE_WAVES" ) ) {
+        int32_t const l_v = std::atoi( l_env );
+        if( l_v == 4 || l_v == 8 || l_v == 16 ) l_w = l_v;
+      }
+      plan.tile = TILE_F32_KWAVE_32x32;
+      plan.tile_fallback = TILE_F32_64x64;
+      plan.kwave_waves = l_w;
+      plan.kwave_kw = (int32_t) ( ( ( l_size_k + l_w - 1 ) / l_w + 15 ) / 16 * 16 );
+      tile_shape( plan.tile, l_bm, l_bn );
+    }
+  }
+
   // ------------------------------------------------------------- split K
   // Few output tiles and a long K leave most CUs idle (e.g. an einsum-tree
   // node with M = 64, N = 1024, K = 32768).  Then the outermost K loops (one
   // of them factored if needed) become C loops of a partial contraction that
   // writes one workspace slice per split, and split_reduce sums the slices.
-  if( allow_split && !l_f64 && !l_cpx && l_size_k >= 512 ) {
+  if( allow_split && !l_f64 && !l_cpx && l_size_k >= 512 && plan.tile != TILE_F32_KWAVE_32x32 ) {
     int64_t const l_tiles = n_tiles( plan.tile );
     if( l_tiles > 0 && l_tiles < l_cus ) {
       // at least 128 k per split; aim for two workgroups per CU
@@ -758,6 +790,17 @@ int plan_contraction_impl( int64_t            num_loops,
   a.dma_stagger = 3;
   if( char const * l_env = std::getenv( "ETIR_DMA_PHASES" ) ) a.dma_phases = std::atoi( l_env );
   if( char const * l_env = std::getenv( "ETIR_DMA_STAGGER" ) ) a.dma_stagger = std::atoi( l_env );
+  auto affine_stride = []( std::vector< int64_t > const & t ) -> int32_t {
+    int64_t const l_st = t.size() > 1 ? t[1] : 0;
+    for( std::size_t l_i = 0; l_i < t.size(); l_i++ ) {
+      if( t[l_i] != int64_t( l_i ) * l_st ) return -1;
+    }
+    return ( l_st >= 0 && l_st <= std::numeric_limits< int32_t >::max() ) ? int32_t( l_st ) : -1;
+  };
+  a.sm_a   = affine_stride( l_tm_a );
+  a.sn_b   = affine_stride( l_tn_b );
+  a.sm_out = affine_stride( l_tm_out );
+  a.sn_out = affine_stride( l_tn_out );
   if( l_cpx ) {
     a.cpx_a   = l_x[0].s[l_sa];
     a.cpx_b   = l_x[0].s[l_sb];
@@ -872,7 +915,7 @@ int launch_contraction( ContractionPlan const & plan,
   if( uintptr_t( a.b ) % align_of( l_mb ) != 0 ) l_mb = LOAD_SCALAR;
   int32_t l_dma_variant = plan.dma_variant;
   int32_t l_tile = plan.tile;
-  if(    ( l_tile == TILE_BF16_DMA_256x256 || l_tile == TILE_BF16_DMA_256x128 )
+  if(    ( l_tile == TILE_BF16_DMA_256x256 || l_tile == TILE_BF16_DMA_256x128 || l_tile == TILE_F32_KWAVE_32x32 )
       && ( l_ma != plan.mode_a || l_mb != plan.mode_b ) ) {
     // the DMA kernel needs the 16-byte vector modes: use the register-staged
     // kernel with its own tile grid
@@ -900,6 +943,9 @@ int launch_contraction( ContractionPlan const & plan,
     case TILE_F64_64x64:    l_err = launch_contract_f64_64x64( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_CPX_F32_64x64: l_err = launch_contract_cpx( false, l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_CPX_F64_64x64: l_err = launch_contract_cpx( true, l_ma, l_mb, l_kaff, a, l_g, stream ); break;
+    case TILE_F32_KWAVE_32x32:
+      l_err = launch_contract_kwave( plan.kwave_waves, plan.kwave_kw, a, l_g, stream );
+      break;
     case TILE_BF16_DMA_256x256:
       l_err = launch_contract_bf16_dma( l_ma, l_mb, l_dma_variant, a, l_g, stream );
       break;

@@ -142,7 +142,8 @@ enum TileCfg : int32_t {
   TILE_BF16_DMA_256x256 = 7,  // direct-to-LDS kernel (contract_dma.h), one workgroup per CU
   TILE_BF16_DMA_256x128 = 8,  // direct-to-LDS kernel, two workgroups per CU
   TILE_CPX_F32_64x64    = 9,  // complex (CPX_MADD) kernels, contract_cpx.hip
-  TILE_CPX_F64_64x64    = 10
+  TILE_CPX_F64_64x64    = 10,
+  TILE_F32_KWAVE_32x32  = 11  // K split over the waves of one workgroup (contract_kwave.hip)
 };
 
 struct ContractArgs {
@@ -177,6 +178,9 @@ struct ContractArgs {
   int32_t c_inner;        // workgroup ids walk C fastest (the output's unit-stride dim is a C dim)
   // complex contractions: element offsets of the imaginary parts (A, B, out)
   int64_t cpx_a, cpx_b, cpx_out;
+  // affine row tables (tm_a[i] == i * sm_a etc.; -1: not affine), used by
+  // kernels that skip the table reads when they can
+  int32_t sm_a, sn_b, sm_out, sn_out;
   // persistent direct-to-LDS kernel: start-time stagger, dma_phases groups of
   // workgroups, group p starts p * dma_stagger sleep units (~1 us) late
   int32_t dma_phases, dma_stagger;
@@ -195,6 +199,8 @@ struct ContractionPlan {
   int32_t mode_b = LOAD_SCALAR;
   int32_t tile = TILE_F32_128x128;
   int32_t tile_fallback = TILE_BF16_256x128;  // used when the DMA kernel's alignment needs fail at launch
+  int32_t kwave_waves = 0;                    // TILE_F32_KWAVE_32x32: waves per workgroup and k per wave
+  int32_t kwave_kw = 0;
   int32_t dma_variant = 0;                    // 0: BK 64, 2 stages; 1: BK 32, 4 stages, scheduled (VEC_MN x VEC_MN);
                                               // 3: its persistent variant where eligible (else 1)
   int64_t flops = 0;

@@ -72,8 +72,8 @@ def _run_both(torch, expr, sizes, dtype=eir.FP32, seed=0):
 
 def test_noalloc_two_calls_match_allocating_path(torch_cuda):
     torch = torch_cuda
-    # 1: BASELINE config 1 at full size (split-K: 4 MB of partial sums in the scratch array)
-    ref1, got1, desc1, _ = _run_both(torch, "abkl,cdkl->abcd", dict(a=32, b=16, c=32, d=16, k=32, l=16), seed=1)
+    # 1: few output tiles and a long K (split-K: 8 MB of partial sums in the scratch array)
+    ref1, got1, desc1, _ = _run_both(torch, "mk,kn->mn", dict(m=64, k=8192, n=512), seed=1)
     assert "split-K" in desc1, desc1
     assert np.array_equal(ref1, got1), "first call differs from the allocating path"
     # 2: a smaller split-K contraction over the same scratch (other tables, fewer slices)
