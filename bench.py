@@ -148,19 +148,24 @@ def bench_permutes_4d(torch, eir, stream):
     """Config 2's permutation kind over other 4-D shapes (fp32 COPY, 16.8-31.9 M
     elements, unit-stride dims from 8 to 512 wide): GB/s per shape."""
     rows = []
+    # one input and one output buffer for all shapes: every shape runs on
+    # memory the process already uses (freshly mapped pages are slower for
+    # the first hundreds of launches, which the timed region would catch)
+    n_max = max(s[0] * s[1] * s[2] * s[3] for _, s in PERMUTES_4D)
+    x_all = torch.rand(n_max, device="cuda")
+    y_all = torch.empty_like(x_all)
     for expr, shape in PERMUTES_4D:
         sizes = dict(zip("abcd", shape))
         u = eir.unary_dims(expr, sizes)
         n = shape[0] * shape[1] * shape[2] * shape[3]
-        x = torch.rand(n, device="cuda")
-        y = torch.empty_like(x)
+        x = x_all[:n]
+        y = y_all[:n]
         plan = eir.PermutePlan(u["sizes"], u["strides_in"], u["strides_out"], dtype=eir.FP32, ktype=eir.COPY)
-        _, per = time_launches(torch, stream, lambda: plan.execute(x, y, stream=stream), 20, 3)
+        _, per = time_launches(torch, stream, lambda: plan.execute(x, y, stream=stream), 20, 10)
         gbs = 8 * n / per * 1e-9
         rows.append(dict(expr=expr, sizes=list(shape), gbs=round(gbs, 1), frac_hbm_peak=round(gbs / PEAK_HBM_GBS, 4),
                          kernel=plan.describe().split(" dims")[0]))
         plan.close()
-        del x, y
     return rows
 
 

@@ -139,7 +139,7 @@ int etir_hip_plan_describe( etir_plan_t plan, char * buf, int64_t len ) {
     l_s = plan->cont.desc;
   }
   else {
-    static char const * l_modes[] = { "fill", "transpose", "copy_vec", "gather", "tiled" };
+    static char const * l_modes[] = { "fill", "transpose", "copy_vec", "gather", "tiled", "reg4" };
     etir::PermutePlan const & p = plan->perm;
     char l_tmp[256];
     std::snprintf( l_tmp, sizeof( l_tmp ), "permute %s dims=%d elems=%lld vec=%d",
@@ -151,6 +151,10 @@ int etir_hip_plan_describe( etir_plan_t plan, char * buf, int64_t len ) {
         l_s += ( l_k ? "," : "" ) + std::to_string( p.args.tile_ext[l_k] );
       }
       l_s += "] pad=" + std::to_string( p.args.tile_pad );
+    }
+    if( p.mode == etir::PermMode::REG4 ) {
+      l_s += " i=" + std::to_string( p.args.size_i ) + " o=" + std::to_string( p.args.size_o )
+           + " c=" + std::to_string( p.args.c_size ) + "/" + std::to_string( p.args.c_chunk );
     }
   }
   std::strncpy( buf, l_s.c_str(), (std::size_t) len - 1 );

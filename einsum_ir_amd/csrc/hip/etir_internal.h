@@ -46,7 +46,8 @@ enum class PermMode : int32_t {
   TRANSPOSE = 1,  // LDS-tiled 2-D transpose of (in-unit dim, out-unit dim) + batch
   COPY_VEC  = 2,  // both innermost dims unit-stride: vectorised strided copy
   GATHER    = 3,  // anything else: one thread per output element
-  TILED     = 4   // small unit-stride dims: tiles over both tensors' innermost runs
+  TILED     = 4,  // small unit-stride dims: tiles over both tensors' innermost runs
+  REG4      = 5   // short unit-stride dims: 4 x 4 register transposes, 16-byte rows through LDS
 };
 
 constexpr int kPermTileDims = 4;   // dims of a TILED tile (2 per run at most)
@@ -88,10 +89,20 @@ struct PermArgs {
   int32_t const * tab_w;
   int32_t const * tab_rc;
   int32_t const * tab_wc;
+  // REG4: the dim next to the unit-stride ones in the thread order (size,
+  // strides) and how many of its indices one workgroup covers
+  int64_t  c_size;
+  int64_t  c_s_in;
+  int64_t  c_s_out;
+  int32_t  c_chunk;
+  int32_t  slot_pi;   // REG4: LDS pitch (16-byte slots) of i and of c
+  int32_t  slot_pc;
+  int32_t  nt_store;  // TRANSPOSE: streaming (non-temporal) output stores
 };
 
 struct PermutePlan {
   PermMode mode = PermMode::GATHER;
+  int32_t  reg4_cpt = 1;                 // REG4: passes of the threads over c per workgroup (1 or 2)
   int32_t  dtype = ETIR_FP32;
   int32_t  ktype = ETIR_KTYPE_COPY;
   int64_t  elem_bytes = 4;

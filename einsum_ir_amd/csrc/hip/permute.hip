@@ -70,6 +70,19 @@ constexpr int kTile = 64;
 constexpr int kThreads = 256;
 constexpr int kPermTileMax = 4096;   // elements of a TILED tile
 
+// 16-byte store that does not keep the line in the caches (the output is
+// written once and not read again by the kernel)
+template< typename T >
+__device__ inline void store_stream( Vec4< T > * p, Vec4< T > const & v ) {
+  if constexpr( sizeof( Vec4< T > ) == 16 ) {
+    typedef uint32_t u4 __attribute__( ( ext_vector_type( 4 ) ) );
+    __builtin_nontemporal_store( __builtin_bit_cast( u4, v ), reinterpret_cast< u4 * >( p ) );
+  }
+  else {
+    *p = v;
+  }
+}
+
 // LDS-tiled transpose of one 64x64 (i, o) tile per workgroup.
 template< typename T >
 __global__ __launch_bounds__( kThreads )
@@ -148,7 +161,8 @@ void perm_transpose_kernel( PermArgs a ) {
         Vec4< T > l_tmp;
 #pragma unroll
         for( int l_e = 0; l_e < 4; l_e++ ) l_tmp.v[l_e] = l_v[l_e];
-        *l_ptr = l_tmp;
+        if( a.nt_store ) store_stream( l_ptr, l_tmp );
+        else             *l_ptr = l_tmp;
       }
     }
     else {
@@ -266,6 +280,129 @@ void perm_tiled_kernel( PermArgs a ) {
   }
 }
 
+// Short unit-stride dims (REG4): 4 x 4 blocks transposed in registers, whole
+// 16-byte rows exchanged through LDS.  i is the input's unit-stride dim, o
+// the output's, c the dim walked next (the one that continues the input's
+// run, or the output's); a workgroup takes all of i and o and c_chunk values
+// of c (size_i * size_o * c_chunk <= 4096 elements).
+//   read:  thread (ig, c, og) -- ig fastest -- loads the four 16-byte rows
+//          in[o = 4 og + r][c][i = 4 ig .. 4 ig + 3], r = 0..3: one load
+//          instruction of a wave covers one input row o over a contiguous
+//          run of (c, i);
+//   swap:  the 4 x 4 block is transposed by renaming registers, and its four
+//          16-byte output rows out[i = 4 ig + q][c][o = 4 og .. +3] go to LDS
+//          at [c][i][og] (one 16-byte slot each; the pitches of i and c are
+//          padded as the planner finds free of bank conflicts for both phases);
+//   write: the threads walk the slots in output order (o groups fastest,
+//          then i or c, whichever is nearer the output's unit stride) and
+//          store them: one store instruction covers a contiguous run of the
+//          output as long as the dims allow.
+// All LDS accesses are 16 bytes; no tables.
+template< typename T, int CPT >
+__global__ __launch_bounds__( kThreads )
+void perm_reg4_kernel( PermArgs a ) {
+  extern __shared__ __attribute__( ( aligned( 16 ) ) ) char l_lds_raw[];
+  Vec4< T > * l_slots = reinterpret_cast< Vec4< T > * >( l_lds_raw );
+  int32_t const l_nig = int32_t( a.size_i / 4 );
+  int32_t const l_nog = int32_t( a.size_o / 4 );
+  int32_t const l_cw  = a.c_chunk / CPT;             // values of c per pass of the threads
+  int32_t const l_ct  = a.c_chunk;                   // values of c per workgroup
+  int32_t const l_pi  = a.slot_pi;                   // slots per i (nog + padding)
+  int32_t const l_pc  = a.slot_pc;                   // slots per c (size_i * pi + padding)
+  int32_t const l_used = l_nig * l_nog * l_cw;       // threads with a block
+
+  int64_t const l_ncb = ( a.c_size + l_ct - 1 ) / l_ct;
+  int64_t l_bid = blockIdx.x;
+  int64_t const l_cbase = ( l_bid % l_ncb ) * l_ct;
+  l_bid /= l_ncb;
+  int64_t l_off_in  = 0;
+  int64_t l_off_out = 0;
+  for( int l_d = a.num_batch - 1; l_d >= 0; l_d-- ) {
+    int64_t const l_idx = l_bid % a.batch_size[l_d];
+    l_bid /= a.batch_size[l_d];
+    l_off_in  += l_idx * a.batch_s_in[l_d];
+    l_off_out += l_idx * a.batch_s_out[l_d];
+  }
+  T const * l_in  = reinterpret_cast< T const * >( a.in ) + l_off_in;
+  T       * l_out = reinterpret_cast< T * >( a.out ) + l_off_out;
+  bool const l_active = int32_t( threadIdx.x ) < l_used;
+
+  // read (all CPT passes' loads in flight together) + register transpose + LDS
+  {
+    int32_t l_x = threadIdx.x;
+    int32_t const l_ig = l_x % l_nig;
+    l_x /= l_nig;
+    int32_t const l_cl = l_x % l_cw;
+    int32_t const l_og = l_x / l_cw;
+    T l_v[CPT][4][4];
+    bool l_ok[CPT];
+#pragma unroll
+    for( int l_u = 0; l_u < CPT; l_u++ ) {
+      int64_t const l_c = l_cbase + l_cl + l_u * l_cw;
+      l_ok[l_u] = l_active && l_c < a.c_size;
+      if( !l_ok[l_u] ) continue;
+      T const * l_p = l_in + l_c * a.c_s_in + int64_t( 4 * l_og ) * a.s_in_o + 4 * l_ig;
+      if( a.vec_ok ) {
+#pragma unroll
+        for( int l_r = 0; l_r < 4; l_r++ ) {
+          Vec4< T > const l_t = *reinterpret_cast< Vec4< T > const * >( l_p + l_r * a.s_in_o );
+#pragma unroll
+          for( int l_q = 0; l_q < 4; l_q++ ) l_v[l_u][l_r][l_q] = l_t.v[l_q];
+        }
+      }
+      else {
+#pragma unroll
+        for( int l_r = 0; l_r < 4; l_r++ )
+#pragma unroll
+          for( int l_q = 0; l_q < 4; l_q++ ) l_v[l_u][l_r][l_q] = l_p[l_r * a.s_in_o + l_q];
+      }
+    }
+#pragma unroll
+    for( int l_u = 0; l_u < CPT; l_u++ ) {
+      if( !l_ok[l_u] ) continue;
+#pragma unroll
+      for( int l_q = 0; l_q < 4; l_q++ ) {
+        Vec4< T > l_w;
+#pragma unroll
+        for( int l_r = 0; l_r < 4; l_r++ ) l_w.v[l_r] = l_v[l_u][l_r][l_q];
+        l_slots[( l_cl + l_u * l_cw ) * l_pc + ( 4 * l_ig + l_q ) * l_pi + l_og] = l_w;
+      }
+    }
+  }
+  __syncthreads();
+  // LDS -> output: the tile's 16-byte slots in output order (o groups
+  // fastest, then whichever of i and c has the smaller output stride), so
+  // that the 64 slots of one store instruction are as contiguous as the
+  // output allows
+  {
+    int32_t const l_si = int32_t( a.size_i );
+    int32_t const l_nslots = l_si * l_ct * l_nog;
+    bool const l_c_inner = a.c_s_out < a.s_out_i;
+    for( int32_t l_s = threadIdx.x; l_s < l_nslots; l_s += kThreads ) {
+      int32_t const l_og = l_s % l_nog;
+      int32_t const l_s2 = l_s / l_nog;
+      int32_t const l_cl = l_c_inner ? l_s2 % l_ct : l_s2 / l_si;
+      int32_t const l_i  = l_c_inner ? l_s2 / l_ct : l_s2 % l_si;
+      int64_t const l_c = l_cbase + l_cl;
+      if( l_c >= a.c_size ) continue;
+      Vec4< T > l_w = l_slots[l_cl * l_pc + l_i * l_pi + l_og];
+      T * l_pq = l_out + l_c * a.c_s_out + int64_t( l_i ) * a.s_out_i + 4 * l_og;
+      if( a.vec_ok ) {
+        if( a.add ) {
+          Vec4< T > const l_old = *reinterpret_cast< Vec4< T > const * >( l_pq );
+#pragma unroll
+          for( int l_r = 0; l_r < 4; l_r++ ) l_w.v[l_r] = Elem< T >::add( l_old.v[l_r], l_w.v[l_r] );
+        }
+        store_stream( reinterpret_cast< Vec4< T > * >( l_pq ), l_w );
+      }
+      else {
+#pragma unroll
+        for( int l_r = 0; l_r < 4; l_r++ ) l_pq[l_r] = a.add ? Elem< T >::add( l_pq[l_r], l_w.v[l_r] ) : l_w.v[l_r];
+      }
+    }
+  }
+}
+
 // One thread per VW consecutive output elements of the innermost dim.
 // Dims are (outer -> inner) in a.batch_*; for VW == 4 the innermost dim has
 // unit stride in both tensors and a size divisible by 4.
@@ -332,6 +469,22 @@ int launch_typed( PermutePlan const & p,
     }
     else {
       hipLaunchKernelGGL( ( perm_tiled_kernel< T, 1 > ), dim3( (uint32_t) l_blocks ), dim3( kThreads ), l_lds, stream, a );
+    }
+  }
+  else if( p.mode == PermMode::REG4 ) {
+    int64_t const l_blocks = ( ( a.c_size + a.c_chunk - 1 ) / a.c_chunk ) * a.num_batch_total;
+    if( l_blocks > 0x7fffffffLL ) {
+      return fail( ETIR_UNDEFINED_ERROR, "permute: grid too large" );
+    }
+    std::size_t const l_lds = std::size_t( a.c_chunk ) * a.slot_pc * 4 * sizeof( T );
+    if( p.reg4_cpt == 4 ) {
+      hipLaunchKernelGGL( ( perm_reg4_kernel< T, 4 > ), dim3( (uint32_t) l_blocks ), dim3( kThreads ), l_lds, stream, a );
+    }
+    else if( p.reg4_cpt == 2 ) {
+      hipLaunchKernelGGL( ( perm_reg4_kernel< T, 2 > ), dim3( (uint32_t) l_blocks ), dim3( kThreads ), l_lds, stream, a );
+    }
+    else {
+      hipLaunchKernelGGL( ( perm_reg4_kernel< T, 1 > ), dim3( (uint32_t) l_blocks ), dim3( kThreads ), l_lds, stream, a );
     }
   }
   else if( p.mode == PermMode::TRANSPOSE ) {
@@ -720,6 +873,138 @@ int plan_permute( int64_t         num_dims,
     return ETIR_SUCCESS;
   }
 
+  // a long input unit-stride dim with a short output one (<= 16): split it
+  // into an inner part that, with the output's dim, fills one wave of 4 x 4
+  // blocks and an outer part (the REG4 tiles below take the inner part whole)
+  if(    l_dim_i >= 0 && l_dim_o >= 0 && l_dim_i != l_dim_o && l_n < kPermMaxDims
+      && plan.size[l_dim_o] % 4 == 0 && plan.size[l_dim_o] <= 16
+      && ( plan.size[l_dim_i] / 4 ) * ( plan.size[l_dim_o] / 4 ) > 64
+      && std::getenv( "ETIR_NO_PERM_REG4" ) == nullptr ) {
+    int64_t const l_lo = 4 * ( 64 / ( plan.size[l_dim_o] / 4 ) );
+    if( plan.size[l_dim_i] % l_lo == 0 ) {
+      for( int l_di = l_n; l_di > l_dim_i; l_di-- ) {
+        plan.size[l_di]  = plan.size[l_di - 1];
+        plan.s_in[l_di]  = plan.s_in[l_di - 1];
+        plan.s_out[l_di] = plan.s_out[l_di - 1];
+      }
+      // dims stay in output order: the outer part has the larger output stride
+      plan.size[l_dim_i]      = plan.size[l_dim_i + 1] / l_lo;
+      plan.s_in[l_dim_i]      = l_lo;
+      plan.s_out[l_dim_i]     = plan.s_out[l_dim_i + 1] * l_lo;
+      plan.size[l_dim_i + 1]  = l_lo;
+      if( l_dim_o > l_dim_i ) l_dim_o++;
+      l_dim_i++;
+      l_n++;
+      plan.num_dims = l_n;
+    }
+  }
+
+  if(    l_dim_i >= 0 && l_dim_o >= 0 && l_dim_i != l_dim_o
+      && plan.size[l_dim_i] % 4 == 0 && plan.size[l_dim_o] % 4 == 0
+      && std::min( plan.size[l_dim_i], plan.size[l_dim_o] ) <= 16
+      && ( plan.size[l_dim_i] / 4 ) * ( plan.size[l_dim_o] / 4 ) <= kThreads
+      && std::getenv( "ETIR_NO_PERM_REG4" ) == nullptr ) {
+    // a short unit-stride dim: 4 x 4 register transposes.  The dim that
+    // continues the input's run (input stride size_i), else the output's,
+    // else the largest other dim, is walked by consecutive lanes after i
+    plan.mode = PermMode::REG4;
+    a.size_i  = plan.size[l_dim_i];
+    a.size_o  = plan.size[l_dim_o];
+    a.s_in_o  = plan.s_in[l_dim_o];
+    a.s_out_i = plan.s_out[l_dim_i];
+    auto other = [&]( int d ) { return d != l_dim_i && d != l_dim_o; };
+    int l_dc = -1;
+    for( int l_di = 0; l_di < l_n && l_dc < 0; l_di++ ) {
+      if( other( l_di ) && plan.s_in[l_di] == a.size_i ) l_dc = l_di;
+    }
+    for( int l_di = 0; l_di < l_n && l_dc < 0; l_di++ ) {
+      if( other( l_di ) && plan.s_out[l_di] == a.size_o ) l_dc = l_di;
+    }
+    if( l_dc < 0 ) {
+      for( int l_di = 0; l_di < l_n; l_di++ ) {
+        if( other( l_di ) && ( l_dc < 0 || plan.size[l_di] > plan.size[l_dc] ) ) l_dc = l_di;
+      }
+    }
+    a.c_size  = l_dc >= 0 ? plan.size[l_dc] : 1;
+    a.c_s_in  = l_dc >= 0 ? plan.s_in[l_dc] : 0;
+    a.c_s_out = l_dc >= 0 ? plan.s_out[l_dc] : 0;
+    // a workgroup's tile: all of i and o, c_chunk values of c -- one value
+    // per thread group of (i/4 x o/4) threads.  Two or four passes of the
+    // threads (ETIR_PERM_REG4_CPT) give longer runs of (c, i) but measured
+    // slower on every 4-D shape tried (more LDS per workgroup, fewer resident)
+    a.c_chunk = (int32_t) std::max< int64_t >( 1, kThreads / ( ( a.size_i / 4 ) * ( a.size_o / 4 ) ) );
+    plan.reg4_cpt = 1;
+    if( char const * l_env = std::getenv( "ETIR_PERM_REG4_CPT" ) ) {
+      int const l_v = std::atoi( l_env );
+      plan.reg4_cpt = ( l_v == 2 || l_v == 4 ) ? l_v : 1;
+    }
+    a.c_chunk *= plan.reg4_cpt;
+    // LDS slot pitches: simulate both phases' 16-byte accesses (eight lanes
+    // per LDS cycle, a slot covers 4 of the 64 four-byte banks) and take the
+    // padding with the fewest conflicts
+    {
+      int32_t const l_nig = int32_t( a.size_i / 4 ), l_nog = int32_t( a.size_o / 4 );
+      int32_t const l_si = int32_t( a.size_i );
+      int32_t const l_cw = a.c_chunk / plan.reg4_cpt, l_ct = a.c_chunk;
+      int32_t const l_used = l_nig * l_nog * l_cw;
+      bool const l_c_inner = a.c_s_out < a.s_out_i;
+      int64_t l_best = -1;
+      for( int32_t l_padi = 0; l_padi < 4; l_padi++ ) {
+        for( int32_t l_padc = 0; l_padc < 16; l_padc++ ) {
+          int32_t const l_pi = l_nog + l_padi, l_pc = l_si * l_pi + l_padc;
+          int64_t l_cost = 0;
+          auto group_cost = [&]( std::vector< int32_t > const & slots ) {
+            for( std::size_t l_g = 0; l_g < slots.size(); l_g += 8 ) {
+              int l_cnt[16] = { 0 };
+              int l_mx = 0;
+              for( std::size_t l_k = l_g; l_k < std::min( slots.size(), l_g + 8 ); l_k++ ) {
+                l_mx = std::max( l_mx, ++l_cnt[slots[l_k] % 16] );
+              }
+              l_cost += l_mx;
+            }
+          };
+          // phase 1: one instruction per (pass, q), lanes = threads
+          for( int l_u = 0; l_u < plan.reg4_cpt; l_u++ ) {
+            for( int l_q = 0; l_q < 4; l_q++ ) {
+              std::vector< int32_t > l_sl;
+              for( int32_t l_t = 0; l_t < l_used; l_t++ ) {
+                int32_t const l_ig = l_t % l_nig, l_cl = ( l_t / l_nig ) % l_cw, l_og = l_t / l_nig / l_cw;
+                l_sl.push_back( ( l_cl + l_u * l_cw ) * l_pc + ( 4 * l_ig + l_q ) * l_pi + l_og );
+              }
+              group_cost( l_sl );
+            }
+          }
+          // phase 2: slots in output order
+          std::vector< int32_t > l_sl;
+          for( int32_t l_s = 0; l_s < l_si * l_ct * l_nog; l_s++ ) {
+            int32_t const l_og = l_s % l_nog, l_s2 = l_s / l_nog;
+            int32_t const l_cl = l_c_inner ? l_s2 % l_ct : l_s2 / l_si;
+            int32_t const l_i  = l_c_inner ? l_s2 / l_ct : l_s2 % l_si;
+            l_sl.push_back( l_cl * l_pc + l_i * l_pi + l_og );
+          }
+          group_cost( l_sl );
+          if( l_best < 0 || l_cost < l_best ) {
+            l_best = l_cost;
+            a.slot_pi = l_pi;
+            a.slot_pc = l_pc;
+          }
+        }
+      }
+    }
+    a.num_batch = 0;
+    a.num_batch_total = 1;
+    for( int l_di = 0; l_di < l_n; l_di++ ) {
+      if( l_di == l_dim_i || l_di == l_dim_o || l_di == l_dc ) continue;
+      a.batch_size[a.num_batch]  = plan.size[l_di];
+      a.batch_s_in[a.num_batch]  = plan.s_in[l_di];
+      a.batch_s_out[a.num_batch] = plan.s_out[l_di];
+      a.num_batch_total *= plan.size[l_di];
+      a.num_batch++;
+    }
+    a.vec_ok = ( a.s_in_o % 4 == 0 && a.s_out_i % 4 == 0 && all_div4( l_dim_i, l_dim_o ) ) ? 1 : 0;
+    return ETIR_SUCCESS;
+  }
+
   if(    l_dim_i >= 0 && l_dim_o >= 0 && l_n > 1
       && (    ( plan.size[l_dim_i] < kTile && plan.size[l_dim_o] < kTile )
            || std::min( plan.size[l_dim_i], plan.size[l_dim_o] ) <= 8
@@ -757,6 +1042,8 @@ int plan_permute( int64_t         num_dims,
     a.vec_ok = (    a.size_i % 4 == 0 && a.size_o % 4 == 0
                  && a.s_in_o % 4 == 0 && a.s_out_i % 4 == 0
                  && all_div4( l_dim_i, l_dim_o ) ) ? 1 : 0;
+    a.nt_store = 1;
+    if( char const * l_env = std::getenv( "ETIR_PERM_NT" ) ) a.nt_store = std::atoi( l_env ) != 0;
     return ETIR_SUCCESS;
   }
 

@@ -102,8 +102,8 @@ def test_permute_rejects_bad_ktype(torch_cuda):
 # both unit-stride dims shorter than a 64-wide tile: tiles over the innermost
 # runs of both tensors (shared middle dims, 2-dim runs, ragged edges, 5-D)
 TILED_CASES = [
-    ("abcd->dbca", dict(a=8, b=64, c=96, d=8)),       # runs (d,c) and (a,c): shared c
-    ("abcd->dbca", dict(a=16, b=40, c=48, d=16)),
+    ("abcd->dbca", dict(a=6, b=64, c=96, d=10)),      # runs (d,c) and (a,c): shared c
+    ("abcd->dbca", dict(a=20, b=40, c=48, d=14)),
     ("abcd->dbca", dict(a=5, b=9, c=70, d=13)),       # ragged everywhere
     ("abcd->acdb", dict(a=7, b=13, c=11, d=5)),
     ("abcde->bdaec", dict(a=12, b=9, c=9, d=12, e=16)),
@@ -127,6 +127,64 @@ def test_permute_tiled(torch_cuda, oracle, expr, sizes, dtype):
 @pytest.mark.parametrize("expr,sizes", [TILED_CASES[0], TILED_CASES[2], TILED_CASES[7]])
 def test_permute_tiled_add(torch_cuda, oracle, expr, sizes):
     _check(torch_cuda, oracle, expr, sizes, dtype=eir.FP32, ktype=eir.ADD)
+
+
+# both unit-stride dims multiples of 4, the shorter <= 16: 4 x 4 register
+# transposes (one input dim whose run continues i, else the output's, else the
+# largest, is walked by the lanes; long input unit dims are split first)
+REG4_CASES = [
+    ("abcd->dbca", dict(a=8, b=64, c=96, d=8)),        # c continues both runs
+    ("abcd->dbca", dict(a=16, b=40, c=48, d=16)),
+    ("abcd->dbca", dict(a=4, b=33, c=17, d=4)),        # ragged last chunk of c
+    ("abcd->adcb", dict(a=12, b=8, c=10, d=64)),       # i=64, o=8: one wave of blocks
+    ("abcd->acdb", dict(a=3, b=8, c=5, d=256)),        # i=cd=1280 split into 10 x 128
+    ("abcd->acdb", dict(a=2, b=4, c=3, d=512)),        # i=cd=1536 split into 6 x 256
+    ("abcde->bdeca", dict(a=4, b=6, c=7, d=5, e=8)),   # 5-D, i=de=40, batch dims around c
+    ("abc->cba", dict(a=12, b=1, c=16)),               # no dim beside i and o
+    ("abcd->dbca", dict(a=20, b=40, c=48, d=12)),      # 15 blocks a value of c: chunk 17
+]
+
+
+@pytest.mark.parametrize("expr,sizes", REG4_CASES)
+@pytest.mark.parametrize("dtype", [eir.FP32, eir.FP64, eir.BF16])
+def test_permute_reg4(torch_cuda, oracle, expr, sizes, dtype):
+    desc = _check(torch_cuda, oracle, expr, sizes, dtype=dtype, seed=3 + len(expr))
+    assert "reg4" in desc
+
+
+@pytest.mark.parametrize("expr,sizes", [REG4_CASES[0], REG4_CASES[2], REG4_CASES[4]])
+@pytest.mark.parametrize("dtype", [eir.FP32, eir.FP64])
+def test_permute_reg4_add(torch_cuda, oracle, expr, sizes, dtype):
+    desc = _check(torch_cuda, oracle, expr, sizes, dtype=dtype, ktype=eir.ADD)
+    assert "reg4" in desc
+
+
+@pytest.mark.parametrize("cpt", ["2", "4"])
+def test_permute_reg4_passes(torch_cuda, oracle, monkeypatch, cpt):
+    """Two and four passes of the threads over c (a planner option)."""
+    monkeypatch.setenv("ETIR_PERM_REG4_CPT", cpt)
+    for expr, sizes in REG4_CASES[:3]:
+        desc = _check(torch_cuda, oracle, expr, sizes, seed=int(cpt))
+        assert "reg4" in desc
+
+
+def test_permute_4d_bench_shapes(torch_cuda):
+    """The 4-D fp32 shapes timed beside config 2, at full size (16.8-31.9 M
+    elements), bit-exact against torch's own permute of the same tensor."""
+    torch = torch_cuda
+    import bench
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    for expr, shape in bench.PERMUTES_4D:
+        u = eir.unary_dims(expr, dict(zip("abcd", shape)))
+        x = torch.rand(shape, device="cuda", generator=gen)
+        y = torch.empty(x.numel(), device="cuda")
+        plan = eir.PermutePlan(u["sizes"], u["strides_in"], u["strides_out"], dtype=eir.FP32, ktype=eir.COPY)
+        plan.execute(x, y, stream=torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        desc = plan.describe()
+        plan.close()
+        perm = ["abcd".index(ch) for ch in expr.split("->")[1]]
+        assert torch.equal(y, x.permute(*perm).contiguous().view(-1)), (expr, shape, desc)
 
 
 @pytest.mark.parametrize("pad", [0, 4])
