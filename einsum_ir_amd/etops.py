@@ -31,6 +31,7 @@ Differences from the tpp backend, by design:
     accumulation).
 """
 import ctypes
+import dataclasses
 import enum
 import json
 from dataclasses import dataclass
@@ -87,61 +88,154 @@ float64 = DataType.float64
 bfloat16 = DataType.bfloat16
 
 
-class prim:
-    """Namespace for primitive types used in tensor operations."""
-    none = PrimType.none
-    zero = PrimType.zero
-    relu = PrimType.relu
-    copy = PrimType.copy
-    gemm = PrimType.gemm
-    brgemm = PrimType.brgemm
-    __all__ = ["none", "zero", "relu", "copy", "gemm", "brgemm"]
+def _namespace(name: str, members: type, doc: str) -> type:
+    """A plain class whose attributes are the members of an enum, so that
+    ``etops.prim.gemm`` is ``PrimType.gemm``."""
+    attrs = {m.name: m for m in members}
+    return type(name, (), {**attrs, "__doc__": doc, "__all__": list(attrs)})
 
 
-class etype:
-    """Namespace for execution types used in tensor operations."""
-    prim = ExecType.prim
-    seq = ExecType.seq
-    shared = ExecType.shared
-    sfc = ExecType.sfc
-    __all__ = ["prim", "seq", "shared", "sfc"]
-
-
-exec = etype  # noqa: A001  (the reference exports this name too)
-
-
-class dim:
-    """Namespace for dimension types used in tensor operations."""
-    c = DimType.c
-    m = DimType.m
-    n = DimType.n
-    k = DimType.k
-    __all__ = ["c", "m", "n", "k"]
-
+prim = _namespace("prim", PrimType, "Primitives of a tensor operation (first touch, main, last touch).")
+etype = _namespace("etype", ExecType, "How a loop of a tensor operation is executed.")
+exec = etype  # noqa: A001  (exported under both names, like the reference module)
+dim = _namespace("dim", DimType, "The role of a dimension: batch c, rows m, columns n, reduction k.")
 
 BACKENDS = ("hip",)
-_BINARY = (PrimType.gemm, PrimType.brgemm)
-_UNARY = (PrimType.copy, PrimType.zero)
 # the tpp backend's optimisation keys (reference bindings.cpp:174-178)
 _OPT_KEYS = ("target_m", "target_n", "target_k", "num_threads", "packed_gemm_support",
              "br_gemm_support", "packing_support", "sfc_support", "l2_cache_size")
 
 
-def _op_kind(prim_main):
-    if prim_main in _BINARY:
-        return "binary"
-    if prim_main in _UNARY:
-        return "unary"
-    return None
+# ---------------------------------------------------------------------------
+# configuration rules
+# ---------------------------------------------------------------------------
+@dataclass(frozen=True)
+class _OpKind:
+    """One kind of operation, selected by its main primitive, and what it
+    allows around it (the accept/reject rules of reference etops/__init__.py:
+    170-253 and TensorOperation.cpp:220-289, restated as data)."""
+    name: str
+    mains: frozenset
+    tensors: tuple             # level-0 stride lists, in order
+    firsts: frozenset          # allowed first-touch primitives
+    lasts: frozenset           # allowed last-touch primitives
+    dims: Optional[frozenset]  # allowed dimension types, None: any
+
+
+_OP_KINDS = (
+    _OpKind("binary", frozenset({PrimType.gemm, PrimType.brgemm}), ("in0", "in1", "out"),
+            frozenset({PrimType.none, PrimType.zero}), frozenset({PrimType.none, PrimType.relu}), None),
+    _OpKind("unary", frozenset({PrimType.copy, PrimType.zero}), ("in", "out"),
+            frozenset({PrimType.none}), frozenset({PrimType.none}), frozenset({DimType.c})),
+)
+
+
+def _kind_of(prim_main) -> Optional[_OpKind]:
+    return next((k for k in _OP_KINDS if prim_main in k.mains), None)
+
+
+class ConfigError(ValueError):
+    """A rejected configuration.  ``rules`` names every rule it breaks, in
+    the order of the rule table; ``str()`` lists them with details."""
+
+    def __init__(self, problems):
+        self.rules = tuple(rule for rule, _ in problems)
+        self.problems = tuple(problems)
+        super().__init__("; ".join(f"[{rule}] {text}" for rule, text in problems))
+
+
+def _bad_entries(values, ok):
+    return [f"{i}: {v!r}" for i, v in enumerate(values) if not ok(v)]
+
+
+def _stride_dims(cfg, kind):
+    off = [f"{name} has {len(st)}" for name, st in zip(kind.tensors, cfg.strides[0])
+           if len(st) != len(cfg.dim_types)]
+    return f"{len(cfg.dim_types)} dims, but " + ", ".join(off) if off else None
+
+
+# (rule, check).  A check gets the config and its operation kind and returns
+# None when the rule holds, else a description.  Rules whose inputs an earlier
+# rule found malformed are skipped (see _problems).
+_RULES = (
+    ("backend", lambda c, k: None if c.backend is None or c.backend in BACKENDS
+        else f"backend {c.backend!r} is not one of {BACKENDS} (or None)"),
+    ("prim_main", lambda c, k: None if k is not None
+        else f"{c.prim_main!r} is no main primitive; binary: gemm, brgemm; unary: copy, zero"),
+    ("exec_types", lambda c, k: None if len(c.exec_types) == len(c.dim_types)
+        else f"{len(c.exec_types)} exec types for {len(c.dim_types)} dims"),
+    ("dim_sizes", lambda c, k: None if len(c.dim_sizes) == len(c.dim_types)
+        else f"{len(c.dim_sizes)} sizes for {len(c.dim_types)} dims"),
+    ("dim_size_positive", lambda c, k: ", ".join(_bad_entries(c.dim_sizes, lambda s: s > 0)) or None),
+    ("stride_levels", lambda c, k: None if len(c.strides) > 0 else "no level-0 strides"),
+    ("stride_tensors", lambda c, k: None if len(c.strides[0]) == len(k.tensors)
+        else f"level 0 holds {len(c.strides[0])} stride lists, a {k.name} operation takes "
+             f"{len(k.tensors)} ({', '.join(k.tensors)})"),
+    ("stride_dims", lambda c, k: _stride_dims(c, k)),
+    ("dim_types", lambda c, k: None if k.dims is None else
+        ", ".join(_bad_entries(c.dim_types, lambda d: d in k.dims)) or None),
+    ("prim_first", lambda c, k: None if c.prim_first in k.firsts
+        else f"{c.prim_first!r} cannot open a {k.name} operation"),
+    ("prim_last", lambda c, k: None if c.prim_last in k.lasts
+        else f"{c.prim_last!r} cannot close a {k.name} operation"),
+)
+# rules that need the operation kind, and the rule each further depends on
+_NEEDS = {"stride_tensors": ("prim_main", "stride_levels"), "stride_dims": ("prim_main", "stride_levels"),
+          "dim_types": ("prim_main",), "prim_first": ("prim_main",), "prim_last": ("prim_main",)}
+
+
+def _problems(cfg) -> list:
+    kind = _kind_of(cfg.prim_main)
+    failed, found = set(), []
+    for rule, check in _RULES:
+        if any(dep in failed for dep in _NEEDS.get(rule, ())):
+            continue
+        text = check(cfg, kind)
+        if text is not None:
+            failed.add(rule)
+            found.append((rule, text))
+    return found
+
+
+# ---------------------------------------------------------------------------
+# JSON form: one codec per field (the keys and value spellings are the
+# reference's file format, etops/__init__.py:269-360; "backend" is optional)
+# ---------------------------------------------------------------------------
+def _enum_codec(members):
+    def decode(name):
+        if name not in members.__members__:
+            raise ConfigError([("json_value", f"{name!r} is not a {members.__name__} name")])
+        return members[name]
+    return (lambda v: v.name), decode
+
+
+def _enum_list_codec(members):
+    enc, dec = _enum_codec(members)
+    return (lambda vs: [enc(v) for v in vs]), (lambda names: tuple(dec(n) for n in names))
+
+
+_JSON_FIELDS = {
+    "data_type": _enum_codec(DataType),
+    "prim_first": _enum_codec(PrimType),
+    "prim_main": _enum_codec(PrimType),
+    "prim_last": _enum_codec(PrimType),
+    "dim_types": _enum_list_codec(DimType),
+    "exec_types": _enum_list_codec(ExecType),
+    "dim_sizes": (list, tuple),
+    "strides": (lambda s: [[list(t) for t in lvl] for lvl in s],
+                lambda s: tuple(tuple(tuple(t) for t in lvl) for lvl in s)),
+}
 
 
 @dataclass(frozen=True)
 class TensorOperationConfig:
-    """Configuration of one tensor operation (reference etops/__init__.py:116-268).
-
-    strides has shape [LEVEL][TENSOR][DIMENSION]: level 0 the tensors' own
-    strides (binary: in0, in1, out; unary: in, out), further levels packing
-    strides (accepted, unused by the GPU kernels)."""
+    """Everything that defines one tensor operation (reference
+    etops/__init__.py:116-268): data type, the three primitives, one entry per
+    loop in dim_types / exec_types / dim_sizes, and strides indexed
+    [level][tensor][loop].  Level 0 holds the tensors' own strides (binary:
+    in0, in1, out; unary: in, out); further levels are packing strides, kept
+    but not used by the GPU kernels.  A config that breaks a rule raises
+    ConfigError (a ValueError) on construction."""
     data_type: DataType
     prim_first: PrimType
     prim_main: PrimType
@@ -153,48 +247,9 @@ class TensorOperationConfig:
     backend: Optional[str] = None
 
     def __post_init__(self):
-        if self.backend is not None and self.backend not in BACKENDS:
-            raise ValueError(f"Unsupported backend: '{self.backend}'. This build provides only 'hip'.")
-        kind = _op_kind(self.prim_main)
-        if kind is None:
-            raise ValueError(f"Invalid prim_main: {self.prim_main}. "
-                             "Must be gemm/brgemm (binary) or copy/zero (unary).")
-        num_dims = len(self.dim_types)
-        if len(self.exec_types) != num_dims:
-            raise ValueError(f"exec_types length ({len(self.exec_types)}) must match "
-                             f"dim_types length ({num_dims}).")
-        if len(self.dim_sizes) != num_dims:
-            raise ValueError(f"dim_sizes length ({len(self.dim_sizes)}) must match "
-                             f"dim_types length ({num_dims}).")
-        for i, size in enumerate(self.dim_sizes):
-            if size <= 0:
-                raise ValueError(f"dim_sizes[{i}] must be positive, got {size}.")
-        if len(self.strides) == 0:
-            raise ValueError("strides must have at least one level (level 0).")
-        names = ["in0", "in1", "out"] if kind == "binary" else ["in", "out"]
-        if len(self.strides[0]) != len(names):
-            raise ValueError(f"strides[0] must have {len(names)} tensors ({', '.join(names)}), "
-                             f"got {len(self.strides[0])}.")
-        for t, st in enumerate(self.strides[0]):
-            if len(st) != num_dims:
-                raise ValueError(f"strides[0][{t}] ({names[t]}) length ({len(st)}) must match "
-                                 f"number of dimensions ({num_dims}).")
-        if kind == "unary":
-            for i, dt in enumerate(self.dim_types):
-                if dt != DimType.c:
-                    raise ValueError("For unary operations, all dim_types must be etops.dim.c. "
-                                     f"dim_types[{i}] is {dt}.")
-            if self.prim_first != PrimType.none:
-                raise ValueError(f"For unary operations, prim_first must be etops.prim.none, got {self.prim_first}.")
-            if self.prim_last != PrimType.none:
-                raise ValueError(f"For unary operations, prim_last must be etops.prim.none, got {self.prim_last}.")
-        else:
-            if self.prim_first not in (PrimType.none, PrimType.zero):
-                raise ValueError("For binary contractions, prim_first must be etops.prim.none or "
-                                 f"etops.prim.zero, got {self.prim_first}.")
-            if self.prim_last not in (PrimType.none, PrimType.relu):
-                raise ValueError("For binary contractions, prim_last must be etops.prim.none or "
-                                 f"etops.prim.relu, got {self.prim_last}.")
+        problems = _problems(self)
+        if problems:
+            raise ConfigError(problems)
 
     def apply(self, op: "TensorOperation") -> None:
         err = op.setup(self.backend if self.backend is not None else "hip", self.data_type, self.prim_first,
@@ -202,19 +257,10 @@ class TensorOperationConfig:
                        tuple(self.dim_sizes),
                        tuple(tuple(tuple(t) for t in level) for level in self.strides))
         if err != ErrorType.success:
-            raise RuntimeError(f"einsum_ir TensorOperation setup failed: ErrorType.{ErrorType(err).name}")
+            raise RuntimeError(f"TensorOperation.setup returned {ErrorType(err).name}")
 
     def to_json(self, indent: Optional[int] = None) -> str:
-        data = {
-            "data_type": self.data_type.name,
-            "prim_first": self.prim_first.name,
-            "prim_main": self.prim_main.name,
-            "prim_last": self.prim_last.name,
-            "dim_types": [d.name for d in self.dim_types],
-            "exec_types": [e.name for e in self.exec_types],
-            "dim_sizes": list(self.dim_sizes),
-            "strides": [[list(t) for t in level] for level in self.strides],
-        }
+        data = {key: encode(getattr(self, key)) for key, (encode, _) in _JSON_FIELDS.items()}
         if self.backend is not None:
             data["backend"] = self.backend
         return json.dumps(data, indent=indent)
@@ -222,27 +268,11 @@ class TensorOperationConfig:
     @classmethod
     def from_json(cls, json_str: str) -> "TensorOperationConfig":
         data = json.loads(json_str)
-        required = ["data_type", "prim_first", "prim_main", "prim_last",
-                    "dim_types", "exec_types", "dim_sizes", "strides"]
-        missing = [f for f in required if f not in data]
-        if missing:
-            raise ValueError(f"Missing required fields: {missing}")
-
-        def get_enum(enum_type, name):
-            try:
-                return enum_type[name]
-            except KeyError:
-                raise ValueError(f"Invalid {enum_type.__name__} value: '{name}'") from None
-
-        return cls(data_type=get_enum(DataType, data["data_type"]),
-                   prim_first=get_enum(PrimType, data["prim_first"]),
-                   prim_main=get_enum(PrimType, data["prim_main"]),
-                   prim_last=get_enum(PrimType, data["prim_last"]),
-                   dim_types=tuple(get_enum(DimType, d) for d in data["dim_types"]),
-                   exec_types=tuple(get_enum(ExecType, e) for e in data["exec_types"]),
-                   dim_sizes=tuple(data["dim_sizes"]),
-                   strides=tuple(tuple(tuple(t) for t in level) for level in data["strides"]),
-                   backend=data.get("backend"))
+        absent = [key for key in _JSON_FIELDS if key not in data]
+        if absent:
+            raise ConfigError([("json_field", f"no {key!r}") for key in absent])
+        fields = {key: decode(data[key]) for key, (_, decode) in _JSON_FIELDS.items()}
+        return cls(backend=data.get("backend"), **fields)
 
     def save(self, path: str, indent: Optional[int] = 2) -> None:
         with open(path, "w") as f:
@@ -252,7 +282,6 @@ class TensorOperationConfig:
     def load(cls, path: str) -> "TensorOperationConfig":
         with open(path) as f:
             return cls.from_json(f.read())
-
 
 # ---------------------------------------------------------------------------
 # tensors: device arrays, raw pointers, host numpy arrays (staged)
@@ -349,11 +378,12 @@ class TensorOperation:
         self.close()
         if backend is not None and backend not in BACKENDS:
             return ErrorType.compilation_failed
-        kind = _op_kind(PrimType(prim_main))
-        if kind is None:
+        op_kind = _kind_of(PrimType(prim_main))
+        if op_kind is None:
             return ErrorType.compilation_failed
+        kind = op_kind.name
         n = len(dim_sizes)
-        if len(strides) == 0 or len(strides[0]) != (3 if kind == "binary" else 2):
+        if len(strides) == 0 or len(strides[0]) != len(op_kind.tensors):
             return ErrorType.invalid_stride_shape
         if any(len(t) != n for t in strides[0]):
             return ErrorType.invalid_stride_shape
@@ -480,24 +510,20 @@ def optimize(config: TensorOperationConfig,
     as given with every exec type ``prim``: the whole operation is one kernel
     grid and the planner chooses fusion and tiles when the operation is set
     up.  Keys other than the tpp backend's raise like the reference's."""
-    actual = config.backend if config.backend is not None else "hip"
+    actual = config.backend or "hip"
     if actual not in BACKENDS:
-        raise ValueError(f"Unknown backend: {actual}")
-    if optimization_config is None:
-        optimization_config = backend.hip.get_default_optimization_config()
-    for key, value in optimization_config.items():
-        if key not in _OPT_KEYS:
-            raise RuntimeError("einsum_ir optimization failed: ErrorType.invalid_optimization_config")
-        if not isinstance(value, (int, bool)):
-            raise RuntimeError("einsum_ir optimization failed: ErrorType.invalid_optimization_config")
-    return TensorOperationConfig(backend=actual, data_type=config.data_type, prim_first=config.prim_first,
-                                 prim_main=config.prim_main, prim_last=config.prim_last,
-                                 dim_types=tuple(config.dim_types),
-                                 exec_types=tuple(ExecType.prim for _ in config.dim_types),
-                                 dim_sizes=tuple(config.dim_sizes),
-                                 strides=(tuple(tuple(t) for t in config.strides[0]),))
+        raise ValueError(f"optimize: no backend {actual!r} here (only {BACKENDS})")
+    options = backend.hip.get_default_optimization_config() if optimization_config is None else optimization_config
+    rejected = [key for key, value in options.items() if key not in _OPT_KEYS or not isinstance(value, (int, bool))]
+    if rejected:
+        raise RuntimeError(f"optimize returned {ErrorType.invalid_optimization_config.name}: "
+                           f"unknown key or non-integer value for {rejected}")
+    return dataclasses.replace(config, backend=actual,
+                               dim_types=tuple(config.dim_types), dim_sizes=tuple(config.dim_sizes),
+                               exec_types=(ExecType.prim,) * len(config.dim_types),
+                               strides=(tuple(tuple(t) for t in config.strides[0]),))
 
 
-__all__ = ["TensorOperation", "TensorOperationConfig", "DataType", "PrimType", "ExecType", "DimType",
+__all__ = ["TensorOperation", "TensorOperationConfig", "ConfigError", "DataType", "PrimType", "ExecType", "DimType",
            "ErrorType", "dtype", "float32", "float64", "bfloat16", "prim", "etype", "exec", "dim", "backend",
            "optimize"]

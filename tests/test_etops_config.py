@@ -3,6 +3,8 @@
 optimize, as the reference states them (reference python/src/etops/__init__.py:
 116-268 validation, 269-360 JSON, 436-514 optimize).  No GPU is needed: no plan
 is created."""
+import json
+
 import pytest
 
 from einsum_ir_amd import etops
@@ -39,48 +41,103 @@ def test_valid_configs():
                                 strides=(((4, 1), (1, 3)),))
 
 
-@pytest.mark.parametrize("kw,msg", [
-    (dict(backend="tpp"), "Unsupported backend"),
-    (dict(prim_main=etops.prim.relu), "Invalid prim_main"),
-    (dict(exec_types=(etops.exec.prim,) * 2), "exec_types length"),
-    (dict(dim_sizes=(32, 16)), "dim_sizes length"),
-    (dict(dim_sizes=(32, 0, 8)), "must be positive"),
-    (dict(strides=()), "at least one level"),
-    (dict(strides=(((1, 0, 32), (0, 8, 1)),)), "must have 3 tensors"),
-    (dict(strides=(((1, 0), (0, 8, 1), (1, 32, 0)),)), "length"),
-    (dict(prim_first=etops.prim.relu), "prim_first must be"),
-    (dict(prim_last=etops.prim.zero), "prim_last must be"),
+@pytest.mark.parametrize("kw,rule", [
+    (dict(backend="tpp"), "backend"),
+    (dict(prim_main=etops.prim.relu), "prim_main"),
+    (dict(prim_main=etops.prim.none), "prim_main"),
+    (dict(exec_types=(etops.exec.prim,) * 2), "exec_types"),
+    (dict(dim_sizes=(32, 16)), "dim_sizes"),
+    (dict(dim_sizes=(32, 0, 8)), "dim_size_positive"),
+    (dict(dim_sizes=(32, 16, -1)), "dim_size_positive"),
+    (dict(strides=()), "stride_levels"),
+    (dict(strides=(((1, 0, 32), (0, 8, 1)),)), "stride_tensors"),
+    (dict(strides=(((1, 0, 32), (0, 8, 1), (1, 32, 0), (1, 1, 1)),)), "stride_tensors"),
+    (dict(strides=(((1, 0), (0, 8, 1), (1, 32, 0)),)), "stride_dims"),
+    (dict(prim_first=etops.prim.relu), "prim_first"),
+    (dict(prim_first=etops.prim.copy), "prim_first"),
+    (dict(prim_last=etops.prim.zero), "prim_last"),
+    (dict(prim_last=etops.prim.gemm), "prim_last"),
 ])
-def test_invalid_binary_configs(kw, msg):
-    with pytest.raises(ValueError, match=msg):
+def test_invalid_binary_configs(kw, rule):
+    with pytest.raises(ValueError) as e:
         _gemm(**kw)
+    assert e.value.rules == (rule,)
 
 
-def test_invalid_unary_configs():
-    base = dict(data_type=etops.float32, prim_first=etops.prim.none, prim_main=etops.prim.copy,
-                prim_last=etops.prim.none, dim_types=(etops.dim.c, etops.dim.c),
-                exec_types=(etops.exec.seq,) * 2, dim_sizes=(3, 4), strides=(((4, 1), (1, 3)),))
-    with pytest.raises(ValueError, match="all dim_types must be"):
-        etops.TensorOperationConfig(**{**base, "dim_types": (etops.dim.c, etops.dim.m)})
-    with pytest.raises(ValueError, match="prim_first must be etops.prim.none"):
-        etops.TensorOperationConfig(**{**base, "prim_first": etops.prim.zero})
-    with pytest.raises(ValueError, match="must have 2 tensors"):
-        etops.TensorOperationConfig(**{**base, "strides": (((4, 1), (1, 3), (1, 3)),)})
+def test_binary_dims_and_levels_are_free():
+    """Binary operations take any dim types, packing levels beyond level 0
+    and every exec type."""
+    _gemm(dim_types=(etops.dim.c, etops.dim.c, etops.dim.c))
+    _gemm(strides=(((1, 0, 32), (0, 8, 1), (1, 32, 0)), ((0, 0, 0),)))
+    _gemm(exec_types=(etops.exec.seq, etops.exec.shared, etops.exec.sfc))
+
+
+def test_every_broken_rule_is_reported():
+    with pytest.raises(ValueError) as e:
+        _gemm(backend="cpu", dim_sizes=(0, 16), prim_last=etops.prim.copy)
+    assert e.value.rules == ("backend", "dim_sizes", "dim_size_positive", "prim_last")
+    # without a level 0 the stride shape rules that read it are not applied
+    with pytest.raises(ValueError) as e:
+        _gemm(strides=(), prim_first=etops.prim.relu)
+    assert e.value.rules == ("stride_levels", "prim_first")
+    # an unknown main primitive leaves nothing to check the kind-specific rules against
+    with pytest.raises(ValueError) as e:
+        _gemm(prim_main=etops.prim.relu, prim_first=etops.prim.relu, strides=(((1,),),))
+    assert e.value.rules == ("prim_main",)
+
+
+_COPY = dict(data_type=etops.float32, prim_first=etops.prim.none, prim_main=etops.prim.copy,
+             prim_last=etops.prim.none, dim_types=(etops.dim.c, etops.dim.c),
+             exec_types=(etops.exec.seq,) * 2, dim_sizes=(3, 4), strides=(((4, 1), (1, 3)),))
+
+
+@pytest.mark.parametrize("kw,rule", [
+    (dict(dim_types=(etops.dim.c, etops.dim.m)), "dim_types"),
+    (dict(dim_types=(etops.dim.k, etops.dim.c)), "dim_types"),
+    (dict(prim_first=etops.prim.zero), "prim_first"),
+    (dict(prim_last=etops.prim.relu), "prim_last"),
+    (dict(strides=(((4, 1), (1, 3), (1, 3)),)), "stride_tensors"),
+    (dict(strides=(((4, 1), (1, 3, 9)),)), "stride_dims"),
+])
+def test_invalid_unary_configs(kw, rule):
+    with pytest.raises(ValueError) as e:
+        etops.TensorOperationConfig(**{**_COPY, **kw})
+    assert e.value.rules == (rule,)
+
+
+def test_unary_zero_is_accepted():
+    etops.TensorOperationConfig(**{**_COPY, "prim_main": etops.prim.zero})
 
 
 def test_json_round_trip(tmp_path):
     cfg = _gemm(prim_last=etops.prim.relu, backend="hip")
     s = cfg.to_json()
-    assert '"prim_last": "relu"' in s and '"backend": "hip"' in s
+    data = json.loads(s)
+    assert data["prim_last"] == "relu" and data["backend"] == "hip"
+    assert data["dim_types"] == ["m", "n", "k"] and data["strides"] == [[[1, 0, 32], [0, 8, 1], [1, 32, 0]]]
     assert etops.TensorOperationConfig.from_json(s) == cfg
     path = tmp_path / "cfg.json"
     cfg.save(str(path))
     assert etops.TensorOperationConfig.load(str(path)) == cfg
-    assert "backend" not in _gemm().to_json()
-    with pytest.raises(ValueError, match="Missing required fields"):
+    assert "backend" not in json.loads(_gemm().to_json())
+    assert etops.TensorOperationConfig.from_json(_gemm().to_json()).backend is None
+
+
+def test_json_rejects():
+    with pytest.raises(ValueError) as e:
         etops.TensorOperationConfig.from_json('{"data_type": "float32"}')
-    with pytest.raises(ValueError, match="Invalid PrimType value"):
+    assert set(e.value.rules) == {"json_field"} and len(e.value.rules) == 7
+    s = _gemm(prim_last=etops.prim.relu).to_json()
+    with pytest.raises(ValueError) as e:
         etops.TensorOperationConfig.from_json(s.replace('"relu"', '"gelu"'))
+    assert e.value.rules == ("json_value",)
+    with pytest.raises(ValueError) as e:
+        etops.TensorOperationConfig.from_json(s.replace('"k"', '"q"'))
+    assert e.value.rules == ("json_value",)
+    # a well-formed file whose content breaks a rule is rejected by the rule
+    with pytest.raises(ValueError) as e:
+        etops.TensorOperationConfig.from_json(s.replace('"relu"', '"zero"'))
+    assert e.value.rules == ("prim_last",)
 
 
 def test_optimize():
@@ -93,6 +150,8 @@ def test_optimize():
     etops.optimize(cfg, {"target_m": 64, "packing_support": False})
     with pytest.raises(RuntimeError, match="invalid_optimization_config"):
         etops.optimize(cfg, {"not_a_key": 1})
+    with pytest.raises(RuntimeError, match="invalid_optimization_config"):
+        etops.optimize(cfg, {"target_m": "large"})
     defaults = etops.backend.hip.get_default_optimization_config()
     assert set(defaults) == {"target_m", "target_n", "target_k", "num_threads", "packed_gemm_support",
                              "br_gemm_support", "packing_support", "sfc_support", "l2_cache_size"}
