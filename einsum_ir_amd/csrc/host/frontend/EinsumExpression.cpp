@@ -243,3 +243,75 @@ einsum_ir::err_t einsum_ir::frontend::EinsumExpression::eval_graph_async() {
 int64_t einsum_ir::frontend::EinsumExpression::num_ops() {
   return m_nodes.empty() ? 0 : m_nodes.back().num_ops( true );
 }
+
+namespace {
+  std::string join_ids( int64_t const * i_ids, int64_t i_n, char i_sep ) {
+    std::string l_s;
+    for( int64_t l_i = 0; l_i < i_n; l_i++ ) {
+      if( l_i > 0 ) l_s += i_sep;
+      l_s += std::to_string( i_ids[l_i] );
+    }
+    return l_s;
+  }
+}
+
+std::string einsum_ir::frontend::EinsumExpression::to_string_exchange_format( backend::EinsumNode const * i_node ) const {
+  if( !m_compiled || m_nodes.empty() ) return "Error: Expression not compiled.";
+  backend::EinsumNode const & l_node = ( i_node != nullptr ) ? *i_node : m_nodes.back();
+  std::string const l_ids = join_ids( l_node.m_dim_ids_int.data(), l_node.m_num_dims, ',' );
+  if( !l_node.m_children.empty() ) {
+    std::string l_s;
+    for( std::size_t l_ch = 0; l_ch < l_node.m_children.size(); l_ch++ ) {
+      l_s += ( l_ch > 0 ? ",[" : "[" ) + to_string_exchange_format( l_node.m_children[l_ch] ) + "]";
+    }
+    return l_s + "->[" + l_ids + "]";
+  }
+  if(    l_node.m_dim_ids_ext != nullptr
+      && !std::equal( l_node.m_dim_ids_ext, l_node.m_dim_ids_ext + l_node.m_num_dims, l_node.m_dim_ids_int.begin() ) ) {
+    return "[" + join_ids( l_node.m_dim_ids_ext, l_node.m_num_dims, ',' ) + "]->[" + l_ids + "]";
+  }
+  return l_ids;
+}
+
+std::string einsum_ir::frontend::EinsumExpression::to_string_render() const {
+  if( !m_compiled || m_nodes.empty() ) return "Error: Expression not compiled.";
+  // levels of (node, slot): a node in slot s has its children in slots 2s, 2s+1
+  std::vector< std::vector< std::pair< backend::EinsumNode const *, int64_t > > > l_levels;
+  l_levels.push_back( { { &m_nodes.back(), 0 } } );
+  while( true ) {
+    std::vector< std::pair< backend::EinsumNode const *, int64_t > > l_next;
+    for( auto const & l_e : l_levels.back() ) {
+      for( std::size_t l_ch = 0; l_ch < l_e.first->m_children.size(); l_ch++ ) {
+        l_next.push_back( { l_e.first->m_children[l_ch], 2 * l_e.second + (int64_t) l_ch } );
+      }
+    }
+    if( l_next.empty() ) break;
+    l_levels.push_back( l_next );
+  }
+  std::size_t l_width = 0;
+  for( auto const & l_lvl : l_levels ) {
+    for( auto const & l_e : l_lvl ) {
+      l_width = std::max( l_width, join_ids( l_e.first->m_dim_ids_int.data(), l_e.first->m_num_dims, ' ' ).size() );
+    }
+  }
+  // the deepest level has 2^(L-1) slots of two cells each; a slot on level l
+  // spans 2^(L-l) cells and its node sits in the cell left of the middle
+  int64_t const l_num_lvls = (int64_t) l_levels.size();
+  std::string l_out;
+  for( int64_t l_lv = 0; l_lv < l_num_lvls; l_lv++ ) {
+    int64_t const l_span = int64_t( 1 ) << ( l_num_lvls - l_lv );
+    int64_t l_cell = 0;
+    std::string l_line;
+    for( auto const & l_e : l_levels[l_lv] ) {
+      int64_t const l_at = l_e.second * l_span + l_span / 2 - 1;
+      for( ; l_cell < l_at; l_cell++ ) l_line += std::string( l_width, ' ' );
+      std::string l_label = join_ids( l_e.first->m_dim_ids_int.data(), l_e.first->m_num_dims, ' ' );
+      l_label.resize( l_width, ' ' );
+      l_line += l_label;
+      l_cell++;
+    }
+    if( l_lv > 0 ) l_out += '\n';
+    l_out += l_line;
+  }
+  return l_out;
+}

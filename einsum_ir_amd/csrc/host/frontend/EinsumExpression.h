@@ -107,6 +107,27 @@ class einsum_ir::frontend::EinsumExpression {
     void reset_graph();
 
     int64_t num_ops();
+
+    /**
+     * The compiled tree in the einsum tree exchange format, the format that
+     * EinsumTreeAscii::parse_tree reads (reference EinsumExpression.h:218-235):
+     * a leaf is its dim ids "3,2,4"; a node is "[child],[child]->[ids]" or
+     * "[child]->[ids]"; a leaf whose internal dim order differs from its
+     * tensor's is the unary node "[ext ids]->[internal ids]".  For example
+     * "[0,3],[[3,2,4],[4,2]->[1,2,3]]->[0,1,2]".
+     *
+     * @param i_node subtree to write, nullptr: the whole tree.
+     * @return the string, or an error text before compile().
+     **/
+    std::string to_string_exchange_format( backend::EinsumNode const * i_node = nullptr ) const;
+
+    /**
+     * The compiled tree drawn for reading (reference EinsumExpression.h:
+     * 210-216): one line per level, root first, each node's dim ids
+     * separated by spaces in a cell of the widest node's width, and every
+     * node placed centred over the cells its children can take.
+     **/
+    std::string to_string_render() const;
 };
 
 #endif
