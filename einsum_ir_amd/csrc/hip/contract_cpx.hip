@@ -189,23 +189,12 @@ void contract_cpx_kernel( ContractArgs a ) {
 template< typename T >
 int launch_cpx_typed( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a, uint32_t grid,
                       hipStream_t stream ) {
-#define ETIR_CPX_CASE( MA, MB, KA )                                                          \
-  if( ma == MA && mb == MB && kaff == KA ) {                                                 \
-    hipLaunchKernelGGL( ( contract_cpx_kernel< T, MA, MB, KA > ), dim3( grid ), dim3( 256 ), \
-                        0, stream, a );                                                      \
-    return ETIR_SUCCESS;                                                                     \
-  }
-#define ETIR_CPX_CASES( KA )                                                                 \
-  ETIR_CPX_CASE( LOAD_SCALAR, LOAD_SCALAR, KA ) ETIR_CPX_CASE( LOAD_SCALAR, LOAD_VEC_MN, KA ) \
-  ETIR_CPX_CASE( LOAD_SCALAR, LOAD_VEC_K, KA )  ETIR_CPX_CASE( LOAD_VEC_MN, LOAD_SCALAR, KA ) \
-  ETIR_CPX_CASE( LOAD_VEC_MN, LOAD_VEC_MN, KA ) ETIR_CPX_CASE( LOAD_VEC_MN, LOAD_VEC_K, KA )  \
-  ETIR_CPX_CASE( LOAD_VEC_K, LOAD_SCALAR, KA )  ETIR_CPX_CASE( LOAD_VEC_K, LOAD_VEC_MN, KA )  \
-  ETIR_CPX_CASE( LOAD_VEC_K, LOAD_VEC_K, KA )
-  ETIR_CPX_CASES( false )
-  ETIR_CPX_CASES( true )
-#undef ETIR_CPX_CASES
-#undef ETIR_CPX_CASE
-  return fail( ETIR_COMPILATION_FAILED, "contraction: no complex kernel for these load modes" );
+  return with_load_modes( ma, mb, kaff, [&]( auto i_ma, auto i_mb, auto i_kaff ) {
+    hipLaunchKernelGGL( ( contract_cpx_kernel< T, decltype( i_ma )::value, decltype( i_mb )::value,
+                                               decltype( i_kaff )::value > ),
+                        dim3( grid ), dim3( 256 ), 0, stream, a );
+    return int( ETIR_SUCCESS );
+  } );
 }
 
 }  // namespace kern

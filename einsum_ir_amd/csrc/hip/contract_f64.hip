@@ -168,23 +168,12 @@ void contract_f64_kernel( ContractArgs a ) {
 
 int launch_contract_f64_64x64( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
                                uint32_t grid, hipStream_t stream ) {
-#define ETIR_F64_CASE( MA, MB, KA )                                                          \
-  if( ma == MA && mb == MB && kaff == KA ) {                                                 \
-    hipLaunchKernelGGL( ( kern::contract_f64_kernel< MA, MB, KA > ), dim3( grid ), dim3( 256 ), \
-                        0, stream, a );                                                      \
-    return ETIR_SUCCESS;                                                                     \
-  }
-#define ETIR_F64_CASES( KA )                                                                 \
-  ETIR_F64_CASE( LOAD_SCALAR, LOAD_SCALAR, KA ) ETIR_F64_CASE( LOAD_SCALAR, LOAD_VEC_MN, KA ) \
-  ETIR_F64_CASE( LOAD_SCALAR, LOAD_VEC_K, KA )  ETIR_F64_CASE( LOAD_VEC_MN, LOAD_SCALAR, KA ) \
-  ETIR_F64_CASE( LOAD_VEC_MN, LOAD_VEC_MN, KA ) ETIR_F64_CASE( LOAD_VEC_MN, LOAD_VEC_K, KA )  \
-  ETIR_F64_CASE( LOAD_VEC_K, LOAD_SCALAR, KA )  ETIR_F64_CASE( LOAD_VEC_K, LOAD_VEC_MN, KA )  \
-  ETIR_F64_CASE( LOAD_VEC_K, LOAD_VEC_K, KA )
-  ETIR_F64_CASES( false )
-  ETIR_F64_CASES( true )
-#undef ETIR_F64_CASES
-#undef ETIR_F64_CASE
-  return fail( ETIR_COMPILATION_FAILED, "contraction: no f64 kernel for these load modes" );
+  return with_load_modes( ma, mb, kaff, [&]( auto i_ma, auto i_mb, auto i_kaff ) {
+    hipLaunchKernelGGL( ( kern::contract_f64_kernel< decltype( i_ma )::value, decltype( i_mb )::value,
+                                                     decltype( i_kaff )::value > ),
+                        dim3( grid ), dim3( 256 ), 0, stream, a );
+    return int( ETIR_SUCCESS );
+  } );
 }
 
 }  // namespace etir

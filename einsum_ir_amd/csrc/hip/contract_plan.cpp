@@ -33,22 +33,12 @@
 
 namespace etir {
 
-int launch_contract_f32_128x128( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
-                                 uint32_t grid, hipStream_t stream );
-int launch_contract_f32_64x64( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
-                               uint32_t grid, hipStream_t stream );
+int launch_contract_tile( int32_t tile, int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
+                          uint32_t grid, hipStream_t stream );
 int launch_contract_f64_64x64( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
                                uint32_t grid, hipStream_t stream );
 int launch_contract_cpx( bool f64, int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
                          uint32_t grid, hipStream_t stream );
-int launch_contract_bf16_256x256( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
-                                  uint32_t grid, hipStream_t stream );
-int launch_contract_bf16_256x128( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
-                                  uint32_t grid, hipStream_t stream );
-int launch_contract_bf16_128x128( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
-                                  uint32_t grid, hipStream_t stream );
-int launch_contract_bf16_64x64( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a,
-                                uint32_t grid, hipStream_t stream );
 int launch_contract_bf16_dma( int32_t ma, int32_t mb, int32_t variant, ContractArgs const & a,
                               uint32_t grid, hipStream_t stream );
 int launch_contract_kwave( int32_t waves, int32_t kw, ContractArgs const & a, uint32_t grid,
@@ -934,12 +924,14 @@ int launch_contraction( ContractionPlan const & plan,
   uint32_t const l_g = (uint32_t) l_grid;
   int l_err;
   switch( l_tile ) {
-    case TILE_F32_128x128:  l_err = launch_contract_f32_128x128( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
-    case TILE_F32_64x64:    l_err = launch_contract_f32_64x64( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
-    case TILE_BF16_256x256: l_err = launch_contract_bf16_256x256( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
-    case TILE_BF16_256x128: l_err = launch_contract_bf16_256x128( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
-    case TILE_BF16_128x128: l_err = launch_contract_bf16_128x128( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
-    case TILE_BF16_64x64:   l_err = launch_contract_bf16_64x64( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
+    case TILE_F32_128x128:
+    case TILE_F32_64x64:
+    case TILE_BF16_256x256:
+    case TILE_BF16_256x128:
+    case TILE_BF16_128x128:
+    case TILE_BF16_64x64:
+      l_err = launch_contract_tile( plan.tile, l_ma, l_mb, l_kaff, a, l_g, stream );
+      break;
     case TILE_F64_64x64:    l_err = launch_contract_f64_64x64( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_CPX_F32_64x64: l_err = launch_contract_cpx( false, l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_CPX_F64_64x64: l_err = launch_contract_cpx( true, l_ma, l_mb, l_kaff, a, l_g, stream ); break;

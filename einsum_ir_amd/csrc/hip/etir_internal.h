@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <memory>
 #include <string>
+#include <type_traits>
 #include <vector>
 #include <hip/hip_runtime.h>
 #include "../../../include/einsum_ir_hip.h"
@@ -141,6 +142,32 @@ enum LoadMode : int32_t {
   LOAD_VEC_MN = 1,   // 16-byte vectors along the operand's M (or N) index
   LOAD_VEC_K  = 2    // 16-byte vectors along K
 };
+
+// Calls fn( MA, MB, KAFF ) with std::integral_constant arguments equal to the
+// run-time operand load modes and affine-K flag, so that a launcher names its
+// kernel template once and every mode combination is instantiated from it.
+// Unknown modes fail with ETIR_COMPILATION_FAILED.
+template< class Fn >
+int with_load_modes( int32_t ma, int32_t mb, bool kaff, Fn && fn ) {
+  auto pick_k = [&]( auto i_ma, auto i_mb ) -> int {
+    if( kaff ) return fn( i_ma, i_mb, std::true_type() );
+    return fn( i_ma, i_mb, std::false_type() );
+  };
+  auto pick_b = [&]( auto i_ma ) -> int {
+    switch( mb ) {
+      case LOAD_SCALAR: return pick_k( i_ma, std::integral_constant< int32_t, LOAD_SCALAR >() );
+      case LOAD_VEC_MN: return pick_k( i_ma, std::integral_constant< int32_t, LOAD_VEC_MN >() );
+      case LOAD_VEC_K:  return pick_k( i_ma, std::integral_constant< int32_t, LOAD_VEC_K >() );
+      default: return fail( ETIR_COMPILATION_FAILED, "contraction: unknown load mode of operand B" );
+    }
+  };
+  switch( ma ) {
+    case LOAD_SCALAR: return pick_b( std::integral_constant< int32_t, LOAD_SCALAR >() );
+    case LOAD_VEC_MN: return pick_b( std::integral_constant< int32_t, LOAD_VEC_MN >() );
+    case LOAD_VEC_K:  return pick_b( std::integral_constant< int32_t, LOAD_VEC_K >() );
+    default: return fail( ETIR_COMPILATION_FAILED, "contraction: unknown load mode of operand A" );
+  }
+}
 
 enum TileCfg : int32_t {
   TILE_F32_128x128 = 0,
