@@ -53,6 +53,13 @@ def parse_args():
                    help="also time a plain 512 MiB device copy (reference for the PMC byte counters)")
     p.add_argument("--settle", type=float, default=1.0,
                    help="seconds of untimed config-3 launches before its timing (GPU clock settling)")
+    p.add_argument("--summarize", nargs="+", metavar="DIR",
+                   help="print statistics of rocprofv3 CSV output directories (kernel durations and/or "
+                        "counters) over each kernel's last --timed dispatches, then exit (no GPU use)")
+    p.add_argument("--timed", type=int, default=20,
+                   help="with --summarize: dispatches per kernel and grid that form the timed region")
+    p.add_argument("--kernel-filter", default="",
+                   help="with --summarize: only kernels whose name matches this regular expression")
     return p.parse_args()
 
 
@@ -90,6 +97,86 @@ def time_launches(torch, stream, fn, steps, warmup, settle=0.0):
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     return t1 - t0, start.elapsed_time(end) * 1e-3 / steps
+
+
+def _read_csv(path):
+    import csv
+    with open(path, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def summarize_rocprof(dirs, timed, kernel_filter=""):
+    """Statistics of rocprofv3 `--output-format csv` results, per kernel and
+    grid size, over the last `timed` dispatches of each (bench.py's timed
+    launches: every workload launches its kernels only for the clock settle,
+    the warm-up and then the timed steps) and over all of them.  Kernel
+    durations come from run_kernel_trace.csv; counters from
+    run_counter_collection.csv.  FETCH_SIZE / WRITE_SIZE (KiB per dispatch)
+    are scaled to bytes by what the same counter reads for the largest plain
+    device copy in the run (bench.py --calibrate-copy: 512 MiB each way)."""
+    import glob
+    import statistics
+    pat = re.compile(kernel_filter) if kernel_filter else None
+    out = []
+    durations = {}
+    counters = {}          # (kernel, grid) -> counter -> [values in dispatch order]
+    for d in dirs:
+        for path in sorted(glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)):
+            for r in _read_csv(path):
+                grid = int(r["Grid_Size"]) if "Grid_Size" in r else \
+                    int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+                key = (r["Kernel_Name"], grid)
+                durations.setdefault(key, []).append(
+                    (int(r["Start_Timestamp"]), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3))
+        for path in sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)):
+            per = {}
+            for r in _read_csv(path):
+                k = (r["Kernel_Name"], int(r["Grid_Size"]))
+                per.setdefault(k, {}).setdefault(r["Counter_Name"], {})[int(r["Dispatch_Id"])] = \
+                    per.get(k, {}).get(r["Counter_Name"], {}).get(int(r["Dispatch_Id"]), 0.0) + float(r["Counter_Value"])
+            for k, cs in per.items():
+                for c, by_id in cs.items():
+                    counters.setdefault(k, {})[c] = [by_id[i] for i in sorted(by_id)]
+    if durations:
+        out.append(f"# kernel durations (us): the last {timed} dispatches of each kernel and grid, and all of them")
+        out.append(f"{'timed_avg':>10} {'timed_min':>10} {'timed_max':>10} {'all_avg':>10} {'calls':>6} "
+                   f"{'grid':>9}  kernel")
+        rows = []
+        for (name, grid), v in durations.items():
+            if pat and not pat.search(name):
+                continue
+            v.sort()
+            last = [x for _, x in v[-timed:]]
+            rows.append((sum(x for _, x in v), name, grid, last, [x for _, x in v]))
+        for _, name, grid, last, alld in sorted(rows, reverse=True)[:40]:
+            out.append(f"{statistics.mean(last):10.2f} {min(last):10.2f} {max(last):10.2f} "
+                       f"{statistics.mean(alld):10.2f} {len(alld):6d} {grid:9d}  {name[:160]}")
+    if counters:
+        scale = {}
+        for c, expect_kib in (("FETCH_SIZE", 524288.0), ("WRITE_SIZE", 524288.0)):
+            copies = [(g, vals) for (n, g), cs in counters.items() for cc, vals in cs.items()
+                      if cc == c and "copyBuffer" in n]
+            if copies:
+                g, vals = max(copies)
+                scale[c] = expect_kib / statistics.mean(vals)
+                out.append(f"# calibration: the 512 MiB device copy reads {c} = {statistics.mean(vals):.0f} KiB "
+                           f"per dispatch; {c} is scaled by {scale[c]:.4f}")
+        out.append(f"# counters: mean per dispatch over the last {timed} dispatches of each kernel and grid")
+        for (name, grid), cs in sorted(counters.items()):
+            if pat and not pat.search(name):
+                continue
+            out.append(f"## {name[:160]}  grid {grid}  ({max(len(v) for v in cs.values())} dispatches)")
+            for c, vals in sorted(cs.items()):
+                out.append(f"{c}: {statistics.mean(vals[-timed:]):.1f}")
+            rd = statistics.mean(cs["FETCH_SIZE"][-timed:]) * 1024 * scale.get("FETCH_SIZE", 1) if "FETCH_SIZE" in cs else None
+            wr = statistics.mean(cs["WRITE_SIZE"][-timed:]) * 1024 * scale.get("WRITE_SIZE", 1) if "WRITE_SIZE" in cs else None
+            if rd is not None:
+                out.append(f"hbm_read_bytes_per_launch: {rd:.0f}")
+            if wr is not None:
+                out.append(f"hbm_write_bytes_per_launch: {wr:.0f}")
+            if rd is not None and wr is not None:
+                out.append(f"hbm_bytes_per_launch: {rd + wr:.0f}")
+    return "\n".join(out)
 
 
 def traffic_from_profile(name):
@@ -137,6 +224,12 @@ def bench_c2(torch, eir, stream, steps, warmup):
     return res
 
 
+# launches timed per figure for the kernels of a few to a few tens of
+# microseconds (configs 1 and 2, the 4-D permutes): the first launch after
+# an idle stream starts tens of microseconds after its start event, which
+# 20 launches of a 22 us kernel would count as 15 % of the time
+SHORT_STEPS = 200
+
 PERMUTES_4D = [
     ("abcd->dbca", (64, 64, 64, 64)), ("abcd->dbca", (16, 256, 256, 16)), ("abcd->dbca", (8, 512, 512, 8)),
     ("abcd->dcba", (32, 32, 128, 128)), ("abcd->acdb", (128, 16, 64, 128)), ("abcd->bdac", (36, 48, 36, 512)),
@@ -161,7 +254,7 @@ def bench_permutes_4d(torch, eir, stream):
         x = x_all[:n]
         y = y_all[:n]
         plan = eir.PermutePlan(u["sizes"], u["strides_in"], u["strides_out"], dtype=eir.FP32, ktype=eir.COPY)
-        _, per = time_launches(torch, stream, lambda: plan.execute(x, y, stream=stream), 20, 10)
+        _, per = time_launches(torch, stream, lambda: plan.execute(x, y, stream=stream), SHORT_STEPS, 20)
         gbs = 8 * n / per * 1e-9
         rows.append(dict(expr=expr, sizes=list(shape), gbs=round(gbs, 1), frac_hbm_peak=round(gbs / PEAK_HBM_GBS, 4),
                          kernel=plan.describe().split(" dims")[0]))
@@ -441,6 +534,9 @@ def cpu_host_probe():
 
 def main():
     args = parse_args()
+    if args.summarize:
+        print(summarize_rocprof(args.summarize, args.timed, args.kernel_filter))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no "
               "multi-GPU path. Run with --gpus 1.", file=sys.stderr)
@@ -468,7 +564,7 @@ def main():
         c3 = bench_c3(torch, eir, stream, args.steps, args.warmup, settle=args.settle)
         log(f"c3: {c3['desc']}  {c3['per_launch']*1e6:.1f} us/launch")
     if run("c2"):
-        c2 = bench_c2(torch, eir, stream, max(args.steps, 20), args.warmup)
+        c2 = bench_c2(torch, eir, stream, max(args.steps, SHORT_STEPS), args.warmup)
         gbs = c2["bytes"] / c2["per_launch"] * 1e-9
         extra["c2_permute_abcd_dbca_64^4_fp32"] = dict(
             value=round(gbs, 1), unit="GB/s", us_per_launch=round(c2["per_launch"] * 1e6, 2),
@@ -479,7 +575,7 @@ def main():
                                          cases=p4)
         log("permutes 4-D: " + ", ".join(f"{r['expr']}{r['sizes']} {r['gbs']:.0f}" for r in p4))
     if run("c1"):
-        c1 = bench_c1(torch, eir, stream, max(args.steps, 20), args.warmup)
+        c1 = bench_c1(torch, eir, stream, max(args.steps, SHORT_STEPS), args.warmup)
         gf = c1["flops"] / c1["per_launch"] * 1e-9
         extra["c1_abkl_cdkl_fp32"] = dict(value=round(gf, 1), unit="GFLOP/s",
                                           us_per_launch=round(c1["per_launch"] * 1e6, 2),
