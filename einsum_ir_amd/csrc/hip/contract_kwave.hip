@@ -61,6 +61,14 @@ void contract_kwave_kernel( ContractArgs a, int32_t kw ) {
   int const l_r    = l_lane & 15;      // row (A) / column (B) within a 16-row half
   int const l_q    = l_lane >> 4;      // k quarter
 
+  // C offsets: with one C value (no C dims) every table holds the single
+  // offset 0, so no table is read -- a memory round trip less before the
+  // first operand load and before the stores
+  bool const l_one_c = ( a.C == 1 );
+  int64_t const l_ca = l_one_c ? 0 : a.tc_a[l_c];
+  int64_t const l_cb = l_one_c ? 0 : a.tc_b[l_c];
+  int64_t const l_coff = l_one_c ? 0 : a.tc_out[l_c];
+
   // this lane's rows of A / columns of B (two 16-row halves of the tile) at
   // k = 0 (K is affine: k * sk); an affine row table is not read, which saves
   // a memory round trip before the first operand load
@@ -75,8 +83,8 @@ void contract_kwave_kernel( ContractArgs a, int32_t kw ) {
     l_nok[l_x] = l_n < a.N;
     int64_t const l_ra = !l_mok[l_x] ? 0 : ( a.sm_a >= 0 ? int64_t( l_m ) * a.sm_a : a.tm_a[l_m] );
     int64_t const l_rb = !l_nok[l_x] ? 0 : ( a.sn_b >= 0 ? int64_t( l_n ) * a.sn_b : a.tn_b[l_n] );
-    l_pa[l_x] = reinterpret_cast< float const * >( a.a ) + a.tc_a[l_c] + l_ra;
-    l_pb[l_x] = reinterpret_cast< float const * >( a.b ) + a.tc_b[l_c] + l_rb;
+    l_pa[l_x] = reinterpret_cast< float const * >( a.a ) + l_ca + l_ra;
+    l_pb[l_x] = reinterpret_cast< float const * >( a.b ) + l_cb + l_rb;
   }
 
   // output offsets of the elements this thread stores at the end (rows
@@ -150,8 +158,7 @@ void contract_kwave_kernel( ContractArgs a, int32_t kw ) {
   bool const l_read_out  = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_UNDEFINED );
   bool const l_aux_first = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_COPY );
   bool const l_need_aux  = ( a.aux != nullptr ) && ( l_aux_first || a.last_touch == ETIR_KTYPE_ADD );
-  int64_t const l_coff = a.tc_out[l_c];
-  int64_t const l_caux = l_need_aux ? a.tc_aux[l_c] : 0;
+  int64_t const l_caux = ( l_need_aux && !l_one_c ) ? a.tc_aux[l_c] : 0;
 #pragma unroll
   for( int l_u = 0; l_u < NU; l_u++ ) {
     int const l_e = threadIdx.x + T * l_u;

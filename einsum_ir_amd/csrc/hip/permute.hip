@@ -68,6 +68,16 @@ struct alignas( 4 * sizeof( T ) ) Vec4 { T v[4]; };
 
 constexpr int kTile = 64;
 constexpr int kThreads = 256;
+
+// REG4 takes permutations whose shorter unit-stride dim is at most this long
+// (ETIR_PERM_REG4_MAX_SHORT overrides, for measurements), and those whose two
+// unit-stride dims are at most 32 long and whole 128-byte lines each (fp32
+// 32 x 32: 74 % of HBM peak against 58 % tiled; 24 x 32, whose 96-byte input
+// runs split lines: 47 % against 53 % tiled)
+inline int64_t reg4_max_short() {
+  char const * l_env = std::getenv( "ETIR_PERM_REG4_MAX_SHORT" );
+  return l_env ? std::atoi( l_env ) : 16;
+}
 constexpr int kPermTileMax = 4096;   // elements of a TILED tile
 
 // 16-byte store that does not keep the line in the caches (the output is
@@ -298,8 +308,8 @@ void perm_tiled_kernel( PermArgs a ) {
 //          store them: one store instruction covers a contiguous run of the
 //          output as long as the dims allow.
 // All LDS accesses are 16 bytes; no tables.
-template< typename T, int CPT >
-__global__ __launch_bounds__( kThreads )
+template< typename T, int CPT, int NT >
+__global__ __launch_bounds__( NT )
 void perm_reg4_kernel( PermArgs a ) {
   extern __shared__ __attribute__( ( aligned( 16 ) ) ) char l_lds_raw[];
   Vec4< T > * l_slots = reinterpret_cast< Vec4< T > * >( l_lds_raw );
@@ -378,7 +388,7 @@ void perm_reg4_kernel( PermArgs a ) {
     int32_t const l_si = int32_t( a.size_i );
     int32_t const l_nslots = l_si * l_ct * l_nog;
     bool const l_c_inner = a.c_s_out < a.s_out_i;
-    for( int32_t l_s = threadIdx.x; l_s < l_nslots; l_s += kThreads ) {
+    for( int32_t l_s = threadIdx.x; l_s < l_nslots; l_s += NT ) {
       int32_t const l_og = l_s % l_nog;
       int32_t const l_s2 = l_s / l_nog;
       int32_t const l_cl = l_c_inner ? l_s2 % l_ct : l_s2 / l_si;
@@ -477,14 +487,23 @@ int launch_typed( PermutePlan const & p,
       return fail( ETIR_UNDEFINED_ERROR, "permute: grid too large" );
     }
     std::size_t const l_lds = std::size_t( a.c_chunk ) * a.slot_pc * 4 * sizeof( T );
-    if( p.reg4_cpt == 4 ) {
-      hipLaunchKernelGGL( ( perm_reg4_kernel< T, 4 > ), dim3( (uint32_t) l_blocks ), dim3( kThreads ), l_lds, stream, a );
+    if( p.reg4_threads == 512 ) {
+      hipLaunchKernelGGL( ( perm_reg4_kernel< T, 1, 512 > ), dim3( (uint32_t) l_blocks ), dim3( 512 ), l_lds, stream, a );
+    }
+    else if( p.reg4_threads == 128 ) {
+      hipLaunchKernelGGL( ( perm_reg4_kernel< T, 1, 128 > ), dim3( (uint32_t) l_blocks ), dim3( 128 ), l_lds, stream, a );
+    }
+    else if( p.reg4_threads == 64 ) {
+      hipLaunchKernelGGL( ( perm_reg4_kernel< T, 1, 64 > ), dim3( (uint32_t) l_blocks ), dim3( 64 ), l_lds, stream, a );
+    }
+    else if( p.reg4_cpt == 4 ) {
+      hipLaunchKernelGGL( ( perm_reg4_kernel< T, 4, kThreads > ), dim3( (uint32_t) l_blocks ), dim3( kThreads ), l_lds, stream, a );
     }
     else if( p.reg4_cpt == 2 ) {
-      hipLaunchKernelGGL( ( perm_reg4_kernel< T, 2 > ), dim3( (uint32_t) l_blocks ), dim3( kThreads ), l_lds, stream, a );
+      hipLaunchKernelGGL( ( perm_reg4_kernel< T, 2, kThreads > ), dim3( (uint32_t) l_blocks ), dim3( kThreads ), l_lds, stream, a );
     }
     else {
-      hipLaunchKernelGGL( ( perm_reg4_kernel< T, 1 > ), dim3( (uint32_t) l_blocks ), dim3( kThreads ), l_lds, stream, a );
+      hipLaunchKernelGGL( ( perm_reg4_kernel< T, 1, kThreads > ), dim3( (uint32_t) l_blocks ), dim3( kThreads ), l_lds, stream, a );
     }
   }
   else if( p.mode == PermMode::TRANSPOSE ) {
@@ -901,7 +920,10 @@ int plan_permute( int64_t         num_dims,
 
   if(    l_dim_i >= 0 && l_dim_o >= 0 && l_dim_i != l_dim_o
       && plan.size[l_dim_i] % 4 == 0 && plan.size[l_dim_o] % 4 == 0
-      && std::min( plan.size[l_dim_i], plan.size[l_dim_o] ) <= 16
+      && (    std::min( plan.size[l_dim_i], plan.size[l_dim_o] ) <= reg4_max_short()
+           || (    std::max( plan.size[l_dim_i], plan.size[l_dim_o] ) <= 32
+                && ( plan.size[l_dim_i] * plan.elem_bytes ) % 128 == 0
+                && ( plan.size[l_dim_o] * plan.elem_bytes ) % 128 == 0 ) )
       && ( plan.size[l_dim_i] / 4 ) * ( plan.size[l_dim_o] / 4 ) <= kThreads
       && std::getenv( "ETIR_NO_PERM_REG4" ) == nullptr ) {
     // a short unit-stride dim: 4 x 4 register transposes.  The dim that
@@ -929,15 +951,28 @@ int plan_permute( int64_t         num_dims,
     a.c_s_in  = l_dc >= 0 ? plan.s_in[l_dc] : 0;
     a.c_s_out = l_dc >= 0 ? plan.s_out[l_dc] : 0;
     // a workgroup's tile: all of i and o, c_chunk values of c -- one value
-    // per thread group of (i/4 x o/4) threads.  Two or four passes of the
-    // threads (ETIR_PERM_REG4_CPT) give longer runs of (c, i) but measured
-    // slower on every 4-D shape tried (more LDS per workgroup, fewer resident)
-    a.c_chunk = (int32_t) std::max< int64_t >( 1, kThreads / ( ( a.size_i / 4 ) * ( a.size_o / 4 ) ) );
+    // per thread group of (i/4 x o/4) threads, in the smallest workgroup of
+    // 64, 128 or 256 threads that holds one value's blocks: small workgroups
+    // measured faster than large ones on every 4-D shape (16,256,256,16 fp32:
+    // 74 % of HBM peak at 64 threads, 62 % at 256, 54 % at 512).  Planner
+    // options: ETIR_PERM_REG4_THREADS (64 ... 512) and ETIR_PERM_REG4_CPT, two
+    // or four passes of 256 threads over c (longer runs of (c, i), measured
+    // slower too)
+    int64_t const l_blocks_c = ( a.size_i / 4 ) * ( a.size_o / 4 );
+    plan.reg4_threads = l_blocks_c <= 64 ? 64 : ( l_blocks_c <= 128 ? 128 : kThreads );
     plan.reg4_cpt = 1;
+    if( char const * l_env = std::getenv( "ETIR_PERM_REG4_THREADS" ) ) {
+      int const l_t = std::atoi( l_env );
+      if( ( l_t == 512 || l_t == 256 || l_t == 128 || l_t == 64 ) && l_t >= l_blocks_c ) plan.reg4_threads = l_t;
+    }
     if( char const * l_env = std::getenv( "ETIR_PERM_REG4_CPT" ) ) {
       int const l_v = std::atoi( l_env );
-      plan.reg4_cpt = ( l_v == 2 || l_v == 4 ) ? l_v : 1;
+      if( l_v == 2 || l_v == 4 ) {
+        plan.reg4_cpt = l_v;
+        plan.reg4_threads = kThreads;
+      }
     }
+    a.c_chunk = (int32_t) std::max< int64_t >( 1, plan.reg4_threads / l_blocks_c );
     a.c_chunk *= plan.reg4_cpt;
     // LDS slot pitches: simulate both phases' 16-byte accesses (eight lanes
     // per LDS cycle, a slot covers 4 of the 64 four-byte banks) and take the

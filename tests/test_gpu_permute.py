@@ -161,11 +161,43 @@ def test_permute_reg4_add(torch_cuda, oracle, expr, sizes, dtype):
 
 @pytest.mark.parametrize("cpt", ["2", "4"])
 def test_permute_reg4_passes(torch_cuda, oracle, monkeypatch, cpt):
-    """Two and four passes of the threads over c (a planner option)."""
+    """Two and four passes of 256 threads over c (a planner option)."""
     monkeypatch.setenv("ETIR_PERM_REG4_CPT", cpt)
     for expr, sizes in REG4_CASES[:3]:
         desc = _check(torch_cuda, oracle, expr, sizes, seed=int(cpt))
-        assert "reg4" in desc
+        assert f"t=256x{cpt}" in desc, desc
+
+
+@pytest.mark.parametrize("threads", ["64", "128", "256", "512"])
+def test_permute_reg4_workgroup_sizes(torch_cuda, oracle, monkeypatch, threads):
+    """Every workgroup size of the REG4 kernel (a planner option, taken when
+    it holds the blocks of one value of c)."""
+    monkeypatch.setenv("ETIR_PERM_REG4_THREADS", threads)
+    for expr, sizes in REG4_CASES[:4]:
+        desc = _check(torch_cuda, oracle, expr, sizes, dtype=eir.FP64, seed=int(threads))
+        assert f"t={threads}x1" in desc, desc
+
+
+@pytest.mark.parametrize("dtype,mode", [(eir.FP32, "reg4"), (eir.FP64, "reg4"), (eir.BF16, "tiled")])
+def test_permute_32_wide_unit_dims(torch_cuda, oracle, dtype, mode):
+    """Unit-stride dims of 32 on both sides take REG4 when each is a whole
+    number of 128-byte lines (fp32, fp64) and the tiled kernel otherwise."""
+    desc = _check(torch_cuda, oracle, "abcd->dbca", dict(a=32, b=5, c=6, d=32), dtype=dtype, seed=32)
+    assert mode in desc, desc
+    desc = _check(torch_cuda, oracle, "abcd->cbda", dict(a=32, b=3, c=7, d=24), dtype=dtype, seed=24)
+    assert "tiled" in desc, desc
+
+
+@pytest.mark.parametrize("expr,sizes,threads", [
+    ("abcd->dbca", dict(a=16, b=4, c=32, d=16), 64),      # 16 blocks of 4 x 4 per value of c
+    ("abc->cba", dict(a=128, b=3, c=16), 128),             # 128 blocks
+    ("abc->cba", dict(a=256, b=3, c=16), 256),             # 256 blocks
+])
+def test_permute_reg4_default_workgroup(torch_cuda, oracle, expr, sizes, threads):
+    """The default is the smallest workgroup of 64, 128 or 256 threads that
+    holds one value of c's blocks."""
+    desc = _check(torch_cuda, oracle, expr, sizes, seed=threads)
+    assert f"t={threads}x1" in desc, desc
 
 
 def test_permute_4d_bench_shapes(torch_cuda):
