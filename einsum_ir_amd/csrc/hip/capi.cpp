@@ -155,7 +155,8 @@ int etir_hip_plan_describe( etir_plan_t plan, char * buf, int64_t len ) {
     if( p.mode == etir::PermMode::REG4 ) {
       l_s += " i=" + std::to_string( p.args.size_i ) + " o=" + std::to_string( p.args.size_o )
            + " c=" + std::to_string( p.args.c_size ) + "/" + std::to_string( p.args.c_chunk )
-           + " t=" + std::to_string( p.reg4_threads ) + "x" + std::to_string( p.reg4_cpt );
+           + " t=" + std::to_string( p.reg4_threads ) + "x" + std::to_string( p.reg4_cpt )
+           + ( p.reg4_direct ? " direct" : "" );
     }
   }
   std::strncpy( buf, l_s.c_str(), (std::size_t) len - 1 );

@@ -104,7 +104,8 @@ struct PermArgs {
 struct PermutePlan {
   PermMode mode = PermMode::GATHER;
   int32_t  reg4_cpt = 1;                 // REG4: passes of the threads over c per workgroup (1, 2 or 4)
-  int32_t  reg4_threads = 256;           // REG4: threads per workgroup (256 or 512)
+  int32_t  reg4_threads = 256;           // REG4: threads per workgroup (64 ... 512)
+  bool     reg4_direct = false;          // REG4: rows stored from registers, no LDS exchange
   int32_t  dtype = ETIR_FP32;
   int32_t  ktype = ETIR_KTYPE_COPY;
   int64_t  elem_bytes = 4;

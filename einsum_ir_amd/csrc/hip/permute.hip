@@ -308,7 +308,28 @@ void perm_tiled_kernel( PermArgs a ) {
 //          store them: one store instruction covers a contiguous run of the
 //          output as long as the dims allow.
 // All LDS accesses are 16 bytes; no tables.
-template< typename T, int CPT, int NT >
+// one 16-byte output row of REG4 (COPY or ADD; element stores when the
+// output's rows are not 16-byte aligned)
+template< typename T >
+__device__ inline void reg4_store( PermArgs const & a, T * p, Vec4< T > w ) {
+  if( a.vec_ok ) {
+    if( a.add ) {
+      Vec4< T > const l_old = *reinterpret_cast< Vec4< T > const * >( p );
+#pragma unroll
+      for( int l_r = 0; l_r < 4; l_r++ ) w.v[l_r] = Elem< T >::add( l_old.v[l_r], w.v[l_r] );
+    }
+    store_stream( reinterpret_cast< Vec4< T > * >( p ), w );
+  }
+  else {
+#pragma unroll
+    for( int l_r = 0; l_r < 4; l_r++ ) p[l_r] = a.add ? Elem< T >::add( p[l_r], w.v[l_r] ) : w.v[l_r];
+  }
+}
+
+// DIRECT: each thread stores its four transposed rows itself, without the
+// LDS exchange -- taken when the rows that one store instruction covers
+// (o, continued by c) are whole 128-byte lines anyway.
+template< typename T, int CPT, int NT, bool DIRECT >
 __global__ __launch_bounds__( NT )
 void perm_reg4_kernel( PermArgs a ) {
   extern __shared__ __attribute__( ( aligned( 16 ) ) ) char l_lds_raw[];
@@ -375,10 +396,17 @@ void perm_reg4_kernel( PermArgs a ) {
         Vec4< T > l_w;
 #pragma unroll
         for( int l_r = 0; l_r < 4; l_r++ ) l_w.v[l_r] = l_v[l_u][l_r][l_q];
-        l_slots[( l_cl + l_u * l_cw ) * l_pc + ( 4 * l_ig + l_q ) * l_pi + l_og] = l_w;
+        if constexpr( DIRECT ) {
+          int64_t const l_c = l_cbase + l_cl + l_u * l_cw;
+          reg4_store( a, l_out + l_c * a.c_s_out + int64_t( 4 * l_ig + l_q ) * a.s_out_i + 4 * l_og, l_w );
+        }
+        else {
+          l_slots[( l_cl + l_u * l_cw ) * l_pc + ( 4 * l_ig + l_q ) * l_pi + l_og] = l_w;
+        }
       }
     }
   }
+  if constexpr( DIRECT ) return;
   __syncthreads();
   // LDS -> output: the tile's 16-byte slots in output order (o groups
   // fastest, then whichever of i and c has the smaller output stride), so
@@ -395,20 +423,8 @@ void perm_reg4_kernel( PermArgs a ) {
       int32_t const l_i  = l_c_inner ? l_s2 / l_ct : l_s2 % l_si;
       int64_t const l_c = l_cbase + l_cl;
       if( l_c >= a.c_size ) continue;
-      Vec4< T > l_w = l_slots[l_cl * l_pc + l_i * l_pi + l_og];
-      T * l_pq = l_out + l_c * a.c_s_out + int64_t( l_i ) * a.s_out_i + 4 * l_og;
-      if( a.vec_ok ) {
-        if( a.add ) {
-          Vec4< T > const l_old = *reinterpret_cast< Vec4< T > const * >( l_pq );
-#pragma unroll
-          for( int l_r = 0; l_r < 4; l_r++ ) l_w.v[l_r] = Elem< T >::add( l_old.v[l_r], l_w.v[l_r] );
-        }
-        store_stream( reinterpret_cast< Vec4< T > * >( l_pq ), l_w );
-      }
-      else {
-#pragma unroll
-        for( int l_r = 0; l_r < 4; l_r++ ) l_pq[l_r] = a.add ? Elem< T >::add( l_pq[l_r], l_w.v[l_r] ) : l_w.v[l_r];
-      }
+      reg4_store( a, l_out + l_c * a.c_s_out + int64_t( l_i ) * a.s_out_i + 4 * l_og,
+                  l_slots[l_cl * l_pc + l_i * l_pi + l_og] );
     }
   }
 }
@@ -487,24 +503,22 @@ int launch_typed( PermutePlan const & p,
       return fail( ETIR_UNDEFINED_ERROR, "permute: grid too large" );
     }
     std::size_t const l_lds = std::size_t( a.c_chunk ) * a.slot_pc * 4 * sizeof( T );
-    if( p.reg4_threads == 512 ) {
-      hipLaunchKernelGGL( ( perm_reg4_kernel< T, 1, 512 > ), dim3( (uint32_t) l_blocks ), dim3( 512 ), l_lds, stream, a );
-    }
-    else if( p.reg4_threads == 128 ) {
-      hipLaunchKernelGGL( ( perm_reg4_kernel< T, 1, 128 > ), dim3( (uint32_t) l_blocks ), dim3( 128 ), l_lds, stream, a );
-    }
-    else if( p.reg4_threads == 64 ) {
-      hipLaunchKernelGGL( ( perm_reg4_kernel< T, 1, 64 > ), dim3( (uint32_t) l_blocks ), dim3( 64 ), l_lds, stream, a );
-    }
-    else if( p.reg4_cpt == 4 ) {
-      hipLaunchKernelGGL( ( perm_reg4_kernel< T, 4, kThreads > ), dim3( (uint32_t) l_blocks ), dim3( kThreads ), l_lds, stream, a );
-    }
-    else if( p.reg4_cpt == 2 ) {
-      hipLaunchKernelGGL( ( perm_reg4_kernel< T, 2, kThreads > ), dim3( (uint32_t) l_blocks ), dim3( kThreads ), l_lds, stream, a );
-    }
-    else {
-      hipLaunchKernelGGL( ( perm_reg4_kernel< T, 1, kThreads > ), dim3( (uint32_t) l_blocks ), dim3( kThreads ), l_lds, stream, a );
-    }
+    dim3 const l_grid( (uint32_t) l_blocks );
+    auto launch = [&]( auto i_kernel, int i_threads, bool i_direct ) {
+      hipLaunchKernelGGL( i_kernel, l_grid, dim3( i_threads ), i_direct ? 0 : l_lds, stream, a );
+    };
+    bool const l_d = p.reg4_direct;
+    if( p.reg4_cpt == 4 )                                  launch( perm_reg4_kernel< T, 4, kThreads, false >, kThreads, false );
+    else if( p.reg4_cpt == 2 )                             launch( perm_reg4_kernel< T, 2, kThreads, false >, kThreads, false );
+    else if( p.reg4_threads == 64 && l_d )                 launch( perm_reg4_kernel< T, 1, 64, true >, 64, true );
+    else if( p.reg4_threads == 64 )                        launch( perm_reg4_kernel< T, 1, 64, false >, 64, false );
+    else if( p.reg4_threads == 128 && l_d )                launch( perm_reg4_kernel< T, 1, 128, true >, 128, true );
+    else if( p.reg4_threads == 128 )                       launch( perm_reg4_kernel< T, 1, 128, false >, 128, false );
+    else if( p.reg4_threads == kThreads && l_d )           launch( perm_reg4_kernel< T, 1, kThreads, true >, kThreads, true );
+    else if( p.reg4_threads == kThreads )                  launch( perm_reg4_kernel< T, 1, kThreads, false >, kThreads, false );
+    else if( p.reg4_threads == 512 && l_d )                launch( perm_reg4_kernel< T, 1, 512, true >, 512, true );
+    else if( p.reg4_threads == 512 )                       launch( perm_reg4_kernel< T, 1, 512, false >, 512, false );
+    else return fail( ETIR_UNDEFINED_ERROR, "permute: no REG4 kernel for this workgroup size" );
   }
   else if( p.mode == PermMode::TRANSPOSE ) {
     int64_t l_blocks = a.tiles_i * a.tiles_o * a.num_batch_total;
@@ -973,6 +987,19 @@ int plan_permute( int64_t         num_dims,
       }
     }
     a.c_chunk = (int32_t) std::max< int64_t >( 1, plan.reg4_threads / l_blocks_c );
+    // stores straight from registers when the output run that one row of
+    // blocks covers (o, continued by the chunk of c when c continues the
+    // output's run) is whole 128-byte lines and both unit dims are at most
+    // 16 (fp32 16,256,256,16: 77 % of HBM peak against 74 % through LDS; at
+    // 32 x 32 the lanes of one store instruction spread over eight rows and
+    // the LDS exchange is faster, 74 % against 65 %)
+    int64_t const l_direct_run = a.size_o * plan.elem_bytes
+                               * ( ( l_dc >= 0 && plan.s_out[l_dc] == a.size_o ) ? a.c_chunk : 1 );
+    plan.reg4_direct = ( l_direct_run % 128 == 0 && plan.reg4_cpt == 1
+                         && std::max( a.size_i, a.size_o ) <= 16 );
+    if( char const * l_env = std::getenv( "ETIR_PERM_REG4_DIRECT" ) ) {
+      plan.reg4_direct = plan.reg4_direct && std::atoi( l_env ) != 0;
+    }
     a.c_chunk *= plan.reg4_cpt;
     // LDS slot pitches: simulate both phases' 16-byte accesses (eight lanes
     // per LDS cycle, a slot covers 4 of the 64 four-byte banks) and take the

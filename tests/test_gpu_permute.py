@@ -188,6 +188,18 @@ def test_permute_32_wide_unit_dims(torch_cuda, oracle, dtype, mode):
     assert "tiled" in desc, desc
 
 
+@pytest.mark.parametrize("dtype", [eir.FP32, eir.FP64, eir.BF16])
+@pytest.mark.parametrize("direct", ["0", "1"])
+def test_permute_reg4_direct_stores(torch_cuda, oracle, monkeypatch, dtype, direct):
+    """Rows stored from registers (no LDS exchange) where the planner takes
+    them, and the exchange where it is switched off; COPY and ADD."""
+    monkeypatch.setenv("ETIR_PERM_REG4_DIRECT", direct)
+    for expr, sizes in [REG4_CASES[0], REG4_CASES[1], REG4_CASES[2]]:
+        desc = _check(torch_cuda, oracle, expr, sizes, dtype=dtype, seed=7)
+        assert ("direct" in desc) == (direct == "1"), desc
+        _check(torch_cuda, oracle, expr, sizes, dtype=dtype, ktype=eir.ADD, seed=8)
+
+
 @pytest.mark.parametrize("expr,sizes,threads", [
     ("abcd->dbca", dict(a=16, b=4, c=32, d=16), 64),      # 16 blocks of 4 x 4 per value of c
     ("abc->cba", dict(a=128, b=3, c=16), 128),             # 128 blocks
