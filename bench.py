@@ -210,6 +210,33 @@ def bench_c3(torch, eir, stream, steps, warmup, settle=1.0):
     return res
 
 
+def bench_c3_comparators(torch, stream, steps, warmup):
+    """Reference points for config 3 from the same run: its FLOPs as one
+    batched GEMM through torch.bmm (hipBLASLt; 8 x [4096 x 1024] x
+    [1024 x 4096], bf16 in, fp32 out; operands contiguous, K-contiguous A and
+    N-contiguous B, not config 3's layout), and the 537 MB fp32 output written
+    alone (torch fill_, the store floor of any kernel of this shape)."""
+    g = torch.Generator(device="cuda").manual_seed(33)
+    a = (torch.rand(8, 4096, 1024, device="cuda", generator=g) * 2 - 1).to(torch.bfloat16)
+    b = (torch.rand(8, 1024, 4096, device="cuda", generator=g) * 2 - 1).to(torch.bfloat16)
+    o = torch.empty(8, 4096, 4096, device="cuda", dtype=torch.float32)
+    flops = 2 * 8 * 4096 * 4096 * 1024
+    res = {}
+    try:
+        _, per = time_launches(torch, stream, lambda: torch.bmm(a, b, out_dtype=torch.float32), steps, warmup,
+                               settle=0.5)
+        res["torch_bmm_bf16_fp32out"] = dict(us_per_launch=round(per * 1e6, 2),
+                                             tflops=round(flops / per * 1e-12, 1),
+                                             frac_bf16_peak=round(flops / per * 1e-12 / PEAK_BF16_TFLOPS, 4))
+    except Exception as e:   # an older torch without out_dtype
+        res["torch_bmm_bf16_fp32out"] = f"unavailable: {e}"
+    _, per = time_launches(torch, stream, lambda: o.fill_(1.5), steps, warmup)
+    res["fill_fp32_output_537MB"] = dict(us_per_launch=round(per * 1e6, 2),
+                                         gbs=round(o.numel() * 4 / per * 1e-9, 1))
+    del a, b, o
+    return res
+
+
 def bench_c2(torch, eir, stream, steps, warmup):
     sizes = dict(a=64, b=64, c=64, d=64)
     u = eir.unary_dims("abcd->dbca", sizes)
@@ -563,6 +590,8 @@ def main():
     if run("c3"):
         c3 = bench_c3(torch, eir, stream, args.steps, args.warmup, settle=args.settle)
         log(f"c3: {c3['desc']}  {c3['per_launch']*1e6:.1f} us/launch")
+        extra["c3_reference_points"] = bench_c3_comparators(torch, stream, args.steps, args.warmup)
+        log(f"c3 reference points: {extra['c3_reference_points']}")
     if run("c2"):
         c2 = bench_c2(torch, eir, stream, max(args.steps, SHORT_STEPS), args.warmup)
         gbs = c2["bytes"] / c2["per_launch"] * 1e-9
