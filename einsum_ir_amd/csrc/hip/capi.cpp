@@ -155,6 +155,7 @@ int etir_hip_plan_describe( etir_plan_t plan, char * buf, int64_t len ) {
     if( p.mode == etir::PermMode::REG4 ) {
       l_s += " i=" + std::to_string( p.args.size_i ) + " o=" + std::to_string( p.args.size_o )
            + " c=" + std::to_string( p.args.c_size ) + "/" + std::to_string( p.args.c_chunk )
+           + " b=" + std::to_string( p.reg4_vb )
            + " t=" + std::to_string( p.reg4_threads ) + "x" + std::to_string( p.reg4_cpt )
            + ( p.reg4_direct ? " direct" : "" );
     }

@@ -96,6 +96,7 @@ struct PermArgs {
   int64_t  c_s_in;
   int64_t  c_s_out;
   int32_t  c_chunk;
+  int32_t  vec_wide;  // COPY_VEC / FILL, bf16: 8-element (16-byte) vectors allowed
   int32_t  slot_pi;   // REG4: LDS pitch (16-byte slots) of i and of c
   int32_t  slot_pc;
   int32_t  nt_store;  // TRANSPOSE: streaming (non-temporal) output stores
@@ -106,6 +107,7 @@ struct PermutePlan {
   int32_t  reg4_cpt = 1;                 // REG4: passes of the threads over c per workgroup (1, 2 or 4)
   int32_t  reg4_threads = 256;           // REG4: threads per workgroup (64 ... 512)
   bool     reg4_direct = false;          // REG4: rows stored from registers, no LDS exchange
+  int32_t  reg4_vb = 4;                  // REG4: block side (bf16: 8 when both unit dims allow)
   int32_t  dtype = ETIR_FP32;
   int32_t  ktype = ETIR_KTYPE_COPY;
   int64_t  elem_bytes = 4;

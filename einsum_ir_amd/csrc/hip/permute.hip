@@ -66,6 +66,11 @@ template<> struct Elem< uint16_t > {  // bf16 bits
 template< typename T >
 struct alignas( 4 * sizeof( T ) ) Vec4 { T v[4]; };
 
+// N consecutive elements moved as one vector
+template< typename T, int N >
+struct alignas( N * sizeof( T ) ) VecN { T v[N]; };
+
+
 constexpr int kTile = 64;
 constexpr int kThreads = 256;
 
@@ -82,9 +87,9 @@ constexpr int kPermTileMax = 4096;   // elements of a TILED tile
 
 // 16-byte store that does not keep the line in the caches (the output is
 // written once and not read again by the kernel)
-template< typename T >
-__device__ inline void store_stream( Vec4< T > * p, Vec4< T > const & v ) {
-  if constexpr( sizeof( Vec4< T > ) == 16 ) {
+template< typename V >
+__device__ inline void store_stream( V * p, V const & v ) {
+  if constexpr( sizeof( V ) == 16 ) {
     typedef uint32_t u4 __attribute__( ( ext_vector_type( 4 ) ) );
     __builtin_nontemporal_store( __builtin_bit_cast( u4, v ), reinterpret_cast< u4 * >( p ) );
   }
@@ -308,34 +313,53 @@ void perm_tiled_kernel( PermArgs a ) {
 //          store them: one store instruction covers a contiguous run of the
 //          output as long as the dims allow.
 // All LDS accesses are 16 bytes; no tables.
-// one 16-byte output row of REG4 (COPY or ADD; element stores when the
-// output's rows are not 16-byte aligned)
-template< typename T >
-__device__ inline void reg4_store( PermArgs const & a, T * p, Vec4< T > w ) {
+// one output row of a REG4 block (COPY or ADD; element stores when the
+// output's rows are not vector-aligned)
+template< typename T, int VB >
+__device__ inline void reg4_store( PermArgs const & a, T * p, VecN< T, VB > w ) {
   if( a.vec_ok ) {
     if( a.add ) {
-      Vec4< T > const l_old = *reinterpret_cast< Vec4< T > const * >( p );
+      VecN< T, VB > const l_old = *reinterpret_cast< VecN< T, VB > const * >( p );
 #pragma unroll
-      for( int l_r = 0; l_r < 4; l_r++ ) w.v[l_r] = Elem< T >::add( l_old.v[l_r], w.v[l_r] );
+      for( int l_r = 0; l_r < VB; l_r++ ) w.v[l_r] = Elem< T >::add( l_old.v[l_r], w.v[l_r] );
     }
-    store_stream( reinterpret_cast< Vec4< T > * >( p ), w );
+    store_stream( reinterpret_cast< VecN< T, VB > * >( p ), w );
   }
   else {
 #pragma unroll
-    for( int l_r = 0; l_r < 4; l_r++ ) p[l_r] = a.add ? Elem< T >::add( p[l_r], w.v[l_r] ) : w.v[l_r];
+    for( int l_r = 0; l_r < VB; l_r++ ) p[l_r] = a.add ? Elem< T >::add( p[l_r], w.v[l_r] ) : w.v[l_r];
   }
 }
 
-// DIRECT: each thread stores its four transposed rows itself, without the
-// LDS exchange -- taken when the rows that one store instruction covers
-// (o, continued by c) are whole 128-byte lines anyway.
-template< typename T, int CPT, int NT, bool DIRECT >
+// Short unit-stride dims (REG4): VB x VB blocks (8 for bf16 when both dims
+// allow it, else 4) transposed in registers, whole block rows
+// exchanged through LDS.  i is the input's unit-stride dim, o the output's,
+// c the dim walked next (the one that continues the input's run, or the
+// output's); a workgroup takes all of i and o and c_chunk values of c.
+//   read:  thread (ig, c, og) -- ig fastest -- loads the VB block rows
+//          in[o = VB og + r][c][i = VB ig .. VB ig + VB - 1], r = 0..VB-1:
+//          one load instruction of a wave covers one input row o over a
+//          contiguous run of (c, i);
+//   swap:  the block is transposed by renaming registers (for bf16 the
+//          compiler packs the 16-bit halves with v_perm), and its VB output
+//          rows out[i = VB ig + q][c][o = VB og .. +VB-1] go to LDS at
+//          [c][i][og] (one slot each; the pitches of i and c are padded as the
+//          planner finds free of bank conflicts for both phases);
+//   write: the threads walk the slots in output order (o groups fastest,
+//          then i or c, whichever is nearer the output's unit stride) and
+//          store them: one store instruction covers a contiguous run of the
+//          output as long as the dims allow.
+// DIRECT: each thread stores its block rows itself, without the LDS exchange
+// -- taken when the rows that one store instruction covers (o, continued by
+// c) are whole 128-byte lines anyway.  No tables.
+template< typename T, int VB, int CPT, int NT, bool DIRECT >
 __global__ __launch_bounds__( NT )
 void perm_reg4_kernel( PermArgs a ) {
+  typedef VecN< T, VB > Row;
   extern __shared__ __attribute__( ( aligned( 16 ) ) ) char l_lds_raw[];
-  Vec4< T > * l_slots = reinterpret_cast< Vec4< T > * >( l_lds_raw );
-  int32_t const l_nig = int32_t( a.size_i / 4 );
-  int32_t const l_nog = int32_t( a.size_o / 4 );
+  Row * l_slots = reinterpret_cast< Row * >( l_lds_raw );
+  int32_t const l_nig = int32_t( a.size_i / VB );
+  int32_t const l_nog = int32_t( a.size_o / VB );
   int32_t const l_cw  = a.c_chunk / CPT;             // values of c per pass of the threads
   int32_t const l_ct  = a.c_chunk;                   // values of c per workgroup
   int32_t const l_pi  = a.slot_pi;                   // slots per i (nog + padding)
@@ -358,60 +382,60 @@ void perm_reg4_kernel( PermArgs a ) {
   T       * l_out = reinterpret_cast< T * >( a.out ) + l_off_out;
   bool const l_active = int32_t( threadIdx.x ) < l_used;
 
-  // read (all CPT passes' loads in flight together) + register transpose + LDS
+  // read (all CPT passes' loads in flight together) + register transpose
+  // + LDS (or, DIRECT, the stores)
   {
     int32_t l_x = threadIdx.x;
     int32_t const l_ig = l_x % l_nig;
     l_x /= l_nig;
     int32_t const l_cl = l_x % l_cw;
     int32_t const l_og = l_x / l_cw;
-    T l_v[CPT][4][4];
+    T l_v[CPT][VB][VB];
     bool l_ok[CPT];
 #pragma unroll
     for( int l_u = 0; l_u < CPT; l_u++ ) {
       int64_t const l_c = l_cbase + l_cl + l_u * l_cw;
       l_ok[l_u] = l_active && l_c < a.c_size;
       if( !l_ok[l_u] ) continue;
-      T const * l_p = l_in + l_c * a.c_s_in + int64_t( 4 * l_og ) * a.s_in_o + 4 * l_ig;
+      T const * l_p = l_in + l_c * a.c_s_in + int64_t( VB * l_og ) * a.s_in_o + VB * l_ig;
       if( a.vec_ok ) {
 #pragma unroll
-        for( int l_r = 0; l_r < 4; l_r++ ) {
-          Vec4< T > const l_t = *reinterpret_cast< Vec4< T > const * >( l_p + l_r * a.s_in_o );
+        for( int l_r = 0; l_r < VB; l_r++ ) {
+          Row const l_t = *reinterpret_cast< Row const * >( l_p + l_r * a.s_in_o );
 #pragma unroll
-          for( int l_q = 0; l_q < 4; l_q++ ) l_v[l_u][l_r][l_q] = l_t.v[l_q];
+          for( int l_q = 0; l_q < VB; l_q++ ) l_v[l_u][l_r][l_q] = l_t.v[l_q];
         }
       }
       else {
 #pragma unroll
-        for( int l_r = 0; l_r < 4; l_r++ )
+        for( int l_r = 0; l_r < VB; l_r++ )
 #pragma unroll
-          for( int l_q = 0; l_q < 4; l_q++ ) l_v[l_u][l_r][l_q] = l_p[l_r * a.s_in_o + l_q];
+          for( int l_q = 0; l_q < VB; l_q++ ) l_v[l_u][l_r][l_q] = l_p[l_r * a.s_in_o + l_q];
       }
     }
 #pragma unroll
     for( int l_u = 0; l_u < CPT; l_u++ ) {
       if( !l_ok[l_u] ) continue;
 #pragma unroll
-      for( int l_q = 0; l_q < 4; l_q++ ) {
-        Vec4< T > l_w;
+      for( int l_q = 0; l_q < VB; l_q++ ) {
+        Row l_w;
 #pragma unroll
-        for( int l_r = 0; l_r < 4; l_r++ ) l_w.v[l_r] = l_v[l_u][l_r][l_q];
+        for( int l_r = 0; l_r < VB; l_r++ ) l_w.v[l_r] = l_v[l_u][l_r][l_q];
         if constexpr( DIRECT ) {
           int64_t const l_c = l_cbase + l_cl + l_u * l_cw;
-          reg4_store( a, l_out + l_c * a.c_s_out + int64_t( 4 * l_ig + l_q ) * a.s_out_i + 4 * l_og, l_w );
+          reg4_store< T, VB >( a, l_out + l_c * a.c_s_out + int64_t( VB * l_ig + l_q ) * a.s_out_i + VB * l_og, l_w );
         }
         else {
-          l_slots[( l_cl + l_u * l_cw ) * l_pc + ( 4 * l_ig + l_q ) * l_pi + l_og] = l_w;
+          l_slots[( l_cl + l_u * l_cw ) * l_pc + ( VB * l_ig + l_q ) * l_pi + l_og] = l_w;
         }
       }
     }
   }
   if constexpr( DIRECT ) return;
   __syncthreads();
-  // LDS -> output: the tile's 16-byte slots in output order (o groups
-  // fastest, then whichever of i and c has the smaller output stride), so
-  // that the 64 slots of one store instruction are as contiguous as the
-  // output allows
+  // LDS -> output: the tile's slots in output order (o groups fastest, then
+  // whichever of i and c has the smaller output stride), so that the 64
+  // slots of one store instruction are as contiguous as the output allows
   {
     int32_t const l_si = int32_t( a.size_i );
     int32_t const l_nslots = l_si * l_ct * l_nog;
@@ -423,18 +447,20 @@ void perm_reg4_kernel( PermArgs a ) {
       int32_t const l_i  = l_c_inner ? l_s2 / l_ct : l_s2 % l_si;
       int64_t const l_c = l_cbase + l_cl;
       if( l_c >= a.c_size ) continue;
-      reg4_store( a, l_out + l_c * a.c_s_out + int64_t( l_i ) * a.s_out_i + 4 * l_og,
-                  l_slots[l_cl * l_pc + l_i * l_pi + l_og] );
+      reg4_store< T, VB >( a, l_out + l_c * a.c_s_out + int64_t( l_i ) * a.s_out_i + VB * l_og,
+                           l_slots[l_cl * l_pc + l_i * l_pi + l_og] );
     }
   }
 }
 
 // One thread per VW consecutive output elements of the innermost dim.
-// Dims are (outer -> inner) in a.batch_*; for VW == 4 the innermost dim has
-// unit stride in both tensors and a size divisible by 4.
+// Dims are (outer -> inner) in a.batch_*; for VW > 1 the innermost dim has
+// unit stride in both tensors and a size divisible by VW (VW elements are one
+// 16-byte vector for bf16 and fp32, 32 bytes for fp64).
 template< typename T, int VW, bool FILL >
 __global__ __launch_bounds__( kThreads )
 void perm_gather_kernel( PermArgs a ) {
+  typedef VecN< T, VW > V;
   int64_t const l_num_items = a.num_elements / VW;
   for( int64_t l_item = int64_t( blockIdx.x ) * kThreads + threadIdx.x;
        l_item < l_num_items;
@@ -451,32 +477,44 @@ void perm_gather_kernel( PermArgs a ) {
     }
     T * l_out = reinterpret_cast< T * >( a.out ) + l_off_out;
     if( FILL ) {
-      if( VW == 4 ) {
-        Vec4< T > l_z;
+      V l_z;
 #pragma unroll
-        for( int l_e = 0; l_e < 4; l_e++ ) l_z.v[l_e] = T(0);
-        *reinterpret_cast< Vec4< T > * >( l_out ) = l_z;
-      }
-      else {
-        *l_out = T(0);
-      }
+      for( int l_e = 0; l_e < VW; l_e++ ) l_z.v[l_e] = T( 0 );
+      *reinterpret_cast< V * >( l_out ) = l_z;
       continue;
     }
     T const * l_in = reinterpret_cast< T const * >( a.in ) + l_off_in;
-    if( VW == 4 ) {
-      Vec4< T > l_v = *reinterpret_cast< Vec4< T > const * >( l_in );
-      if( a.add ) {
-        Vec4< T > l_old = *reinterpret_cast< Vec4< T > * >( l_out );
+    V l_v = *reinterpret_cast< V const * >( l_in );
+    if( a.add ) {
+      V const l_old = *reinterpret_cast< V const * >( l_out );
 #pragma unroll
-        for( int l_e = 0; l_e < 4; l_e++ ) l_v.v[l_e] = Elem< T >::add( l_old.v[l_e], l_v.v[l_e] );
-      }
-      *reinterpret_cast< Vec4< T > * >( l_out ) = l_v;
+      for( int l_e = 0; l_e < VW; l_e++ ) l_v.v[l_e] = Elem< T >::add( l_old.v[l_e], l_v.v[l_e] );
     }
-    else {
-      T l_v = *l_in;
-      *l_out = a.add ? Elem< T >::add( *l_out, l_v ) : l_v;
-    }
+    *reinterpret_cast< V * >( l_out ) = l_v;
   }
+}
+
+// REG4 launch: every (block side, passes, threads, direct) variant from one table
+template< typename T, int VB >
+int launch_reg4( PermutePlan const & p, PermArgs const & a, int64_t blocks, hipStream_t stream ) {
+  std::size_t const l_lds = std::size_t( a.c_chunk ) * a.slot_pc * VB * sizeof( T );
+  dim3 const l_grid( (uint32_t) blocks );
+  auto launch = [&]( auto i_kernel, int i_threads, bool i_direct ) {
+    hipLaunchKernelGGL( i_kernel, l_grid, dim3( i_threads ), i_direct ? 0 : l_lds, stream, a );
+    return int( ETIR_SUCCESS );
+  };
+  bool const l_d = p.reg4_direct;
+  if( p.reg4_cpt == 4 )                        return launch( perm_reg4_kernel< T, VB, 4, kThreads, false >, kThreads, false );
+  if( p.reg4_cpt == 2 )                        return launch( perm_reg4_kernel< T, VB, 2, kThreads, false >, kThreads, false );
+  if( p.reg4_threads == 64 && l_d )            return launch( perm_reg4_kernel< T, VB, 1, 64, true >, 64, true );
+  if( p.reg4_threads == 64 )                   return launch( perm_reg4_kernel< T, VB, 1, 64, false >, 64, false );
+  if( p.reg4_threads == 128 && l_d )           return launch( perm_reg4_kernel< T, VB, 1, 128, true >, 128, true );
+  if( p.reg4_threads == 128 )                  return launch( perm_reg4_kernel< T, VB, 1, 128, false >, 128, false );
+  if( p.reg4_threads == kThreads && l_d )      return launch( perm_reg4_kernel< T, VB, 1, kThreads, true >, kThreads, true );
+  if( p.reg4_threads == kThreads )             return launch( perm_reg4_kernel< T, VB, 1, kThreads, false >, kThreads, false );
+  if( p.reg4_threads == 512 && l_d )           return launch( perm_reg4_kernel< T, VB, 1, 512, true >, 512, true );
+  if( p.reg4_threads == 512 )                  return launch( perm_reg4_kernel< T, VB, 1, 512, false >, 512, false );
+  return fail( ETIR_UNDEFINED_ERROR, "permute: no REG4 kernel for this workgroup size" );
 }
 
 template< typename T >
@@ -502,23 +540,10 @@ int launch_typed( PermutePlan const & p,
     if( l_blocks > 0x7fffffffLL ) {
       return fail( ETIR_UNDEFINED_ERROR, "permute: grid too large" );
     }
-    std::size_t const l_lds = std::size_t( a.c_chunk ) * a.slot_pc * 4 * sizeof( T );
-    dim3 const l_grid( (uint32_t) l_blocks );
-    auto launch = [&]( auto i_kernel, int i_threads, bool i_direct ) {
-      hipLaunchKernelGGL( i_kernel, l_grid, dim3( i_threads ), i_direct ? 0 : l_lds, stream, a );
-    };
-    bool const l_d = p.reg4_direct;
-    if( p.reg4_cpt == 4 )                                  launch( perm_reg4_kernel< T, 4, kThreads, false >, kThreads, false );
-    else if( p.reg4_cpt == 2 )                             launch( perm_reg4_kernel< T, 2, kThreads, false >, kThreads, false );
-    else if( p.reg4_threads == 64 && l_d )                 launch( perm_reg4_kernel< T, 1, 64, true >, 64, true );
-    else if( p.reg4_threads == 64 )                        launch( perm_reg4_kernel< T, 1, 64, false >, 64, false );
-    else if( p.reg4_threads == 128 && l_d )                launch( perm_reg4_kernel< T, 1, 128, true >, 128, true );
-    else if( p.reg4_threads == 128 )                       launch( perm_reg4_kernel< T, 1, 128, false >, 128, false );
-    else if( p.reg4_threads == kThreads && l_d )           launch( perm_reg4_kernel< T, 1, kThreads, true >, kThreads, true );
-    else if( p.reg4_threads == kThreads )                  launch( perm_reg4_kernel< T, 1, kThreads, false >, kThreads, false );
-    else if( p.reg4_threads == 512 && l_d )                launch( perm_reg4_kernel< T, 1, 512, true >, 512, true );
-    else if( p.reg4_threads == 512 )                       launch( perm_reg4_kernel< T, 1, 512, false >, 512, false );
-    else return fail( ETIR_UNDEFINED_ERROR, "permute: no REG4 kernel for this workgroup size" );
+    if constexpr( sizeof( T ) == 2 ) {
+      if( p.reg4_vb == 8 ) return launch_reg4< T, 8 >( p, a, l_blocks, stream );
+    }
+    return launch_reg4< T, 4 >( p, a, l_blocks, stream );
   }
   else if( p.mode == PermMode::TRANSPOSE ) {
     int64_t l_blocks = a.tiles_i * a.tiles_o * a.num_batch_total;
@@ -528,19 +553,23 @@ int launch_typed( PermutePlan const & p,
     hipLaunchKernelGGL( perm_transpose_kernel< T >, dim3( (uint32_t) l_blocks ), dim3( kThreads ), 0, stream, a );
   }
   else {
-    int const l_vw = ( p.mode == PermMode::COPY_VEC || ( p.mode == PermMode::FILL && a.vec_ok ) ) && a.vec_ok ? 4 : 1;
+    // bf16 moves 8 elements (16 bytes) per vector where the planner allows it
+    int const l_vw = !a.vec_ok ? 1 : ( a.vec_wide && sizeof( T ) == 2 ? 8 : 4 );
     int64_t l_items = a.num_elements / l_vw;
     int64_t l_blocks = ( l_items + kThreads - 1 ) / kThreads;
     l_blocks = std::min< int64_t >( l_blocks, 65536 );
     if( l_blocks < 1 ) l_blocks = 1;
     bool const l_fill = ( p.mode == PermMode::FILL );
+    dim3 const l_g( (uint32_t) l_blocks );
     if( l_fill ) {
-      if( l_vw == 4 ) hipLaunchKernelGGL( ( perm_gather_kernel< T, 4, true > ), dim3( (uint32_t) l_blocks ), dim3( kThreads ), 0, stream, a );
-      else            hipLaunchKernelGGL( ( perm_gather_kernel< T, 1, true > ), dim3( (uint32_t) l_blocks ), dim3( kThreads ), 0, stream, a );
+      if( l_vw == 8 )      hipLaunchKernelGGL( ( perm_gather_kernel< T, 8, true > ), l_g, dim3( kThreads ), 0, stream, a );
+      else if( l_vw == 4 ) hipLaunchKernelGGL( ( perm_gather_kernel< T, 4, true > ), l_g, dim3( kThreads ), 0, stream, a );
+      else                 hipLaunchKernelGGL( ( perm_gather_kernel< T, 1, true > ), l_g, dim3( kThreads ), 0, stream, a );
     }
     else {
-      if( l_vw == 4 ) hipLaunchKernelGGL( ( perm_gather_kernel< T, 4, false > ), dim3( (uint32_t) l_blocks ), dim3( kThreads ), 0, stream, a );
-      else            hipLaunchKernelGGL( ( perm_gather_kernel< T, 1, false > ), dim3( (uint32_t) l_blocks ), dim3( kThreads ), 0, stream, a );
+      if( l_vw == 8 )      hipLaunchKernelGGL( ( perm_gather_kernel< T, 8, false > ), l_g, dim3( kThreads ), 0, stream, a );
+      else if( l_vw == 4 ) hipLaunchKernelGGL( ( perm_gather_kernel< T, 4, false > ), l_g, dim3( kThreads ), 0, stream, a );
+      else                 hipLaunchKernelGGL( ( perm_gather_kernel< T, 1, false > ), l_g, dim3( kThreads ), 0, stream, a );
     }
   }
   hipError_t l_err = hipGetLastError();
@@ -883,13 +912,14 @@ int plan_permute( int64_t         num_dims,
     if( plan.s_out[l_di] == 1 && l_dim_o < 0 ) l_dim_o = l_di;
   }
 
-  auto all_div4 = [&]( int skip0, int skip1 ) {
+  auto all_div = [&]( int64_t v, int skip0, int skip1 ) {
     for( int l_di = 0; l_di < l_n; l_di++ ) {
       if( l_di == skip0 || l_di == skip1 ) continue;
-      if( plan.s_in[l_di] % 4 != 0 || plan.s_out[l_di] % 4 != 0 ) return false;
+      if( plan.s_in[l_di] % v != 0 || plan.s_out[l_di] % v != 0 ) return false;
     }
     return true;
   };
+  auto all_div4 = [&]( int skip0, int skip1 ) { return all_div( 4, skip0, skip1 ); };
 
   if( ktype == ETIR_KTYPE_ZERO ) {
     plan.mode = PermMode::FILL;
@@ -903,17 +933,32 @@ int plan_permute( int64_t         num_dims,
     for( int l_di = 0; l_di < l_n - 1 && a.vec_ok; l_di++ ) {
       if( plan.s_out[l_di] % 4 != 0 ) a.vec_ok = 0;
     }
+    a.vec_wide = ( a.vec_ok && plan.elem_bytes == 2 && plan.size[l_n-1] % 8 == 0 );
+    for( int l_di = 0; l_di < l_n - 1 && a.vec_wide; l_di++ ) {
+      if( plan.s_out[l_di] % 8 != 0 ) a.vec_wide = 0;
+    }
     return ETIR_SUCCESS;
   }
 
-  // a long input unit-stride dim with a short output one (<= 16): split it
-  // into an inner part that, with the output's dim, fills one wave of 4 x 4
-  // blocks and an outer part (the REG4 tiles below take the inner part whole)
+  // REG4 block side and its dim-length limits, in elements: a block row is
+  // one vector -- 16 bytes for fp32 (4 x 4) and for bf16 when both unit dims
+  // are multiples of 8 (8 x 8; else 4 x 4 with 8-byte rows), 32 bytes for
+  // fp64 (4 x 4) -- and the limits measured for fp32 (a short dim up to 16,
+  // both up to 32) scale with the elements per 4 bytes
+  int64_t const l_vb = (    plan.elem_bytes == 2 && l_dim_i >= 0 && l_dim_o >= 0
+                         && plan.size[l_dim_i] % 8 == 0 && plan.size[l_dim_o] % 8 == 0 ) ? 8 : 4;
+  int64_t const l_scale = plan.elem_bytes == 2 ? 2 : 1;
+  int64_t const l_short = reg4_max_short() * l_scale;
+  int64_t const l_both = 32 * l_scale;
+
+  // a long input unit-stride dim with a short output one: split it into an
+  // inner part that, with the output's dim, fills one wave of blocks and an
+  // outer part (the REG4 tiles below take the inner part whole)
   if(    l_dim_i >= 0 && l_dim_o >= 0 && l_dim_i != l_dim_o && l_n < kPermMaxDims
-      && plan.size[l_dim_o] % 4 == 0 && plan.size[l_dim_o] <= 16
-      && ( plan.size[l_dim_i] / 4 ) * ( plan.size[l_dim_o] / 4 ) > 64
+      && plan.size[l_dim_o] % l_vb == 0 && plan.size[l_dim_o] <= l_short
+      && ( plan.size[l_dim_i] / l_vb ) * ( plan.size[l_dim_o] / l_vb ) > 64
       && std::getenv( "ETIR_NO_PERM_REG4" ) == nullptr ) {
-    int64_t const l_lo = 4 * ( 64 / ( plan.size[l_dim_o] / 4 ) );
+    int64_t const l_lo = l_vb * ( 64 / ( plan.size[l_dim_o] / l_vb ) );
     if( plan.size[l_dim_i] % l_lo == 0 ) {
       for( int l_di = l_n; l_di > l_dim_i; l_di-- ) {
         plan.size[l_di]  = plan.size[l_di - 1];
@@ -933,17 +978,18 @@ int plan_permute( int64_t         num_dims,
   }
 
   if(    l_dim_i >= 0 && l_dim_o >= 0 && l_dim_i != l_dim_o
-      && plan.size[l_dim_i] % 4 == 0 && plan.size[l_dim_o] % 4 == 0
-      && (    std::min( plan.size[l_dim_i], plan.size[l_dim_o] ) <= reg4_max_short()
-           || (    std::max( plan.size[l_dim_i], plan.size[l_dim_o] ) <= 32
+      && plan.size[l_dim_i] % l_vb == 0 && plan.size[l_dim_o] % l_vb == 0
+      && (    std::min( plan.size[l_dim_i], plan.size[l_dim_o] ) <= l_short
+           || (    std::max( plan.size[l_dim_i], plan.size[l_dim_o] ) <= l_both
                 && ( plan.size[l_dim_i] * plan.elem_bytes ) % 128 == 0
                 && ( plan.size[l_dim_o] * plan.elem_bytes ) % 128 == 0 ) )
-      && ( plan.size[l_dim_i] / 4 ) * ( plan.size[l_dim_o] / 4 ) <= kThreads
+      && ( plan.size[l_dim_i] / l_vb ) * ( plan.size[l_dim_o] / l_vb ) <= kThreads
       && std::getenv( "ETIR_NO_PERM_REG4" ) == nullptr ) {
-    // a short unit-stride dim: 4 x 4 register transposes.  The dim that
+    // a short unit-stride dim: register-transposed blocks.  The dim that
     // continues the input's run (input stride size_i), else the output's,
     // else the largest other dim, is walked by consecutive lanes after i
     plan.mode = PermMode::REG4;
+    plan.reg4_vb = (int32_t) l_vb;
     a.size_i  = plan.size[l_dim_i];
     a.size_o  = plan.size[l_dim_o];
     a.s_in_o  = plan.s_in[l_dim_o];
@@ -972,7 +1018,7 @@ int plan_permute( int64_t         num_dims,
     // options: ETIR_PERM_REG4_THREADS (64 ... 512) and ETIR_PERM_REG4_CPT, two
     // or four passes of 256 threads over c (longer runs of (c, i), measured
     // slower too)
-    int64_t const l_blocks_c = ( a.size_i / 4 ) * ( a.size_o / 4 );
+    int64_t const l_blocks_c = ( a.size_i / l_vb ) * ( a.size_o / l_vb );
     plan.reg4_threads = l_blocks_c <= 64 ? 64 : ( l_blocks_c <= 128 ? 128 : kThreads );
     plan.reg4_cpt = 1;
     if( char const * l_env = std::getenv( "ETIR_PERM_REG4_THREADS" ) ) {
@@ -996,16 +1042,17 @@ int plan_permute( int64_t         num_dims,
     int64_t const l_direct_run = a.size_o * plan.elem_bytes
                                * ( ( l_dc >= 0 && plan.s_out[l_dc] == a.size_o ) ? a.c_chunk : 1 );
     plan.reg4_direct = ( l_direct_run % 128 == 0 && plan.reg4_cpt == 1
-                         && std::max( a.size_i, a.size_o ) <= 16 );
+                         && std::max( a.size_i, a.size_o ) <= 16 * l_scale );
     if( char const * l_env = std::getenv( "ETIR_PERM_REG4_DIRECT" ) ) {
       plan.reg4_direct = plan.reg4_direct && std::atoi( l_env ) != 0;
     }
     a.c_chunk *= plan.reg4_cpt;
     // LDS slot pitches: simulate both phases' 16-byte accesses (eight lanes
-    // per LDS cycle, a slot covers 4 of the 64 four-byte banks) and take the
-    // padding with the fewest conflicts
+    // per LDS cycle, a slot covers 4 of the 64 four-byte banks; fp64's
+    // 32-byte slots are counted as 16-byte ones) and take the padding with
+    // the fewest conflicts
     {
-      int32_t const l_nig = int32_t( a.size_i / 4 ), l_nog = int32_t( a.size_o / 4 );
+      int32_t const l_nig = int32_t( a.size_i / l_vb ), l_nog = int32_t( a.size_o / l_vb );
       int32_t const l_si = int32_t( a.size_i );
       int32_t const l_cw = a.c_chunk / plan.reg4_cpt, l_ct = a.c_chunk;
       int32_t const l_used = l_nig * l_nog * l_cw;
@@ -1027,11 +1074,11 @@ int plan_permute( int64_t         num_dims,
           };
           // phase 1: one instruction per (pass, q), lanes = threads
           for( int l_u = 0; l_u < plan.reg4_cpt; l_u++ ) {
-            for( int l_q = 0; l_q < 4; l_q++ ) {
+            for( int l_q = 0; l_q < l_vb; l_q++ ) {
               std::vector< int32_t > l_sl;
               for( int32_t l_t = 0; l_t < l_used; l_t++ ) {
                 int32_t const l_ig = l_t % l_nig, l_cl = ( l_t / l_nig ) % l_cw, l_og = l_t / l_nig / l_cw;
-                l_sl.push_back( ( l_cl + l_u * l_cw ) * l_pc + ( 4 * l_ig + l_q ) * l_pi + l_og );
+                l_sl.push_back( ( l_cl + l_u * l_cw ) * l_pc + ( int32_t( l_vb ) * l_ig + l_q ) * l_pi + l_og );
               }
               group_cost( l_sl );
             }
@@ -1063,7 +1110,8 @@ int plan_permute( int64_t         num_dims,
       a.num_batch_total *= plan.size[l_di];
       a.num_batch++;
     }
-    a.vec_ok = ( a.s_in_o % 4 == 0 && a.s_out_i % 4 == 0 && all_div4( l_dim_i, l_dim_o ) ) ? 1 : 0;
+    // block rows as vectors: every stride a multiple of the row length
+    a.vec_ok = ( a.s_in_o % l_vb == 0 && a.s_out_i % l_vb == 0 && all_div( l_vb, l_dim_i, l_dim_o ) ) ? 1 : 0;
     return ETIR_SUCCESS;
   }
 
@@ -1120,6 +1168,7 @@ int plan_permute( int64_t         num_dims,
       && plan.size[l_n-1] % 4 == 0 && all_div4( l_n - 1, l_n - 1 ) ) {
     plan.mode = PermMode::COPY_VEC;
     a.vec_ok = 1;
+    a.vec_wide = ( plan.elem_bytes == 2 && plan.size[l_n-1] % 8 == 0 && all_div( 8, l_n - 1, l_n - 1 ) ) ? 1 : 0;
   }
   else {
     plan.mode = PermMode::GATHER;
@@ -1139,13 +1188,19 @@ int launch_permute( PermutePlan const & plan,
   PermArgs a = plan.args;
   a.in  = in;
   a.out = out;
-  // 16-byte alignment (4 elements) is required for the vector paths
-  uintptr_t const l_align = uintptr_t( 4 * plan.elem_bytes );
+  // the vector paths need their vectors aligned: 4 elements, REG4 one block
+  // row (8 bf16 elements)
+  uintptr_t const l_align = uintptr_t( ( plan.mode == PermMode::REG4 ? plan.reg4_vb : 4 ) * plan.elem_bytes );
   if( a.vec_ok ) {
     if(    ( uintptr_t( out ) % l_align ) != 0
         || ( plan.mode != PermMode::FILL && ( uintptr_t( in ) % l_align ) != 0 ) ) {
       a.vec_ok = 0;
     }
+  }
+  if(    a.vec_wide
+      && (    ( uintptr_t( out ) % 16 ) != 0
+           || ( plan.mode != PermMode::FILL && ( uintptr_t( in ) % 16 ) != 0 ) ) ) {
+    a.vec_wide = 0;
   }
   PermutePlan l_plan = plan;
   if( plan.mode == PermMode::COPY_VEC && !a.vec_ok ) l_plan.mode = PermMode::GATHER;
