@@ -288,6 +288,10 @@ std::string einsum_ir::frontend::EinsumExpression::to_string_render() const {
     if( l_next.empty() ) break;
     l_levels.push_back( l_next );
   }
+  // the drawing doubles in width with every level
+  if( l_levels.size() > 16 ) {
+    return "Error: tree too deep to draw (" + std::to_string( l_levels.size() ) + " levels).";
+  }
   std::size_t l_width = 0;
   for( auto const & l_lvl : l_levels ) {
     for( auto const & l_e : l_lvl ) {

@@ -125,7 +125,9 @@ class einsum_ir::frontend::EinsumExpression {
      * The compiled tree drawn for reading (reference EinsumExpression.h:
      * 210-216): one line per level, root first, each node's dim ids
      * separated by spaces in a cell of the widest node's width, and every
-     * node placed centred over the cells its children can take.
+     * node placed centred over the cells its children can take.  Trees of
+     * more than 16 levels (whose drawing would be 2^levels cells wide) give
+     * an error text instead.
      **/
     std::string to_string_render() const;
 };
