@@ -129,11 +129,11 @@ def summarize_rocprof(dirs, timed, kernel_filter=""):
                 durations.setdefault(key, []).append(
                     (int(r["Start_Timestamp"]), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3))
         for path in sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)):
-            per = {}
+            per = {}          # (kernel, grid) -> counter -> dispatch id -> value (summed over rows)
             for r in _read_csv(path):
-                k = (r["Kernel_Name"], int(r["Grid_Size"]))
-                per.setdefault(k, {}).setdefault(r["Counter_Name"], {})[int(r["Dispatch_Id"])] = \
-                    per.get(k, {}).get(r["Counter_Name"], {}).get(int(r["Dispatch_Id"]), 0.0) + float(r["Counter_Value"])
+                by_id = per.setdefault((r["Kernel_Name"], int(r["Grid_Size"])), {}).setdefault(r["Counter_Name"], {})
+                d = int(r["Dispatch_Id"])
+                by_id[d] = by_id.get(d, 0.0) + float(r["Counter_Value"])
             for k, cs in per.items():
                 for c, by_id in cs.items():
                     counters.setdefault(k, {})[c] = [by_id[i] for i in sorted(by_id)]
