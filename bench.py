@@ -48,6 +48,8 @@ def parse_args():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-mfma-ceiling", action="store_true",
+                   help="skip the matrix-core rate and clock probe (einsum_ir_amd/bin/mfma_ceiling)")
     p.add_argument("--only", default="", help="comma list of configs to run (c1,c2,c3,c4,c5,mlp,samples)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also time a plain 512 MiB device copy (reference for the PMC byte counters)")
@@ -559,6 +561,26 @@ def cpu_host_probe():
                 libxsmm=ctypes.util.find_library("xsmm"), openblas=ctypes.util.find_library("openblas"))
 
 
+def mfma_ceiling():
+    """Runs einsum_ir_amd/bin/mfma_ceiling as a child process: the rate of an
+    MFMA-only loop on every CU and the median shader clock of its waves, with
+    constant and with random operands (the second is the power-limited clock
+    that real data sees).  Returns {"<mfma>_<operands>": {...}}."""
+    import subprocess
+    exe = os.path.join(ROOT, "einsum_ir_amd", "bin", "mfma_ceiling")
+    if not os.path.exists(exe):
+        return {"error": "einsum_ir_amd/bin/mfma_ceiling is not built"}
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    if r.returncode != 0:
+        return {"error": (r.stderr or r.stdout).strip()[-300:]}
+    res = {}
+    for ln in r.stdout.splitlines():
+        if ln.startswith("{"):
+            x = json.loads(ln)
+            res[f"{x['mfma']}_{x['operands']}"] = {k: x[k] for k in ("tflops", "frac_peak", "clock_ghz_median")}
+    return res
+
+
 def main():
     args = parse_args()
     if args.summarize:
@@ -649,6 +671,14 @@ def main():
         log(f"tccg: {tccg}")
         for name, r in nets.items():
             log(f"{name}: {r}")
+
+    if not args.no_mfma_ceiling and run("c3"):
+        # after every GPU timing above: the probe runs the matrix cores flat out
+        extra["mfma_ceiling"] = mfma_ceiling()
+        log(f"mfma ceiling: {extra['mfma_ceiling']}")
+        sustained = extra["mfma_ceiling"].get("bf16_32x32x16_random", {}).get("tflops")
+        if c3 is not None and sustained:
+            extra["c3_frac_sustained_bf16"] = round(c3["flops"] / c3["per_launch"] * 1e-12 / sustained, 4)
 
     cpu = None
     if not args.no_cpu_baseline and run("c3"):

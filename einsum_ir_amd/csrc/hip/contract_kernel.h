@@ -28,7 +28,9 @@
 // (BM/WM) x (BN/WN) block of 32x32 MFMA tiles.  Operands are staged through a
 // double-buffered LDS tile stored K-contiguous ([row][k], rows padded by 16 B
 // so the 16-byte fragment reads of 8 consecutive lanes hit disjoint banks).
-// Global loads for step k+1 are issued before the MFMAs of step k.
+// The global loads of step k+1 are issued between the MFMAs of the first
+// fragment step of step k and their LDS stores between those of the last one
+// (branch-free loaders, fixed by scheduling barriers).
 #ifndef ETIR_CONTRACT_KERNEL_H
 #define ETIR_CONTRACT_KERNEL_H
 
@@ -78,13 +80,33 @@ struct KmPitch {
   static constexpr int value = ( bytes_raw + pad ) / ESZ;
 };
 
+// compile-time loop: f( std::integral_constant< int, 0 .. N-1 > ); keeps
+// register-array indices static where #pragma unroll alone may give up
+template< typename F, int... Is >
+__device__ __attribute__( ( always_inline ) ) inline void static_for_impl( F && f,
+                                                                          std::integer_sequence< int, Is... > ) {
+  ( f( std::integral_constant< int, Is >{} ), ... );
+}
+template< int N, typename F >
+__device__ __attribute__( ( always_inline ) ) inline void static_for( F && f ) {
+  static_for_impl( f, std::make_integer_sequence< int, N >{} );
+}
+
 // ---------------------------------------------------------------------------
 // Operand loader: global -> registers -> LDS ([row][k], pitch LDK elements)
 // ---------------------------------------------------------------------------
 template< int R, int BK, int T, int ESZ, int MODE >
 struct Loader;
 
-// 16-byte vectors along K; the k index of a vector is fixed per thread
+// 16-byte vectors along K; the k index of a vector is fixed per thread.
+//
+// All vector loaders share one interface: init() once per tile, setup(k0)
+// per K step (offsets and the validity mask), issue<I>() for the global load
+// of vector I and put<I>() for its LDS store; load() and store() do all
+// vectors at once.  Loads never branch: a vector outside the tensor (rows
+// past M/N, k past K) reads row 0 / k 0 of the operand instead, which always
+// exists, and put<I>() writes zeros for it.  Branch-free loads can be placed
+// between MFMAs by the caller.
 template< int R, int BK, int T, int ESZ >
 struct Loader< R, BK, T, ESZ, LOAD_VEC_K > {
   static constexpr int V      = 16 / ESZ;           // elements per vector
@@ -92,53 +114,64 @@ struct Loader< R, BK, T, ESZ, LOAD_VEC_K > {
   static constexpr int COUNT  = R * VPR;
   static constexpr int NV     = ( COUNT + T - 1 ) / T;
   static constexpr int LDK    = BK + V;
+  static_assert( NV <= 32, "validity mask" );
 
-  u32x4   m_reg[NV];
-  int32_t m_row_off[NV];
-  int     m_kv;
+  u32x4    m_reg[NV];
+  int32_t  m_row_off[NV];
+  uint32_t m_row_ok;      // bit i: vector i is inside the tile and its row inside the tensor
+  uint32_t m_ok;          // bit i: vector i of the current step holds data
+  int32_t  m_koff;
+  int      m_kv;
 
   __device__ inline void init( int32_t const * tab_rows, int32_t rows, int32_t row0 ) {
     int const l_t = threadIdx.x;
     m_kv = ( l_t % VPR ) * V;
+    m_row_ok = 0;
 #pragma unroll
     for( int l_i = 0; l_i < NV; l_i++ ) {
       int const l_idx = l_t + l_i * T;
       int const l_row = l_idx / VPR;
       int const l_g   = row0 + l_row;
-      m_row_off[l_i] = ( l_idx < COUNT && l_g < rows ) ? tab_rows[l_g] : -1;
+      bool const l_ok = l_idx < COUNT && l_g < rows;
+      if( l_ok ) m_row_ok |= 1u << l_i;
+      m_row_off[l_i] = tab_rows[l_ok ? l_g : 0];
+    }
+  }
+
+  template< bool KAFF >
+  __device__ inline void setup( int32_t k0, int32_t K, int32_t const * tab_k, int32_t sk ) {
+    int32_t const l_k  = k0 + m_kv;
+    bool const    l_ok = l_k < K;
+    int32_t const l_kc = l_ok ? l_k : 0;
+    m_koff = KAFF ? l_kc * sk : tab_k[l_kc];
+    m_ok   = l_ok ? m_row_ok : 0u;
+  }
+
+  template< int I, typename TE >
+  __device__ inline void issue( TE const * base ) {
+    m_reg[I] = *reinterpret_cast< u32x4 const * >( base + m_row_off[I] + m_koff );
+  }
+
+  template< int I, typename TE >
+  __device__ inline void put( TE * lds ) {
+    int const l_idx = int( threadIdx.x ) + I * T;
+    if( COUNT % T == 0 || l_idx < COUNT ) {
+      int const l_row = l_idx / VPR;
+      u32x4 const l_v = ( ( m_ok >> I ) & 1u ) ? m_reg[I] : u32x4{ 0u, 0u, 0u, 0u };
+      *reinterpret_cast< u32x4 * >( lds + l_row * LDK + m_kv ) = l_v;
     }
   }
 
   template< bool KAFF, typename TE >
   __device__ inline void load( TE const * base, int32_t k0, int32_t K,
                                int32_t const * tab_k, int32_t sk ) {
-    int32_t const l_k = k0 + m_kv;
-    bool const l_kok = l_k < K;
-    int32_t l_koff = 0;
-    if( KAFF ) l_koff = l_k * sk;
-    else if( l_kok ) l_koff = tab_k[l_k];
-#pragma unroll
-    for( int l_i = 0; l_i < NV; l_i++ ) {
-      if( l_kok && m_row_off[l_i] >= 0 ) {
-        m_reg[l_i] = *reinterpret_cast< u32x4 const * >( base + m_row_off[l_i] + l_koff );
-      }
-      else {
-        m_reg[l_i] = u32x4{ 0u, 0u, 0u, 0u };
-      }
-    }
+    setup< KAFF >( k0, K, tab_k, sk );
+    static_for< NV >( [&]( auto ic ) __attribute__( ( always_inline ) ) { issue< decltype( ic )::value >( base ); } );
   }
 
   template< typename TE >
   __device__ inline void store( TE * lds ) {
-    int const l_t = threadIdx.x;
-#pragma unroll
-    for( int l_i = 0; l_i < NV; l_i++ ) {
-      int const l_idx = l_t + l_i * T;
-      if( COUNT % T == 0 || l_idx < COUNT ) {
-        int const l_row = l_idx / VPR;
-        *reinterpret_cast< u32x4 * >( lds + l_row * LDK + m_kv ) = m_reg[l_i];
-      }
-    }
+    static_for< NV >( [&]( auto ic ) __attribute__( ( always_inline ) ) { put< decltype( ic )::value >( lds ); } );
   }
 };
 
@@ -153,6 +186,8 @@ struct Loader< R, BK, T, ESZ, LOAD_SCALAR > {
 
   u32x4   m_reg[NV];
   int32_t m_row_off[NV];
+  int32_t m_koff[V];
+  bool    m_kok[V];
   int     m_kv;
 
   __device__ inline void init( int32_t const * tab_rows, int32_t rows, int32_t row0 ) {
@@ -167,44 +202,50 @@ struct Loader< R, BK, T, ESZ, LOAD_SCALAR > {
     }
   }
 
-  template< bool KAFF, typename TE >
-  __device__ inline void load( TE const * base, int32_t k0, int32_t K,
-                               int32_t const * tab_k, int32_t sk ) {
-    // all table reads first, then all data reads: one wait for the tables
-    int32_t l_koff[V];
-    bool    l_kok[V];
+  // all table reads first, then all data reads: one wait for the tables
+  template< bool KAFF >
+  __device__ inline void setup( int32_t k0, int32_t K, int32_t const * tab_k, int32_t sk ) {
 #pragma unroll
     for( int l_e = 0; l_e < V; l_e++ ) {
       int32_t const l_k = k0 + m_kv + l_e;
-      l_kok[l_e] = l_k < K;
-      l_koff[l_e] = 0;
-      if( KAFF ) l_koff[l_e] = l_k * sk;
-      else if( l_kok[l_e] ) l_koff[l_e] = tab_k[l_k];
+      m_kok[l_e] = l_k < K;
+      m_koff[l_e] = 0;
+      if( KAFF ) m_koff[l_e] = l_k * sk;
+      else if( m_kok[l_e] ) m_koff[l_e] = tab_k[l_k];
     }
+  }
+
+  template< int I, typename TE >
+  __device__ inline void issue( TE const * base ) {
+    TE l_v[V];
 #pragma unroll
-    for( int l_i = 0; l_i < NV; l_i++ ) {
-      TE l_v[V];
-#pragma unroll
-      for( int l_e = 0; l_e < V; l_e++ ) {
-        l_v[l_e] = TE( 0 );
-        // row and k offsets each fit int32 (planner), their sum need not
-        if( l_kok[l_e] && m_row_off[l_i] >= 0 ) l_v[l_e] = base[ int64_t( m_row_off[l_i] ) + l_koff[l_e] ];
-      }
-      m_reg[l_i] = *reinterpret_cast< u32x4 * >( l_v );
+    for( int l_e = 0; l_e < V; l_e++ ) {
+      l_v[l_e] = TE( 0 );
+      // row and k offsets each fit int32 (planner), their sum need not
+      if( m_kok[l_e] && m_row_off[I] >= 0 ) l_v[l_e] = base[ int64_t( m_row_off[I] ) + m_koff[l_e] ];
     }
+    m_reg[I] = *reinterpret_cast< u32x4 * >( l_v );
+  }
+
+  template< int I, typename TE >
+  __device__ inline void put( TE * lds ) {
+    int const l_idx = int( threadIdx.x ) + I * T;
+    if( COUNT % T == 0 || l_idx < COUNT ) {
+      int const l_row = l_idx / VPR;
+      *reinterpret_cast< u32x4 * >( lds + l_row * LDK + m_kv ) = m_reg[I];
+    }
+  }
+
+  template< bool KAFF, typename TE >
+  __device__ inline void load( TE const * base, int32_t k0, int32_t K,
+                               int32_t const * tab_k, int32_t sk ) {
+    setup< KAFF >( k0, K, tab_k, sk );
+    static_for< NV >( [&]( auto ic ) __attribute__( ( always_inline ) ) { issue< decltype( ic )::value >( base ); } );
   }
 
   template< typename TE >
   __device__ inline void store( TE * lds ) {
-    int const l_t = threadIdx.x;
-#pragma unroll
-    for( int l_i = 0; l_i < NV; l_i++ ) {
-      int const l_idx = l_t + l_i * T;
-      if( COUNT % T == 0 || l_idx < COUNT ) {
-        int const l_row = l_idx / VPR;
-        *reinterpret_cast< u32x4 * >( lds + l_row * LDK + m_kv ) = m_reg[l_i];
-      }
-    }
+    static_for< NV >( [&]( auto ic ) __attribute__( ( always_inline ) ) { put< decltype( ic )::value >( lds ); } );
   }
 };
 
@@ -222,50 +263,60 @@ struct Loader< R, BK, T, ESZ, LOAD_VEC_MN > {
   static constexpr int NV     = COUNT / T;
   static constexpr int PK     = KmPitch< R, ESZ >::value;
   static_assert( COUNT % T == 0 && T % VPK == 0, "VEC_MN loader: tile/threads mismatch" );
+  static_assert( NV <= 32, "validity mask" );
 
-  u32x4   m_reg[NV];
-  int32_t m_row_off;
-  int     m_mv;
-  int     m_k;
+  u32x4    m_reg[NV];
+  int32_t  m_koff[NV];
+  int32_t  m_row_off;
+  bool     m_row_ok;
+  uint32_t m_ok;          // bit i: vector i of the current step holds data
+  int      m_mv;
+  int      m_k;
 
   __device__ inline void init( int32_t const * tab_rows, int32_t rows, int32_t row0 ) {
     int const l_t = threadIdx.x;
     m_mv = l_t % VPK;
     m_k  = l_t / VPK;
     int const l_g = row0 + m_mv * V;
-    m_row_off = ( l_g < rows ) ? tab_rows[l_g] : -1;
+    m_row_ok  = l_g < rows;
+    m_row_off = tab_rows[m_row_ok ? l_g : 0];
+  }
+
+  template< bool KAFF >
+  __device__ inline void setup( int32_t k0, int32_t K, int32_t const * tab_k, int32_t sk ) {
+    m_ok = 0;
+#pragma unroll
+    for( int l_i = 0; l_i < NV; l_i++ ) {
+      int32_t const l_k  = k0 + m_k + l_i * ( T / VPK );
+      bool const    l_ok = l_k < K;
+      int32_t const l_kc = l_ok ? l_k : 0;
+      m_koff[l_i] = KAFF ? l_kc * sk : tab_k[l_kc];
+      if( l_ok && m_row_ok ) m_ok |= 1u << l_i;
+    }
+  }
+
+  template< int I, typename TE >
+  __device__ inline void issue( TE const * base ) {
+    m_reg[I] = *reinterpret_cast< u32x4 const * >( base + m_row_off + m_koff[I] );
+  }
+
+  template< int I, typename TE >
+  __device__ inline void put( TE * lds ) {
+    int const l_k = m_k + I * ( T / VPK );
+    u32x4 const l_v = ( ( m_ok >> I ) & 1u ) ? m_reg[I] : u32x4{ 0u, 0u, 0u, 0u };
+    *reinterpret_cast< u32x4 * >( lds + l_k * PK + m_mv * V ) = l_v;
   }
 
   template< bool KAFF, typename TE >
   __device__ inline void load( TE const * base, int32_t k0, int32_t K,
                                int32_t const * tab_k, int32_t sk ) {
-    int32_t l_koff[NV];
-#pragma unroll
-    for( int l_i = 0; l_i < NV; l_i++ ) {
-      int32_t const l_k = k0 + m_k + l_i * ( T / VPK );
-      l_koff[l_i] = 0;
-      if( KAFF ) l_koff[l_i] = l_k * sk;
-      else if( l_k < K ) l_koff[l_i] = tab_k[l_k];
-    }
-#pragma unroll
-    for( int l_i = 0; l_i < NV; l_i++ ) {
-      int32_t const l_k = k0 + m_k + l_i * ( T / VPK );
-      if( l_k < K && m_row_off >= 0 ) {
-        m_reg[l_i] = *reinterpret_cast< u32x4 const * >( base + m_row_off + l_koff[l_i] );
-      }
-      else {
-        m_reg[l_i] = u32x4{ 0u, 0u, 0u, 0u };
-      }
-    }
+    setup< KAFF >( k0, K, tab_k, sk );
+    static_for< NV >( [&]( auto ic ) __attribute__( ( always_inline ) ) { issue< decltype( ic )::value >( base ); } );
   }
 
   template< typename TE >
   __device__ inline void store( TE * lds ) {
-#pragma unroll
-    for( int l_i = 0; l_i < NV; l_i++ ) {
-      int const l_k = m_k + l_i * ( T / VPK );
-      *reinterpret_cast< u32x4 * >( lds + l_k * PK + m_mv * V ) = m_reg[l_i];
-    }
+    static_for< NV >( [&]( auto ic ) __attribute__( ( always_inline ) ) { put< decltype( ic )::value >( lds ); } );
   }
 };
 
@@ -347,18 +398,6 @@ struct LdsSize {
 // counter on gfx9).  Accumulator layout of v_mfma_f32_32x32x*: register r of
 // lane l holds row = 8*(r/4) + 4*(l/32) + r%4, column = l%32.
 // ---------------------------------------------------------------------------
-// compile-time loop: f( std::integral_constant< int, 0 .. N-1 > ); keeps
-// register-array indices static where #pragma unroll alone may give up
-template< typename F, int... Is >
-__device__ __attribute__( ( always_inline ) ) inline void static_for_impl( F && f,
-                                                                          std::integer_sequence< int, Is... > ) {
-  ( f( std::integral_constant< int, Is >{} ), ... );
-}
-template< int N, typename F >
-__device__ __attribute__( ( always_inline ) ) inline void static_for( F && f ) {
-  static_for_impl( f, std::make_integer_sequence< int, N >{} );
-}
-
 // a pointer whose value is the same in every lane, moved to scalar registers
 // (buffer resources must be wave-uniform; the compiler cannot always prove it)
 template< typename P >
@@ -649,69 +688,100 @@ void contract_kernel( ContractArgs a ) {
     l_ld_b.store( l_lds_b[0] );
     __syncthreads();
 
-    for( int32_t l_kt = 0; l_kt < l_nk; l_kt++ ) {
-      int const l_cur = l_kt & 1;
-      bool const l_more = ( l_kt + 1 ) < l_nk;
-      if( l_more ) {
-        l_ld_a.template load< KAFF >( l_a, ( l_kt + 1 ) * BK, a.K, a.tk_a, a.sk_a );
-        l_ld_b.template load< KAFF >( l_b, ( l_kt + 1 ) * BK, a.K, a.tk_b, a.sk_b );
-      }
+    // rows of this wave's blocks; VEC_MN readers take the block base row
+    int const l_ra = l_wm * TM * 32 + ( MA == LOAD_VEC_MN ? 0 : l_lr );
+    int const l_rb = l_wn * TN * 32 + ( MB == LOAD_VEC_MN ? 0 : l_lr );
 
+    // One K step on LDS buffer l_cur.  With MORE, the operand vectors of the
+    // next step are loaded from global memory between the MFMAs of the first
+    // fragment step and stored to the other buffer between those of the last
+    // one, so that neither the load issue nor the LDS stores leave the MFMA
+    // pipe idle.  The scheduling barriers keep that placement.
+    typedef Loader< BM, BK, T, ESZ, MA > LdA;
+    typedef Loader< BN, BK, T, ESZ, MB > LdB;
+    constexpr int NS  = ( DT == ETIR_FP32 ) ? BK / 8 : BK / 16;        // fragment steps
+    constexpr int NMF = ( DT == ETIR_FP32 ) ? 4 * TM * TN : TM * TN;   // MFMAs per fragment step
+    constexpr int NG  = NMF < 4 ? NMF : 4;                              // MFMA groups per fragment step
+    constexpr int NL  = LdA::NV + LdB::NV;                              // vectors per thread and step
+    auto l_step = [&]( int l_cur, int32_t l_knext, auto more_c ) __attribute__( ( always_inline ) ) {
+      constexpr bool MORE = decltype( more_c )::value;
       TE const * l_sa = l_lds_a[l_cur];
       TE const * l_sb = l_lds_b[l_cur];
-      // rows of this wave's blocks; VEC_MN readers take the block base row
-      int const l_ra = l_wm * TM * 32 + ( MA == LOAD_VEC_MN ? 0 : l_lr );
-      int const l_rb = l_wn * TN * 32 + ( MB == LOAD_VEC_MN ? 0 : l_lr );
-
-      if constexpr( DT == ETIR_FP32 ) {
-#pragma unroll
-        for( int l_s4 = 0; l_s4 < BK / 8; l_s4++ ) {
-          f32x4 l_fa[TM];
-          f32x4 l_fb[TN];
-#pragma unroll
-          for( int l_i = 0; l_i < TM; l_i++ )
-            l_fa[l_i] = Frag< 4, MA, BM, BK >::read4( l_sa, l_ra + l_i * 32 + ( MA == LOAD_VEC_MN ? l_lr : 0 ),
-                                                      l_s4, l_lane );
-#pragma unroll
-          for( int l_j = 0; l_j < TN; l_j++ )
-            l_fb[l_j] = Frag< 4, MB, BN, BK >::read4( l_sb, l_rb + l_j * 32 + ( MB == LOAD_VEC_MN ? l_lr : 0 ),
-                                                      l_s4, l_lane );
-#pragma unroll
-          for( int l_e = 0; l_e < 4; l_e++ )
-#pragma unroll
-            for( int l_i = 0; l_i < TM; l_i++ )
-#pragma unroll
-              for( int l_j = 0; l_j < TN; l_j++ )
-                l_acc[l_i][l_j] = __builtin_amdgcn_mfma_f32_32x32x2f32( l_fa[l_i][l_e], l_fb[l_j][l_e],
-                                                                        l_acc[l_i][l_j], 0, 0, 0 );
-        }
+      TE * l_na = l_lds_a[l_cur ^ 1];
+      TE * l_nb = l_lds_b[l_cur ^ 1];
+      if constexpr( MORE ) {
+        l_ld_a.template setup< KAFF >( l_knext, a.K, a.tk_a, a.sk_a );
+        l_ld_b.template setup< KAFF >( l_knext, a.K, a.tk_b, a.sk_b );
       }
-      else {
+      static_for< NS >( [&]( auto sc ) __attribute__( ( always_inline ) ) {
+        constexpr int l_s = decltype( sc )::value;
+        // fragments of step s: fp32 f32x4 (4 MFMA k-pairs), bf16 bf16x8 (one MFMA)
+        typedef typename std::conditional< DT == ETIR_FP32, f32x4, bf16x8 >::type FragT;
+        FragT l_fa[TM];
+        FragT l_fb[TN];
 #pragma unroll
-        for( int l_s = 0; l_s < BK / 16; l_s++ ) {
-          bf16x8 l_fa[TM];
-          bf16x8 l_fb[TN];
-#pragma unroll
-          for( int l_i = 0; l_i < TM; l_i++ )
+        for( int l_i = 0; l_i < TM; l_i++ ) {
+          if constexpr( DT == ETIR_FP32 )
+            l_fa[l_i] = Frag< 4, MA, BM, BK >::read4( l_sa, l_ra + l_i * 32 + ( MA == LOAD_VEC_MN ? l_lr : 0 ),
+                                                      l_s, l_lane );
+          else
             l_fa[l_i] = Frag< 2, MA, BM, BK >::read8( l_sa, l_ra + l_i * 32, l_s, l_lane );
+        }
 #pragma unroll
-          for( int l_j = 0; l_j < TN; l_j++ )
+        for( int l_j = 0; l_j < TN; l_j++ ) {
+          if constexpr( DT == ETIR_FP32 )
+            l_fb[l_j] = Frag< 4, MB, BN, BK >::read4( l_sb, l_rb + l_j * 32 + ( MB == LOAD_VEC_MN ? l_lr : 0 ),
+                                                      l_s, l_lane );
+          else
             l_fb[l_j] = Frag< 2, MB, BN, BK >::read8( l_sb, l_rb + l_j * 32, l_s, l_lane );
-#pragma unroll
-          for( int l_i = 0; l_i < TM; l_i++ )
-#pragma unroll
-            for( int l_j = 0; l_j < TN; l_j++ )
+        }
+        static_for< NG >( [&]( auto gc ) __attribute__( ( always_inline ) ) {
+          constexpr int l_g = decltype( gc )::value;
+          if constexpr( MORE && ( l_s == 0 || l_s == NS - 1 ) ) {
+            static_for< NL >( [&]( auto vc ) __attribute__( ( always_inline ) ) {
+              constexpr int l_v = decltype( vc )::value;
+              // vector v goes to group v*NG/NL (NL >= NG) or group v (NL < NG)
+              if constexpr( ( NL >= NG ? l_v * NG / NL : l_v ) == l_g ) {
+                if constexpr( l_s == 0 ) {
+                  if constexpr( l_v < LdA::NV ) l_ld_a.template issue< l_v >( l_a );
+                  else                          l_ld_b.template issue< l_v - LdA::NV >( l_b );
+                }
+                if constexpr( l_s == NS - 1 ) {
+                  if constexpr( l_v < LdA::NV ) l_ld_a.template put< l_v >( l_na );
+                  else                          l_ld_b.template put< l_v - LdA::NV >( l_nb );
+                }
+              }
+            } );
+          }
+          static_for< NMF / NG >( [&]( auto fc ) __attribute__( ( always_inline ) ) {
+            constexpr int l_f = l_g * ( NMF / NG ) + decltype( fc )::value;
+            if constexpr( DT == ETIR_FP32 ) {
+              // flat index f = (e, i, j), e the k-pair inside the fragment
+              constexpr int l_e = l_f / ( TM * TN );
+              constexpr int l_i = ( l_f / TN ) % TM;
+              constexpr int l_j = l_f % TN;
+              l_acc[l_i][l_j] = __builtin_amdgcn_mfma_f32_32x32x2f32( l_fa[l_i][l_e], l_fb[l_j][l_e],
+                                                                      l_acc[l_i][l_j], 0, 0, 0 );
+            }
+            else {
+              constexpr int l_i = l_f / TN;
+              constexpr int l_j = l_f % TN;
               l_acc[l_i][l_j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16( l_fa[l_i], l_fb[l_j],
                                                                          l_acc[l_i][l_j], 0, 0, 0 );
-        }
-      }
+            }
+          } );
+          __builtin_amdgcn_sched_barrier( 0 );
+        } );
+      } );
+    };
 
-      if( l_more ) {
-        l_ld_a.store( l_lds_a[l_cur ^ 1] );
-        l_ld_b.store( l_lds_b[l_cur ^ 1] );
-      }
+    int32_t l_kt = 0;
+    for( ; l_kt + 1 < l_nk; l_kt++ ) {
+      l_step( l_kt & 1, ( l_kt + 1 ) * BK, std::true_type{} );
       __syncthreads();
     }
+    l_step( l_kt & 1, 0, std::false_type{} );
+    __syncthreads();
   }
 
   // ---------------------------------------------------------------- epilogue
