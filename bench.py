@@ -54,7 +54,7 @@ def parse_args():
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also time a plain 512 MiB device copy (reference for the PMC byte counters)")
     p.add_argument("--settle", type=float, default=1.0,
-                   help="seconds of untimed config-3 launches before its timing (GPU clock settling)")
+                   help="seconds of untimed launches before the timing of configs 3, 4 and 5 (GPU clock settling)")
     p.add_argument("--summarize", nargs="+", metavar="DIR",
                    help="print statistics of rocprofv3 CSV output directories (kernel durations and/or "
                         "counters) over each kernel's last --timed dispatches, then exit (no GPU use)")
@@ -307,7 +307,7 @@ def bench_c1(torch, eir, stream, steps, warmup):
     return res
 
 
-def bench_c4(torch, eir, stream, steps, warmup):
+def bench_c4(torch, eir, stream, steps, warmup, settle=0.0):
     """the 4-layer MLP tree bi,ih,hj,jk,ko->bo through
     EinsumExpression (left-to-right path, intermediates in the HBM arena, all
     nodes on one stream)."""
@@ -321,13 +321,13 @@ def bench_c4(torch, eir, stream, steps, warmup):
     e = host.Expression("bi,ih,hj,jk,ko->bo", sizes, [(0, 1), (0, 3), (0, 2), (0, 1)], [x] + ws + [out],
                         stream=stream)
     flops = 4 * 2 * b * w * w
-    wall, per_eval = time_launches(torch, stream, e.eval_async, steps, warmup)
+    wall, per_eval = time_launches(torch, stream, e.eval_async, steps, warmup, settle=settle)
     res = dict(flops=flops, wall=wall, per_launch=per_eval, num_ops=e.num_ops(), arena=e.arena_bytes())
     e.close()
     return res
 
 
-def bench_c5(torch, eir, stream, steps, warmup):
+def bench_c5(torch, eir, stream, steps, warmup, settle=0.0):
     """the committed random tensor network (~50 GFLOP) through
     EinsumExpression along its greedy path."""
     from einsum_ir_amd import host
@@ -339,7 +339,7 @@ def bench_c5(torch, eir, stream, steps, warmup):
     tensors = [torch.rand(numel(t), device="cuda", generator=g) * 2 - 1 for t in ins.split(",")]
     tensors.append(torch.empty(numel(out), device="cuda"))
     e = host.Expression(expr, sizes, path, tensors, stream=stream)
-    wall, per_eval = time_launches(torch, stream, e.eval_async, steps, warmup)
+    wall, per_eval = time_launches(torch, stream, e.eval_async, steps, warmup, settle=settle)
     res = dict(flops=fx["flops"], wall=wall, per_launch=per_eval, num_ops=e.num_ops())
     e.close()
     # the same tree replayed as a recorded HIP graph (needs a stream of its own)
@@ -634,7 +634,7 @@ def main():
                                           kernel=c1["desc"])
         log(f"c1: {c1['desc']}  {c1['per_launch']*1e6:.2f} us/launch")
     if run("c4"):
-        c4 = bench_c4(torch, eir, stream, max(5, args.steps // 5), min(args.warmup, 2))
+        c4 = bench_c4(torch, eir, stream, max(5, args.steps // 5), min(args.warmup, 2), settle=args.settle)
         gf = c4["flops"] / c4["per_launch"] * 1e-9
         extra["c4_mlp_tree_fp32"] = dict(value=round(gf, 1), unit="GFLOP/s",
                                          ms_per_eval=round(c4["per_launch"] * 1e3, 3),
@@ -643,7 +643,7 @@ def main():
                                               f"{c4['arena'] / 2**20:.0f} MiB)")
         log(f"c4: {c4['per_launch']*1e3:.3f} ms/eval")
     if run("c5"):
-        c5 = bench_c5(torch, eir, stream, max(5, args.steps // 5), min(args.warmup, 2))
+        c5 = bench_c5(torch, eir, stream, max(5, args.steps // 5), min(args.warmup, 2), settle=args.settle)
         gf = c5["flops"] / c5["per_launch"] * 1e-9
         extra["c5_tensor_network_fp32"] = dict(value=round(gf, 1), unit="GFLOP/s",
                                                ms_per_eval=round(c5["per_launch"] * 1e3, 3),
