@@ -43,6 +43,7 @@ int launch_contract_bf16_dma( int32_t ma, int32_t mb, int32_t variant, ContractA
                               uint32_t grid, hipStream_t stream );
 int launch_contract_kwave( int32_t waves, int32_t kw, ContractArgs const & a, uint32_t grid,
                            hipStream_t stream );
+int launch_contract_f32_dma( int32_t ma, int32_t mb, ContractArgs const & a, uint32_t grid, hipStream_t stream );
 
 namespace {
 
@@ -154,6 +155,7 @@ char const * tile_str( int32_t t ) {
     case TILE_CPX_F32_64x64: return "cpx_f32_64x64x16";
     case TILE_CPX_F64_64x64: return "cpx_f64_64x64x16";
     case TILE_F32_KWAVE_32x32: return "f32_kwave_32x32";
+    case TILE_F32_DMA_128x128: return "f32_dma_128x128x32";
     default:                return "?";
   }
 }
@@ -168,6 +170,7 @@ void tile_shape( int32_t t, int64_t & bm, int64_t & bn ) {
     case TILE_BF16_DMA_256x128: bm = 256; bn = 128; break;
     case TILE_F32_KWAVE_32x32: bm = 32; bn = 32; break;
     case TILE_BF16_128x128: bm = 128; bn = 128; break;
+    case TILE_F32_DMA_128x128: bm = 128; bn = 128; break;
     default:                bm = 64;  bn = 64;  break;
   }
 }
@@ -451,12 +454,27 @@ int plan_contraction_impl( int64_t            num_loops,
       && 2 * int64_t( 64 ) * std::max( l_sk_a, l_sk_b ) * ( ( l_size_k + 63 ) / 64 + 4 ) < ( int64_t( 1 ) << 31 );
   plan.tile_fallback = plan.tile;
   if( l_dma_ok && n_tiles( TILE_BF16_DMA_256x256 ) >= l_cus ) plan.tile = TILE_BF16_DMA_256x256;
+  // the fp32 direct-to-LDS kernel: where the planner chose the 128 x 128 fp32
+  // tile, under the same conditions (4-byte elements; the loads of the step
+  // past the last one are issued too)
+  bool const l_f32_dma_ok =
+         l_f32 && !l_cpx
+      && ( plan.mode_a == LOAD_VEC_MN || plan.mode_a == LOAD_VEC_K )
+      && ( plan.mode_b == LOAD_VEC_MN || plan.mode_b == LOAD_VEC_K )
+      && l_k_affine
+      && 4 * ( max_of( l_tm_a ) + std::max< int64_t >( l_size_k - 1, 0 ) * l_sk_a ) + 64 < ( int64_t( 1 ) << 31 )
+      && 4 * ( max_of( l_tn_b ) + std::max< int64_t >( l_size_k - 1, 0 ) * l_sk_b ) + 64 < ( int64_t( 1 ) << 31 )
+      && 4 * int64_t( 32 ) * std::max( l_sk_a, l_sk_b ) * ( ( l_size_k + 31 ) / 32 + 2 ) < ( int64_t( 1 ) << 31 )
+      && std::getenv( "ETIR_NO_F32_DMA" ) == nullptr;
+  if( l_f32_dma_ok && plan.tile == TILE_F32_128x128 ) plan.tile = TILE_F32_DMA_128x128;
   if( char const * l_env = ( l_f64 || l_cpx ) ? nullptr : std::getenv( "ETIR_TILE" ) ) {
     // diagnostic override of the tile heuristic (must match the dtype)
     int32_t l_t = std::atoi( l_env );
-    bool const l_t_f32 = ( l_t == TILE_F32_128x128 || l_t == TILE_F32_64x64 );
+    bool const l_t_f32 = ( l_t == TILE_F32_128x128 || l_t == TILE_F32_64x64
+                           || ( l_t == TILE_F32_DMA_128x128 && l_f32_dma_ok ) );
     bool const l_t_dma = ( l_t == TILE_BF16_DMA_256x256 || l_t == TILE_BF16_DMA_256x128 );
-    bool const l_t_ok = ( l_t >= 0 && l_t <= TILE_BF16_DMA_256x128 && l_t != TILE_F64_64x64 && l_t_f32 == l_f32 )
+    bool const l_t_ok = ( ( ( l_t >= 0 && l_t <= TILE_BF16_DMA_256x128 ) || l_t == TILE_F32_DMA_128x128 )
+                          && l_t != TILE_F64_64x64 && l_t_f32 == l_f32 )
                      && ( !l_t_dma || l_dma_ok )
                      && ( l_t != TILE_BF16_DMA_256x128
                           || ( plan.mode_a == LOAD_VEC_MN && plan.mode_b == LOAD_VEC_MN ) );
@@ -905,10 +923,11 @@ int launch_contraction( ContractionPlan const & plan,
   if( uintptr_t( a.b ) % align_of( l_mb ) != 0 ) l_mb = LOAD_SCALAR;
   int32_t l_dma_variant = plan.dma_variant;
   int32_t l_tile = plan.tile;
-  if(    ( l_tile == TILE_BF16_DMA_256x256 || l_tile == TILE_BF16_DMA_256x128 || l_tile == TILE_F32_KWAVE_32x32 )
+  if(    ( l_tile == TILE_BF16_DMA_256x256 || l_tile == TILE_BF16_DMA_256x128 || l_tile == TILE_F32_KWAVE_32x32
+           || l_tile == TILE_F32_DMA_128x128 )
       && ( l_ma != plan.mode_a || l_mb != plan.mode_b ) ) {
-    // the DMA kernel needs the 16-byte vector modes: use the register-staged
-    // kernel with its own tile grid
+    // the DMA and K-over-waves kernels need the 16-byte vector modes: use
+    // the register-staged kernel with its own tile grid
     l_tile = plan.tile_fallback;
     int64_t l_bm, l_bn;
     tile_shape( l_tile, l_bm, l_bn );
@@ -930,7 +949,7 @@ int launch_contraction( ContractionPlan const & plan,
     case TILE_BF16_256x128:
     case TILE_BF16_128x128:
     case TILE_BF16_64x64:
-      l_err = launch_contract_tile( plan.tile, l_ma, l_mb, l_kaff, a, l_g, stream );
+      l_err = launch_contract_tile( l_tile, l_ma, l_mb, l_kaff, a, l_g, stream );
       break;
     case TILE_F64_64x64:    l_err = launch_contract_f64_64x64( l_ma, l_mb, l_kaff, a, l_g, stream ); break;
     case TILE_CPX_F32_64x64: l_err = launch_contract_cpx( false, l_ma, l_mb, l_kaff, a, l_g, stream ); break;
@@ -943,6 +962,9 @@ int launch_contraction( ContractionPlan const & plan,
       break;
     case TILE_BF16_DMA_256x128:
       l_err = launch_contract_bf16_dma( l_ma, l_mb, 2, a, l_g, stream );
+      break;
+    case TILE_F32_DMA_128x128:
+      l_err = launch_contract_f32_dma( l_ma, l_mb, a, l_g, stream );
       break;
     default: return fail( ETIR_COMPILATION_FAILED, "contraction: unknown tile configuration" );
   }
