@@ -509,9 +509,10 @@ int plan_contraction_impl( int64_t            num_loops,
                       && l_size_k <= 4096 && n_tiles( plan.tile ) < l_cus && l_t32 >= l_cus / 2
                       && std::getenv( "ETIR_NO_KWAVE" ) == nullptr;
     if( l_kw_ok ) {
-      // 16 waves (4 per SIMD) measured fastest for K = 256 .. 1024 (config 1:
-      // 7.4 us against 8.0 with 8 waves and 9.0 with 4)
-      int32_t l_w = 16;
+      // 8 waves up to K = 512, 16 above (config 1, K = 512: 7.58-7.65 us with
+      // 8 waves against 7.85-7.87 with 16 and 8.8 with 4; K = 256 and 1024:
+      // 8 and 16 equal within 1 %)
+      int32_t l_w = ( l_size_k <= 512 ) ? 8 : 16;
       if( char const * l_env = std::getenv( "ETIR_KWAVE_WAVES" ) ) {
         int32_t const l_v = std::atoi( l_env );
         if( l_v == 4 || l_v == 8 || l_v == 16 ) l_w = l_v;
