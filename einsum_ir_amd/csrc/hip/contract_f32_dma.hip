@@ -3,8 +3,8 @@
 // Same contraction and first/last-touch epilogue as contract_kernel.h
 //   out[c][m][n] = touch( sum_k A[c][m][k] * B[c][n][k] )
 // (reference src/basic/binary/ContractionBackendTpp.cpp:127-163 for the touch
-// kernels), for large fp32 contractions with 16-byte vector operands and an
-// affine K: 128 x 128 tiles, k step 32, 8 waves of 32 x 64
+// kernels), for large fp32 contractions with 16-byte vector operands:
+// 128 x 128 tiles, k step 32, 8 waves of 32 x 64
 // (v_mfma_f32_32x32x2_f32), two LDS stages of 32 KB (two workgroups per CU,
 // four waves per SIMD).
 //
@@ -16,6 +16,8 @@
 // peak).  Step t issues the loads of step t + 1 into the other stage between
 // the MFMAs of its first fragment step and ends with one wait + barrier.
 // Rows past M/N and k past K read zeros through the buffer range check.
+// A K that is not one affine index (K <= 1024) takes its offsets from the
+// plan's K tables, staged in LDS once per workgroup.
 //
 // LDS layouts per stage, written one KiB per DMA instruction (lane i at 16 i):
 // VEC_MN (16-byte runs along the rows): [k][R] fp32, R * 4 bytes per k row;
@@ -32,6 +34,9 @@
 
 namespace etir {
 namespace kern {
+
+// longest K whose offset tables the kernel stages in LDS (2 x 4 KB)
+constexpr int kF32DmaMaxTableK = 1024;
 
 __device__ inline uint32_t swz_f32_mn( int k ) {
   return uint32_t( ( k & 4 ) << 1 );
@@ -72,6 +77,31 @@ struct F32DmaLoader< R, BK, W, LOAD_VEC_MN > {
     uint32_t const l_off = ( k0 + m_kk[J] < K ) ? m_off[J] + kstep_bytes : kDmaOob;
     dma16( rsrc, l_off, lds_stage + ( wave * NJ + J ) * 1024 );
   }
+
+  // K through an offset table (staged in LDS): m_off holds the row part only
+  __device__ inline void init_tab( int32_t const * tab_rows, int32_t rows, int32_t row0, int wave, int lane ) {
+#pragma unroll
+    for( int l_j = 0; l_j < NJ; l_j++ ) {
+      int const l_kk  = ( wave * NJ + l_j ) * KPC + lane / SEGS;
+      int const l_g   = ( lane % SEGS ) ^ int( swz_f32_mn( l_kk ) );
+      int32_t const l_row = row0 + 4 * l_g;
+      m_kk[l_j]  = l_kk;
+      m_off[l_j] = ( l_row < rows ) ? uint32_t( 4 * tab_rows[l_row] ) : kDmaOob;
+    }
+  }
+  // table entry of the lane's k row in step k0 (0 past K: the load is out of range anyway)
+  template< int J >
+  __device__ __attribute__( ( always_inline ) ) inline int32_t tab_entry( int32_t const * tab_k, int32_t k0,
+                                                                         int32_t K ) const {
+    int32_t const l_k = k0 + m_kk[J];
+    return tab_k[l_k < K ? l_k : 0];
+  }
+  template< int J >
+  __device__ __attribute__( ( always_inline ) ) inline void issue_tab( i32x4 rsrc, uint32_t lds_stage, int wave,
+                                                                       int32_t k0, int32_t K, int32_t koff ) {
+    uint32_t const l_off = ( k0 + m_kk[J] < K ) ? m_off[J] + uint32_t( 4 * koff ) : kDmaOob;
+    dma16( rsrc, l_off, lds_stage + ( wave * NJ + J ) * 1024 );
+  }
 };
 
 template< int R, int BK, int W >
@@ -104,6 +134,32 @@ struct F32DmaLoader< R, BK, W, LOAD_VEC_K > {
                                                                        int32_t k0, int32_t K,
                                                                        uint32_t kstep_bytes ) {
     uint32_t const l_off = ( k0 + m_kl[J] < K ) ? m_off[J] + kstep_bytes : kDmaOob;
+    dma16( rsrc, l_off, lds_stage + ( wave * NJ + J ) * 1024 );
+  }
+
+  // K through an offset table: the planner's VEC_K mode guarantees runs of
+  // 4 consecutive k at consecutive offsets, so the lane's 4 k start at
+  // tab_k[k0 + 4g]
+  __device__ inline void init_tab( int32_t const * tab_rows, int32_t rows, int32_t row0, int wave, int lane ) {
+#pragma unroll
+    for( int l_j = 0; l_j < NJ; l_j++ ) {
+      int const l_r   = ( wave * NJ + l_j ) * RPC + lane / SEGS;
+      int const l_g   = ( lane % SEGS ) ^ int( swz_k( l_r ) );
+      int32_t const l_row = row0 + l_r;
+      m_kl[l_j]  = 4 * l_g;
+      m_off[l_j] = ( l_row < rows ) ? uint32_t( 4 * tab_rows[l_row] ) : kDmaOob;
+    }
+  }
+  template< int J >
+  __device__ __attribute__( ( always_inline ) ) inline int32_t tab_entry( int32_t const * tab_k, int32_t k0,
+                                                                         int32_t K ) const {
+    int32_t const l_k = k0 + m_kl[J];
+    return tab_k[l_k < K ? l_k : 0];
+  }
+  template< int J >
+  __device__ __attribute__( ( always_inline ) ) inline void issue_tab( i32x4 rsrc, uint32_t lds_stage, int wave,
+                                                                       int32_t k0, int32_t K, int32_t koff ) {
+    uint32_t const l_off = ( k0 + m_kl[J] < K ) ? m_off[J] + uint32_t( 4 * koff ) : kDmaOob;
     dma16( rsrc, l_off, lds_stage + ( wave * NJ + J ) * 1024 );
   }
 };
@@ -153,7 +209,9 @@ struct F32DmaFrag< R, BK, NB, LOAD_VEC_K > {
   }
 };
 
-template< int BM, int BN, int BK, int WM, int WN, int MA, int MB >
+// KAFF false: K offsets from the plan's tables, which are staged in LDS
+// (KTAB entries per operand, K <= KTAB) behind the stage buffers
+template< int BM, int BN, int BK, int WM, int WN, int MA, int MB, bool KAFF >
 __global__ __launch_bounds__( 64 * WM * WN, 1 )
 void contract_f32_dma_kernel( ContractArgs a ) {
   constexpr int W   = WM * WN;
@@ -169,7 +227,9 @@ void contract_f32_dma_kernel( ContractArgs a ) {
   constexpr int ND  = LdA::NJ + LdB::NJ;       // DMA issues per wave and step
   constexpr int LDS_MAIN = 2 * ( SA + SB );
   constexpr int LDS_EPI  = EpilogueLds< BM, BN, WM, WN, TM, TN >::BYTES;
-  constexpr int LDS_BYTES = LDS_MAIN > LDS_EPI ? LDS_MAIN : LDS_EPI;
+  constexpr int LDS_OPS   = LDS_MAIN > LDS_EPI ? LDS_MAIN : LDS_EPI;
+  constexpr int KTAB      = kF32DmaMaxTableK;
+  constexpr int LDS_BYTES = LDS_OPS + ( KAFF ? 0 : 2 * KTAB * 4 );
   static_assert( TM >= 1 && TN >= 1 && BK == 32, "fp32 DMA kernel: 32x32 MFMA blocks, k step 32" );
   static_assert( ND <= NMF, "at most one DMA issue per MFMA of the first fragment step" );
 
@@ -192,8 +252,22 @@ void contract_f32_dma_kernel( ContractArgs a ) {
   i32x4 const l_rb = make_rsrc( reinterpret_cast< float const * >( a.b ) + a.tc_b[l_c], kDmaOob );
   LdA l_lda;
   LdB l_ldb;
-  l_lda.init( a.tm_a, a.M, l_m0, a.sk_a, l_wave, l_lane );
-  l_ldb.init( a.tn_b, a.N, l_n0, a.sk_b, l_wave, l_lane );
+  int32_t * l_tka = reinterpret_cast< int32_t * >( l_lds + LDS_OPS );
+  int32_t * l_tkb = l_tka + KTAB;
+  if constexpr( KAFF ) {
+    l_lda.init( a.tm_a, a.M, l_m0, a.sk_a, l_wave, l_lane );
+    l_ldb.init( a.tn_b, a.N, l_n0, a.sk_b, l_wave, l_lane );
+  }
+  else {
+    l_lda.init_tab( a.tm_a, a.M, l_m0, l_wave, l_lane );
+    l_ldb.init_tab( a.tn_b, a.N, l_n0, l_wave, l_lane );
+    // the K tables into LDS (K <= KTAB, planner); read before the first issue
+    for( int32_t l_k = threadIdx.x; l_k < a.K; l_k += T ) {
+      l_tka[l_k] = a.tk_a[l_k];
+      l_tkb[l_k] = a.tk_b[l_k];
+    }
+    __syncthreads();
+  }
   F32DmaFrag< BM, BK, TM, MA > l_fra;
   F32DmaFrag< BN, BK, TN, MB > l_frb;
   l_fra.init( l_wm * TM * 32, l_lane );
@@ -214,14 +288,32 @@ void contract_f32_dma_kernel( ContractArgs a ) {
   uint32_t const l_kb_b = uint32_t( 4 * BK * a.sk_b );
   uint32_t const l_lds0 = lds_addr( l_lds );
 
-  // DMA issue d of a step: A chunks first, then B
+  // DMA issue d of a step: A chunks first, then B.  With a K table the
+  // lane's k offsets are read from LDS first (l_koff, per issue).
+  int32_t l_koff[ND];
+  auto l_tab = [&]( int32_t l_k0 ) __attribute__( ( always_inline ) ) {
+    if constexpr( !KAFF ) {
+      static_for< ND >( [&]( auto dc ) __attribute__( ( always_inline ) ) {
+        constexpr int l_d = decltype( dc )::value;
+        if constexpr( l_d < LdA::NJ ) l_koff[l_d] = l_lda.template tab_entry< l_d >( l_tka, l_k0, l_K );
+        else l_koff[l_d] = l_ldb.template tab_entry< l_d - LdA::NJ >( l_tkb, l_k0, l_K );
+      } );
+    }
+  };
   auto l_issue = [&]( auto dc, uint32_t l_st, int32_t l_k0, uint32_t l_kt ) __attribute__( ( always_inline ) ) {
     constexpr int l_d = decltype( dc )::value;
-    if constexpr( l_d < LdA::NJ ) l_lda.template issue_one< l_d >( l_ra, l_st, l_wave, l_k0, l_K, l_kt * l_kb_a );
-    else l_ldb.template issue_one< l_d - LdA::NJ >( l_rb, l_st + SA, l_wave, l_k0, l_K, l_kt * l_kb_b );
+    if constexpr( KAFF ) {
+      if constexpr( l_d < LdA::NJ ) l_lda.template issue_one< l_d >( l_ra, l_st, l_wave, l_k0, l_K, l_kt * l_kb_a );
+      else l_ldb.template issue_one< l_d - LdA::NJ >( l_rb, l_st + SA, l_wave, l_k0, l_K, l_kt * l_kb_b );
+    }
+    else {
+      if constexpr( l_d < LdA::NJ ) l_lda.template issue_tab< l_d >( l_ra, l_st, l_wave, l_k0, l_K, l_koff[l_d] );
+      else l_ldb.template issue_tab< l_d - LdA::NJ >( l_rb, l_st + SA, l_wave, l_k0, l_K, l_koff[l_d] );
+    }
   };
 
   if( l_nk > 0 ) {
+    l_tab( 0 );
     static_for< ND >( [&]( auto dc ) __attribute__( ( always_inline ) ) { l_issue( dc, l_lds0, 0, 0u ); } );
     wait_vmcnt< 0 >();
     barrier_lds();
@@ -235,6 +327,7 @@ void contract_f32_dma_kernel( ContractArgs a ) {
       // are drained by the wait below like all others
       uint32_t const l_nst = l_lds0 + uint32_t( l_cur ^ 1 ) * ( SA + SB );
       int32_t const  l_nk0 = ( l_kt + 1 ) * BK;
+      l_tab( l_nk0 );
       static_for< NS >( [&]( auto sc ) __attribute__( ( always_inline ) ) {
         constexpr int l_s = decltype( sc )::value;
         f32x4 l_fa[TM];
@@ -275,10 +368,20 @@ void contract_f32_dma_kernel( ContractArgs a ) {
 }  // namespace kern
 
 int launch_contract_f32_dma( int32_t ma, int32_t mb, ContractArgs const & a, uint32_t grid, hipStream_t stream ) {
+  if( !a.k_affine && a.K > kern::kF32DmaMaxTableK ) {
+    return fail( ETIR_COMPILATION_FAILED, "fp32 direct-to-LDS kernel: K table longer than its LDS copy" );
+  }
   auto l_go = [&]( auto ma_c, auto mb_c ) {
-    hipLaunchKernelGGL( ( kern::contract_f32_dma_kernel< 128, 128, 32, 4, 2, decltype( ma_c )::value,
-                                                         decltype( mb_c )::value > ),
-                        dim3( grid ), dim3( 512 ), 0, stream, a );
+    if( a.k_affine ) {
+      hipLaunchKernelGGL( ( kern::contract_f32_dma_kernel< 128, 128, 32, 4, 2, decltype( ma_c )::value,
+                                                           decltype( mb_c )::value, true > ),
+                          dim3( grid ), dim3( 512 ), 0, stream, a );
+    }
+    else {
+      hipLaunchKernelGGL( ( kern::contract_f32_dma_kernel< 128, 128, 32, 4, 2, decltype( ma_c )::value,
+                                                           decltype( mb_c )::value, false > ),
+                          dim3( grid ), dim3( 512 ), 0, stream, a );
+    }
     return int( ETIR_SUCCESS );
   };
   typedef std::integral_constant< int32_t, LOAD_VEC_MN > Mn;

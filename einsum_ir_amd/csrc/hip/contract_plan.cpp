@@ -456,15 +456,22 @@ int plan_contraction_impl( int64_t            num_loops,
   if( l_dma_ok && n_tiles( TILE_BF16_DMA_256x256 ) >= l_cus ) plan.tile = TILE_BF16_DMA_256x256;
   // the fp32 direct-to-LDS kernel: where the planner chose the 128 x 128 fp32
   // tile, under the same conditions (4-byte elements; the loads of the step
-  // past the last one are issued too)
+  // past the last one are issued too); a K that is not affine up to 1024,
+  // whose offset tables the kernel copies into LDS
+  int64_t const l_bytes_max = int64_t( 1 ) << 31;
+  bool const l_f32_dma_k =
+         ( l_k_affine
+           && 4 * ( max_of( l_tm_a ) + std::max< int64_t >( l_size_k - 1, 0 ) * l_sk_a ) + 64 < l_bytes_max
+           && 4 * ( max_of( l_tn_b ) + std::max< int64_t >( l_size_k - 1, 0 ) * l_sk_b ) + 64 < l_bytes_max
+           && 4 * int64_t( 32 ) * std::max( l_sk_a, l_sk_b ) * ( ( l_size_k + 31 ) / 32 + 2 ) < l_bytes_max )
+      || ( !l_k_affine && l_size_k <= 1024
+           && 4 * ( max_of( l_tm_a ) + max_of( l_tk_a ) ) + 64 < l_bytes_max
+           && 4 * ( max_of( l_tn_b ) + max_of( l_tk_b ) ) + 64 < l_bytes_max );
   bool const l_f32_dma_ok =
          l_f32 && !l_cpx
       && ( plan.mode_a == LOAD_VEC_MN || plan.mode_a == LOAD_VEC_K )
       && ( plan.mode_b == LOAD_VEC_MN || plan.mode_b == LOAD_VEC_K )
-      && l_k_affine
-      && 4 * ( max_of( l_tm_a ) + std::max< int64_t >( l_size_k - 1, 0 ) * l_sk_a ) + 64 < ( int64_t( 1 ) << 31 )
-      && 4 * ( max_of( l_tn_b ) + std::max< int64_t >( l_size_k - 1, 0 ) * l_sk_b ) + 64 < ( int64_t( 1 ) << 31 )
-      && 4 * int64_t( 32 ) * std::max( l_sk_a, l_sk_b ) * ( ( l_size_k + 31 ) / 32 + 2 ) < ( int64_t( 1 ) << 31 )
+      && l_f32_dma_k
       && std::getenv( "ETIR_NO_F32_DMA" ) == nullptr;
   if( l_f32_dma_ok && plan.tile == TILE_F32_128x128 ) plan.tile = TILE_F32_DMA_128x128;
   if( char const * l_env = ( l_f64 || l_cpx ) ? nullptr : std::getenv( "ETIR_TILE" ) ) {

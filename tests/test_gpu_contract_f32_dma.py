@@ -1,6 +1,7 @@
 """GPU parity of the fp32 direct-to-LDS contraction kernel (tile
 f32_dma_128x128x32): every load-mode pairing, ragged M/N edges, K that is not
-a multiple of the k step, C dims, the touch kernels, the split-K partials it
+a multiple of the k step, K through offset tables, C dims, the touch kernels,
+the split-K partials it
 runs for few tiles and a long K; and the launch-time fallback of every
 vector-only kernel (fp32 and bf16 direct-to-LDS, K over waves) to the
 register-staged kernel when an operand pointer is not 16-byte aligned.
@@ -31,6 +32,23 @@ def test_f32_dma_layouts(torch_cuda, oracle, monkeypatch, expr, sizes):
     monkeypatch.setenv("ETIR_TILE", "12")
     _, desc = run_case(torch_cuda, oracle, expr, sizes, seed=len(expr) + sizes["k"])
     assert "f32_dma_128x128x32" in desc, desc
+
+
+# K of two dims whose strides make it affine for one operand only: the K
+# offsets come from the plan's tables (staged in LDS by the kernel)
+F32_DMA_TABLE_K = [
+    ("klm,lkn->mn", dict(k=8, l=16, m=264, n=520)),                        # vec_mn x vec_mn
+    ("mkl,lkn->mn", dict(m=300, k=16, l=8, n=260)),                        # vec_k x vec_mn
+    ("klm,nlk->mn", dict(k=12, l=8, m=136, n=264)),
+    ("zklm,zlkn->zmn", dict(z=3, k=4, l=36, m=128, n=128)),                # K = 144, C dim
+]
+
+
+@pytest.mark.parametrize("expr,sizes", F32_DMA_TABLE_K)
+def test_f32_dma_table_k(torch_cuda, oracle, monkeypatch, expr, sizes):
+    monkeypatch.setenv("ETIR_TILE", "12")
+    _, desc = run_case(torch_cuda, oracle, expr, sizes, seed=sum(sizes.values()))
+    assert "f32_dma_128x128x32" in desc and "k_affine=0" in desc, desc
 
 
 @pytest.mark.parametrize("first,last", [(eir.COPY, eir.UNDEFINED_KTYPE), (eir.ADD, eir.UNDEFINED_KTYPE),
