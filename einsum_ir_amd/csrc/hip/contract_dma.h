@@ -381,18 +381,26 @@ __device__ __attribute__( ( always_inline ) ) inline void prologue_issue( char *
   }
 }
 
-// Main loop after the prologue's loads were issued.  FIRST_VMCNT: loads or
-// stores that may still be in flight beyond the prologue's when the loop
-// starts (-1: none, the wait for step 0 counts only the prologue; otherwise
-// the loop waits for everything, vmcnt(0)).  Ends after the last step's
-// MFMAs are issued; the stage buffers may still be read by other waves.
-// SWAPAB: the MFMA takes the B fragment as its first operand, so the
-// accumulators hold the tile transposed (see epilogue_fast_f32_t).
-template< int BM, int BN, int BK, int WM, int WN, int MA, int MB, int STAGES, int FIRST_VMCNT, bool SWAPAB,
+// Main loop after the prologue's loads were issued.  FIRST_VMCNT: what may
+// still be in flight beyond the prologue's loads when the loop starts
+//   -1: nothing; the waits count only the loads issued after the awaited ones
+//    0: unknown; the first wait is for everything, vmcnt(0)
+//    1: when l_pend, at least 63 stores issued after the prologue (the
+//       previous tile's output).  The waits for the prologue's steps (0 ..
+//       STAGES-2) are then vmcnt(63): every one of those loads has at least
+//       63 younger operations behind it, so at most 63 outstanding means it
+//       has landed, while the stores keep draining under the first steps'
+//       MFMAs (vmcnt counts loads and stores in one in-order counter).  The
+//       first wait for a load issued inside the loop, after the stores,
+//       counts normally and so also waits for the stores.
+// Ends after the last step's MFMAs are issued; the stage buffers may still
+// be read by other waves.
+template< int BM, int BN, int BK, int WM, int WN, int MA, int MB, int STAGES, int FIRST_VMCNT,
           typename LdA, typename LdB, typename FrA, typename FrB, int TM, int TN >
 __device__ __attribute__( ( always_inline ) ) inline void mainloop_body(
     f32x16 ( &l_acc )[TM][TN], char * l_lds, LdA & l_lda, LdB & l_ldb, FrA const & l_fra, FrB const & l_frb,
-    i32x4 l_ra, i32x4 l_rb, int l_wave, int32_t l_K, int32_t l_nk, uint32_t l_kb_a, uint32_t l_kb_b ) {
+    i32x4 l_ra, i32x4 l_rb, int l_wave, int32_t l_K, int32_t l_nk, uint32_t l_kb_a, uint32_t l_kb_b,
+    bool l_pend = false ) {
   constexpr int SA  = LdA::STAGE_BYTES;
   constexpr int SB  = LdB::STAGE_BYTES;
   constexpr int NJA = LdA::NJ;
@@ -416,7 +424,11 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_body(
 
   // step 0 has landed, then fragments of step 0, substep 0
   if constexpr( FIRST_VMCNT < 0 ) wait_vmcnt< ( STAGES - 2 ) * NJW >();
-  else                            wait_vmcnt< 0 >();
+  else if constexpr( FIRST_VMCNT == 0 ) wait_vmcnt< 0 >();
+  else {
+    if( l_pend ) wait_vmcnt< 63 >();
+    else         wait_vmcnt< ( STAGES - 2 ) * NJW >();
+  }
   barrier_lds();
   static_for< U >( [&]( auto rc ) __attribute__( ( always_inline ) ) {
     constexpr int l_r = decltype( rc )::value;
@@ -442,16 +454,9 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_body(
       constexpr int l_p = l_q % NMF;                 // MFMA within the substep
       constexpr int l_i = kMo.i[l_p];
       constexpr int l_j = kMo.j[l_p];
-      if constexpr( SWAPAB ) {
-        l_acc[l_i][l_j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16( FrB::value( l_pb[l_s][l_j] ),
-                                                                   FrA::value( l_pa[l_s][l_i] ),
-                                                                   l_acc[l_i][l_j], 0, 0, 0 );
-      }
-      else {
-        l_acc[l_i][l_j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16( FrA::value( l_pa[l_s][l_i] ),
-                                                                   FrB::value( l_pb[l_s][l_j] ),
-                                                                   l_acc[l_i][l_j], 0, 0, 0 );
-      }
+      l_acc[l_i][l_j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16( FrA::value( l_pa[l_s][l_i] ),
+                                                                 FrB::value( l_pb[l_s][l_j] ),
+                                                                 l_acc[l_i][l_j], 0, 0, 0 );
       if constexpr( l_s == 0 ) {
         // fragments of substep 1 of this step
         static_for< U >( [&]( auto rc ) __attribute__( ( always_inline ) ) {
@@ -470,8 +475,9 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_body(
           // are in flight: all of steps t + 2 .. t + STAGES - 2 (issued in
           // earlier steps) and the DMA_BEFORE loads of step t + STAGES - 1
           // issued so far in this step
-          if constexpr( DMA ) wait_vmcnt< ( STAGES - 3 ) * NJW + DMA_BEFORE >();
-          else                wait_vmcnt< 0 >();
+          if( FIRST_VMCNT == 1 && l_pend && l_t + 1 <= STAGES - 2 ) wait_vmcnt< 63 >();
+          else if constexpr( DMA ) wait_vmcnt< ( STAGES - 3 ) * NJW + DMA_BEFORE >();
+          else                     wait_vmcnt< 0 >();
           wait_lgkmcnt0();
           barrier_lds();
         }
@@ -516,7 +522,7 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_scheduled(
     f32x16 ( &l_acc )[TM][TN], char * l_lds, LdA & l_lda, LdB & l_ldb, FrA const & l_fra, FrB const & l_frb,
     i32x4 l_ra, i32x4 l_rb, int l_wave, int32_t l_K, int32_t l_nk, uint32_t l_kb_a, uint32_t l_kb_b ) {
   prologue_issue< BK, STAGES >( l_lds, l_lda, l_ldb, l_ra, l_rb, l_wave, l_K, l_kb_a, l_kb_b );
-  mainloop_body< BM, BN, BK, WM, WN, MA, MB, STAGES, -1, false >( l_acc, l_lds, l_lda, l_ldb, l_fra, l_frb, l_ra,
+  mainloop_body< BM, BN, BK, WM, WN, MA, MB, STAGES, -1 >( l_acc, l_lds, l_lda, l_ldb, l_fra, l_frb, l_ra,
                                                                 l_rb, l_wave, l_K, l_nk, l_kb_a, l_kb_b );
   // the prologue's loads past the last step (zeros) still target LDS: drain
   // them before the epilogue reuses it
@@ -739,6 +745,7 @@ void contract_dma_persistent_kernel( ContractArgs a ) {
   constexpr int OPS = STAGES * ( SA + SB );              // operand stage buffers
   constexpr int TABS = EpilogueLds< BM, BN, WM, WN, TM, TN >::TABS;
   static_assert( BK == 32 && STAGES >= 3, "persistent kernel runs the scheduled BK 32 loop" );
+  static_assert( 16 * TM * TN >= 63, "vmcnt(63) waits need 63 stores behind the prologue" );
 
   __shared__ __attribute__( ( aligned( 1024 ) ) ) char l_lds[OPS + TABS];
   int32_t * l_tabs_lds = reinterpret_cast< int32_t * >( l_lds + OPS );
@@ -824,10 +831,10 @@ void contract_dma_persistent_kernel( ContractArgs a ) {
       for( int l_j = 0; l_j < TN; l_j++ )
         l_acc[l_i][l_j] = f32x16( 0.0f );
     if( l_nk > 0 ) {
-      // the previous task's output stores may still be in flight behind this
-      // task's prologue loads: the first wait is for everything
-      mainloop_body< BM, BN, BK, WM, WN, MA, MB, STAGES, 0, false >( l_acc, l_lds, l_lda, l_ldb, l_fra, l_frb, l_ra,
-                                                                   l_rb, l_wave, l_K, l_nk, l_kb_a, l_kb_b );
+      // the previous task's output stores (from the second task on) were
+      // issued after this task's prologue loads
+      mainloop_body< BM, BN, BK, WM, WN, MA, MB, STAGES, 1 >( l_acc, l_lds, l_lda, l_ldb, l_fra, l_frb, l_ra, l_rb,
+                                                             l_wave, l_K, l_nk, l_kb_a, l_kb_b, l_t > 0 );
     }
     // every wave is done with the operand buffers (and nothing of this task
     // is still loading into them)
