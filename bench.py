@@ -345,7 +345,7 @@ def bench_c5(torch, eir, stream, steps, warmup, settle=0.0):
     # the same tree replayed as a recorded HIP graph (needs a stream of its own)
     gs = torch.cuda.Stream()
     e = host.Expression(expr, sizes, path, tensors, stream=gs)
-    _, res["per_launch_graph"] = time_launches(torch, gs, e.eval_graph_async, steps, warmup)
+    _, res["per_launch_graph"] = time_launches(torch, gs, e.eval_graph_async, steps, warmup, settle=settle)
     e.close()
     return res
 
