@@ -96,6 +96,7 @@ struct PermArgs {
   int64_t  c_s_in;
   int64_t  c_s_out;
   int32_t  c_chunk;
+  int64_t  c_nblk;    // workgroups along c (set at launch)
   int32_t  vec_wide;  // COPY_VEC / FILL, bf16: 8-element (16-byte) vectors allowed
   int32_t  slot_pi;   // REG4: LDS pitch (16-byte slots) of i and of c
   int32_t  slot_pc;

@@ -98,22 +98,33 @@ __device__ inline void store_stream( V * p, V const & v ) {
   }
 }
 
+// Next digit of a workgroup index in the mixed radix of the grid: returns
+// io_rest % i_size and leaves io_rest / i_size.  Every radix is a factor of
+// the grid size, which the launch keeps below 2^31, so 32-bit unsigned
+// division is exact; the 64-bit one is a long emulated sequence that delayed
+// every workgroup's first load by several hundred instructions.
+__device__ inline int64_t grid_digit( uint32_t & io_rest, int64_t i_size ) {
+  uint32_t const l_s = uint32_t( i_size );
+  uint32_t const l_q = io_rest / l_s;
+  uint32_t const l_r = io_rest - l_q * l_s;
+  io_rest = l_q;
+  return int64_t( l_r );
+}
+
 // LDS-tiled transpose of one 64x64 (i, o) tile per workgroup.
 template< typename T >
 __global__ __launch_bounds__( kThreads )
 void perm_transpose_kernel( PermArgs a ) {
   __shared__ T l_tile[kTile][kTile + 1];
 
-  int64_t l_bid = blockIdx.x;
-  int64_t l_ti  = l_bid % a.tiles_i;  l_bid /= a.tiles_i;
-  int64_t l_to  = l_bid % a.tiles_o;
-  int64_t l_bb  = l_bid / a.tiles_o;
+  uint32_t l_bid = blockIdx.x;
+  int64_t const l_ti = grid_digit( l_bid, a.tiles_i );
+  int64_t const l_to = grid_digit( l_bid, a.tiles_o );
 
   int64_t l_off_in  = 0;
   int64_t l_off_out = 0;
   for( int l_d = a.num_batch - 1; l_d >= 0; l_d-- ) {
-    int64_t l_idx = l_bb % a.batch_size[l_d];
-    l_bb /= a.batch_size[l_d];
+    int64_t const l_idx = grid_digit( l_bid, a.batch_size[l_d] );
     l_off_in  += l_idx * a.batch_s_in[l_d];
     l_off_out += l_idx * a.batch_s_out[l_d];
   }
@@ -210,13 +221,12 @@ void perm_tiled_kernel( PermArgs a ) {
   extern __shared__ __attribute__( ( aligned( 16 ) ) ) char l_lds_raw[];
   T * l_tile = reinterpret_cast< T * >( l_lds_raw );
 
-  int64_t l_bid = blockIdx.x;
+  uint32_t l_bid = blockIdx.x;
   int64_t l_off_in = 0, l_off_out = 0;
   uint32_t l_lim = 0;
   bool l_full = true;
   for( int l_k = 0; l_k < a.tile_nd; l_k++ ) {
-    int64_t const l_b = l_bid % a.tile_nblk[l_k];
-    l_bid /= a.tile_nblk[l_k];
+    int64_t const l_b = grid_digit( l_bid, a.tile_nblk[l_k] );
     int64_t const l_c0 = l_b * a.tile_ext[l_k];
     int64_t const l_left = a.tile_size[l_k] - l_c0;
     int64_t const l_n = l_left < a.tile_ext[l_k] ? l_left : a.tile_ext[l_k];
@@ -226,8 +236,7 @@ void perm_tiled_kernel( PermArgs a ) {
     l_off_out += l_c0 * a.tile_s_out[l_k];
   }
   for( int l_d = a.num_batch - 1; l_d >= 0; l_d-- ) {
-    int64_t const l_idx = l_bid % a.batch_size[l_d];
-    l_bid /= a.batch_size[l_d];
+    int64_t const l_idx = grid_digit( l_bid, a.batch_size[l_d] );
     l_off_in  += l_idx * a.batch_s_in[l_d];
     l_off_out += l_idx * a.batch_s_out[l_d];
   }
@@ -366,15 +375,12 @@ void perm_reg4_kernel( PermArgs a ) {
   int32_t const l_pc  = a.slot_pc;                   // slots per c (size_i * pi + padding)
   int32_t const l_used = l_nig * l_nog * l_cw;       // threads with a block
 
-  int64_t const l_ncb = ( a.c_size + l_ct - 1 ) / l_ct;
-  int64_t l_bid = blockIdx.x;
-  int64_t const l_cbase = ( l_bid % l_ncb ) * l_ct;
-  l_bid /= l_ncb;
+  uint32_t l_bid = blockIdx.x;
+  int64_t const l_cbase = grid_digit( l_bid, a.c_nblk ) * l_ct;
   int64_t l_off_in  = 0;
   int64_t l_off_out = 0;
   for( int l_d = a.num_batch - 1; l_d >= 0; l_d-- ) {
-    int64_t const l_idx = l_bid % a.batch_size[l_d];
-    l_bid /= a.batch_size[l_d];
+    int64_t const l_idx = grid_digit( l_bid, a.batch_size[l_d] );
     l_off_in  += l_idx * a.batch_s_in[l_d];
     l_off_out += l_idx * a.batch_s_out[l_d];
   }
@@ -456,8 +462,10 @@ void perm_reg4_kernel( PermArgs a ) {
 // One thread per VW consecutive output elements of the innermost dim.
 // Dims are (outer -> inner) in a.batch_*; for VW > 1 the innermost dim has
 // unit stride in both tensors and a size divisible by VW (VW elements are one
-// 16-byte vector for bf16 and fp32, 32 bytes for fp64).
-template< typename T, int VW, bool FILL >
+// 16-byte vector for bf16 and fp32, 32 bytes for fp64).  I is the type of
+// the element index the coordinates are decoded from: uint32_t when the
+// element count fits it (32-bit division), else uint64_t.
+template< typename T, int VW, bool FILL, typename I >
 __global__ __launch_bounds__( kThreads )
 void perm_gather_kernel( PermArgs a ) {
   typedef VecN< T, VW > V;
@@ -465,13 +473,14 @@ void perm_gather_kernel( PermArgs a ) {
   for( int64_t l_item = int64_t( blockIdx.x ) * kThreads + threadIdx.x;
        l_item < l_num_items;
        l_item += int64_t( gridDim.x ) * kThreads ) {
-    int64_t l_rem = l_item * VW;
+    I l_rem = I( l_item * VW );
     int64_t l_off_in  = 0;
     int64_t l_off_out = 0;
     for( int l_d = a.num_batch - 1; l_d >= 0; l_d-- ) {
-      int64_t l_sz  = a.batch_size[l_d];
-      int64_t l_idx = l_rem % l_sz;
-      l_rem /= l_sz;
+      I const l_sz  = I( a.batch_size[l_d] );
+      I const l_q   = l_rem / l_sz;
+      int64_t const l_idx = int64_t( l_rem - l_q * l_sz );
+      l_rem = l_q;
       l_off_in  += l_idx * a.batch_s_in[l_d];
       l_off_out += l_idx * a.batch_s_out[l_d];
     }
@@ -517,6 +526,8 @@ int launch_reg4( PermutePlan const & p, PermArgs const & a, int64_t blocks, hipS
   return fail( ETIR_UNDEFINED_ERROR, "permute: no REG4 kernel for this workgroup size" );
 }
 
+template< typename X > struct IdxTag { typedef X type; };
+
 template< typename T >
 int launch_typed( PermutePlan const & p,
                   PermArgs          & a,
@@ -536,7 +547,8 @@ int launch_typed( PermutePlan const & p,
     }
   }
   else if( p.mode == PermMode::REG4 ) {
-    int64_t const l_blocks = ( ( a.c_size + a.c_chunk - 1 ) / a.c_chunk ) * a.num_batch_total;
+    a.c_nblk = ( a.c_size + a.c_chunk - 1 ) / a.c_chunk;
+    int64_t const l_blocks = a.c_nblk * a.num_batch_total;
     if( l_blocks > 0x7fffffffLL ) {
       return fail( ETIR_UNDEFINED_ERROR, "permute: grid too large" );
     }
@@ -559,17 +571,22 @@ int launch_typed( PermutePlan const & p,
     int64_t l_blocks = ( l_items + kThreads - 1 ) / kThreads;
     l_blocks = std::min< int64_t >( l_blocks, 65536 );
     if( l_blocks < 1 ) l_blocks = 1;
-    bool const l_fill = ( p.mode == PermMode::FILL );
     dim3 const l_g( (uint32_t) l_blocks );
-    if( l_fill ) {
-      if( l_vw == 8 )      hipLaunchKernelGGL( ( perm_gather_kernel< T, 8, true > ), l_g, dim3( kThreads ), 0, stream, a );
-      else if( l_vw == 4 ) hipLaunchKernelGGL( ( perm_gather_kernel< T, 4, true > ), l_g, dim3( kThreads ), 0, stream, a );
-      else                 hipLaunchKernelGGL( ( perm_gather_kernel< T, 1, true > ), l_g, dim3( kThreads ), 0, stream, a );
+    auto launch = [&]( auto i_fill, auto i_idx ) {
+      constexpr bool l_fill = decltype( i_fill )::value;
+      typedef typename decltype( i_idx )::type I;
+      if( l_vw == 8 )      hipLaunchKernelGGL( ( perm_gather_kernel< T, 8, l_fill, I > ), l_g, dim3( kThreads ), 0, stream, a );
+      else if( l_vw == 4 ) hipLaunchKernelGGL( ( perm_gather_kernel< T, 4, l_fill, I > ), l_g, dim3( kThreads ), 0, stream, a );
+      else                 hipLaunchKernelGGL( ( perm_gather_kernel< T, 1, l_fill, I > ), l_g, dim3( kThreads ), 0, stream, a );
+    };
+    bool const l_small = a.num_elements <= int64_t( UINT32_MAX );
+    if( p.mode == PermMode::FILL ) {
+      if( l_small ) launch( std::true_type(), IdxTag< uint32_t >() );
+      else          launch( std::true_type(), IdxTag< uint64_t >() );
     }
     else {
-      if( l_vw == 8 )      hipLaunchKernelGGL( ( perm_gather_kernel< T, 8, false > ), l_g, dim3( kThreads ), 0, stream, a );
-      else if( l_vw == 4 ) hipLaunchKernelGGL( ( perm_gather_kernel< T, 4, false > ), l_g, dim3( kThreads ), 0, stream, a );
-      else                 hipLaunchKernelGGL( ( perm_gather_kernel< T, 1, false > ), l_g, dim3( kThreads ), 0, stream, a );
+      if( l_small ) launch( std::false_type(), IdxTag< uint32_t >() );
+      else          launch( std::false_type(), IdxTag< uint64_t >() );
     }
   }
   hipError_t l_err = hipGetLastError();
