@@ -139,7 +139,7 @@ int etir_hip_plan_describe( etir_plan_t plan, char * buf, int64_t len ) {
     l_s = plan->cont.desc;
   }
   else {
-    static char const * l_modes[] = { "fill", "transpose", "copy_vec", "gather", "tiled", "reg4" };
+    static char const * l_modes[] = { "fill", "transpose", "copy_vec", "gather", "tiled", "reg4", "rows" };
     etir::PermutePlan const & p = plan->perm;
     char l_tmp[256];
     std::snprintf( l_tmp, sizeof( l_tmp ), "permute %s dims=%d elems=%lld vec=%d",
@@ -151,6 +151,11 @@ int etir_hip_plan_describe( etir_plan_t plan, char * buf, int64_t len ) {
         l_s += ( l_k ? "," : "" ) + std::to_string( p.args.tile_ext[l_k] );
       }
       l_s += "] pad=" + std::to_string( p.args.tile_pad );
+    }
+    if( p.mode == etir::PermMode::ROWS ) {
+      l_s += " row=" + std::to_string( p.rows_len ) + "/" + std::to_string( p.rows_vw )
+           + " tile=" + std::to_string( p.args.rows_ex ) + "x" + std::to_string( p.args.rows_ey )
+           + " pitch=" + std::to_string( p.args.rows_pitch );
     }
     if( p.mode == etir::PermMode::REG4 ) {
       l_s += " i=" + std::to_string( p.args.size_i ) + " o=" + std::to_string( p.args.size_o )

@@ -48,7 +48,8 @@ enum class PermMode : int32_t {
   COPY_VEC  = 2,  // both innermost dims unit-stride: vectorised strided copy
   GATHER    = 3,  // anything else: one thread per output element
   TILED     = 4,  // small unit-stride dims: tiles over both tensors' innermost runs
-  REG4      = 5   // short unit-stride dims: 4 x 4 register transposes, 16-byte rows through LDS
+  REG4      = 5,  // short unit-stride dims: 4 x 4 register transposes, 16-byte rows through LDS
+  ROWS      = 6   // shared short unit-stride dim: tiles of whole rows, both sides' runs contiguous
 };
 
 constexpr int kPermTileDims = 4;   // dims of a TILED tile (2 per run at most)
@@ -101,6 +102,19 @@ struct PermArgs {
   int32_t  slot_pi;   // REG4: LDS pitch (16-byte slots) of i and of c
   int32_t  slot_pc;
   int32_t  nt_store;  // TRANSPOSE: streaming (non-temporal) output stores
+  // ROWS: rows of the shared unit-stride dim (g chunks of the kernel's vector
+  // width each); x continues the input's run, y the output's; tiles of
+  // rows_ex x rows_ey rows, parked in LDS at rows_pitch chunks per x
+  int32_t  rows_g;
+  int32_t  rows_ex;
+  int32_t  rows_ey;
+  int32_t  rows_pitch;
+  int64_t  rows_nx;
+  int64_t  rows_ny;
+  int64_t  rows_nbx;
+  int64_t  rows_nby;
+  int64_t  rows_s_in_y;
+  int64_t  rows_s_out_x;
 };
 
 struct PermutePlan {
@@ -120,6 +134,8 @@ struct PermutePlan {
   PermArgs args{};                       // pointers filled at execute time
   void *   d_tables = nullptr;           // TILED: device offset tables (owned)
   int32_t  tile_vw = 1;                  // TILED: elements per table entry (1 or 4)
+  int32_t  rows_vw = 1;                  // ROWS: elements per chunk (16, 8 or 4 bytes; 1 element when unaligned)
+  int64_t  rows_len = 0;                 // ROWS: row length (elements of the shared unit-stride dim)
 };
 
 // frees the device memory of a permutation plan

@@ -459,6 +459,128 @@ void perm_reg4_kernel( PermArgs a ) {
   }
 }
 
+// Rows (ROWS): both tensors have the same unit-stride dim u, so the
+// permutation moves whole rows of R = rows_g * VW elements.  x is the dim
+// that continues the input's contiguous run (input stride R), y the one that
+// continues the output's (output stride R).  A workgroup moves a tile of
+// rows_ex x rows_ey rows: it reads the tile's ey input runs (ex rows each,
+// contiguous), parks every chunk of VW elements in LDS at slot
+// x * rows_pitch + y * g + c (the output's order) and writes the tile's ex
+// output runs (ey rows each, contiguous).  Every index advances by adds (the
+// step of the workgroup's threads is split into runs, rows and chunks once
+// per tile); kPer chunks per thread are loaded before any is stored.
+// raw bits of one chunk of B bytes (vector types stay in registers where
+// arrays of the element structs were placed in scratch memory)
+template< int B > struct RawChunk { typedef uint32_t type __attribute__( ( ext_vector_type( B / 4 ) ) ); };
+template<> struct RawChunk< 4 > { typedef uint32_t type; };
+template<> struct RawChunk< 2 > { typedef uint16_t type; };
+
+template< typename T, int VW >
+__global__ __launch_bounds__( kThreads )
+void perm_rows_kernel( PermArgs a ) {
+  typedef typename RawChunk< int( VW * sizeof( T ) ) >::type V;
+  typedef VecN< T, VW > E;
+  constexpr int kPer = 8;
+  extern __shared__ __attribute__( ( aligned( 16 ) ) ) char l_lds_raw[];
+  V * l_slots = reinterpret_cast< V * >( l_lds_raw );
+
+  uint32_t l_bid = blockIdx.x;
+  int64_t const l_bx = grid_digit( l_bid, a.rows_nbx );
+  int64_t const l_by = grid_digit( l_bid, a.rows_nby );
+  int64_t l_off_in = 0, l_off_out = 0;
+  for( int l_d = a.num_batch - 1; l_d >= 0; l_d-- ) {
+    int64_t const l_idx = grid_digit( l_bid, a.batch_size[l_d] );
+    l_off_in  += l_idx * a.batch_s_in[l_d];
+    l_off_out += l_idx * a.batch_s_out[l_d];
+  }
+  int32_t const l_g  = a.rows_g;
+  int64_t const l_x0 = int64_t( l_bx ) * a.rows_ex;
+  int64_t const l_y0 = int64_t( l_by ) * a.rows_ey;
+  int32_t const l_nx = int32_t( min( int64_t( a.rows_ex ), a.rows_nx - l_x0 ) );
+  int32_t const l_ny = int32_t( min( int64_t( a.rows_ey ), a.rows_ny - l_y0 ) );
+  int64_t const l_len = int64_t( l_g ) * VW;
+  T const * l_in  = reinterpret_cast< T const * >( a.in ) + l_off_in + l_x0 * l_len + l_y0 * a.rows_s_in_y;
+  T       * l_out = reinterpret_cast< T * >( a.out ) + l_off_out + l_y0 * l_len + l_x0 * a.rows_s_out_x;
+  int32_t const l_pitch = a.rows_pitch;
+  int32_t const l_tid   = threadIdx.x;
+
+  // read: chunk j = (y, x, c), c fastest -- the tile's input runs in turn;
+  // r = x * g + c is the chunk's place in its run
+  int32_t const l_rrun = l_nx * l_g;
+  int32_t const l_n    = l_ny * l_rrun;
+  {
+    // the step of kThreads chunks as (sy runs, sx rows, sc chunks)
+    int32_t const l_sy = kThreads / l_rrun;
+    int32_t const l_sx = ( kThreads - l_sy * l_rrun ) / l_g;
+    int32_t const l_sc = kThreads - l_sy * l_rrun - l_sx * l_g;
+    int32_t l_y = l_tid / l_rrun;
+    int32_t l_x = ( l_tid - l_y * l_rrun ) / l_g;
+    int32_t l_c = l_tid - l_y * l_rrun - l_x * l_g;
+    for( int32_t l_j0 = 0; l_j0 < l_n; l_j0 += kPer * kThreads ) {
+      V       l_v[kPer];
+      int32_t l_s[kPer];
+#pragma unroll
+      for( int l_p = 0; l_p < kPer; l_p++ ) {
+        l_s[l_p] = -1;
+        if( l_j0 + l_p * kThreads + l_tid < l_n ) {
+          l_v[l_p] = *reinterpret_cast< V const * >( l_in + int64_t( l_y ) * a.rows_s_in_y
+                                                          + int64_t( l_x * l_g + l_c ) * VW );
+          l_s[l_p] = l_x * l_pitch + l_y * l_g + l_c;
+        }
+        l_c += l_sc;
+        l_x += l_sx;
+        l_y += l_sy;
+        if( l_c >= l_g )  { l_c -= l_g;  l_x++; }
+        if( l_x >= l_nx ) { l_x -= l_nx; l_y++; }
+      }
+#pragma unroll
+      for( int l_p = 0; l_p < kPer; l_p++ ) {
+        if( l_s[l_p] >= 0 ) l_slots[l_s[l_p]] = l_v[l_p];
+      }
+    }
+  }
+  __syncthreads();
+  // write: chunk j = (x, w), w = y * g + c fastest -- the tile's output runs
+  // in turn
+  int32_t const l_wrun = l_ny * l_g;
+  {
+    int32_t const l_sx = kThreads / l_wrun;
+    int32_t const l_sw = kThreads - l_sx * l_wrun;
+    int32_t l_x = l_tid / l_wrun;
+    int32_t l_w = l_tid - l_x * l_wrun;
+    for( int32_t l_j0 = 0; l_j0 < l_n; l_j0 += kPer * kThreads ) {
+      V       l_v[kPer];
+      int64_t l_o[kPer];
+#pragma unroll
+      for( int l_p = 0; l_p < kPer; l_p++ ) {
+        l_o[l_p] = -1;
+        if( l_j0 + l_p * kThreads + l_tid < l_n ) {
+          l_v[l_p] = l_slots[l_x * l_pitch + l_w];
+          l_o[l_p] = int64_t( l_x ) * a.rows_s_out_x + int64_t( l_w ) * VW;
+        }
+        l_w += l_sw;
+        l_x += l_sx;
+        if( l_w >= l_wrun ) { l_w -= l_wrun; l_x++; }
+      }
+#pragma unroll
+      for( int l_p = 0; l_p < kPer; l_p++ ) {
+        if( l_o[l_p] < 0 ) continue;
+        V * l_ptr = reinterpret_cast< V * >( l_out + l_o[l_p] );
+        if( a.add ) {
+          E const l_old = __builtin_bit_cast( E, *l_ptr );
+          E       l_sum = __builtin_bit_cast( E, l_v[l_p] );
+#pragma unroll
+          for( int l_e = 0; l_e < VW; l_e++ ) l_sum.v[l_e] = Elem< T >::add( l_old.v[l_e], l_sum.v[l_e] );
+          *l_ptr = __builtin_bit_cast( V, l_sum );
+        }
+        else {
+          __builtin_nontemporal_store( l_v[l_p], l_ptr );
+        }
+      }
+    }
+  }
+}
+
 // One thread per VW consecutive output elements of the innermost dim.
 // Dims are (outer -> inner) in a.batch_*; for VW > 1 the innermost dim has
 // unit stride in both tensors and a size divisible by VW (VW elements are one
@@ -557,6 +679,28 @@ int launch_typed( PermutePlan const & p,
     }
     return launch_reg4< T, 4 >( p, a, l_blocks, stream );
   }
+  else if( p.mode == PermMode::ROWS ) {
+    int64_t const l_blocks = a.rows_nbx * a.rows_nby * a.num_batch_total;
+    if( l_blocks > 0x7fffffffLL ) {
+      return fail( ETIR_UNDEFINED_ERROR, "permute: grid too large" );
+    }
+    std::size_t const l_lds = std::size_t( a.rows_ex ) * a.rows_pitch * p.rows_vw * sizeof( T );
+    auto launch = [&]( auto i_vw ) {
+      constexpr int l_vw = decltype( i_vw )::value;
+      hipLaunchKernelGGL( ( perm_rows_kernel< T, l_vw > ), dim3( (uint32_t) l_blocks ), dim3( kThreads ), l_lds, stream, a );
+    };
+    int64_t const l_cb = p.rows_vw * int64_t( sizeof( T ) );
+    if constexpr( sizeof( T ) <= 8 ) {
+      if( l_cb == 16 ) launch( std::integral_constant< int, int( 16 / sizeof( T ) ) >() );
+    }
+    if constexpr( sizeof( T ) <= 4 ) {
+      if( l_cb == 8 ) launch( std::integral_constant< int, int( 8 / sizeof( T ) ) >() );
+    }
+    if constexpr( sizeof( T ) == 2 ) {
+      if( l_cb == 4 ) launch( std::integral_constant< int, 2 >() );
+    }
+    if( p.rows_vw == 1 ) launch( std::integral_constant< int, 1 >() );
+  }
   else if( p.mode == PermMode::TRANSPOSE ) {
     int64_t l_blocks = a.tiles_i * a.tiles_o * a.num_batch_total;
     if( l_blocks > 0x7fffffffLL ) {
@@ -594,6 +738,150 @@ int launch_typed( PermutePlan const & p,
     return fail( ETIR_UNDEFINED_ERROR, std::string( "permute launch failed: " ) + hipGetErrorString( l_err ) );
   }
   return ETIR_SUCCESS;
+}
+
+// ROWS configuration for a permutation whose tensors share their
+// unit-stride dim dim_u (plan.size/s_in/s_out set); false when the rows are
+// long (the vector copy moves them as well), or no dim continues the input's
+// or the output's run past the rows.
+bool plan_rows( PermutePlan & plan, int dim_u ) {
+  if( char const * l_env = std::getenv( "ETIR_PERM_ROWS" ) ) {
+    if( std::atoi( l_env ) == 0 ) return false;
+  }
+  // rows from 256 bytes on (bf16: 128) move as fast with the vector copy
+  // (fp32 abcd->cabd 16,32,256,64: 68.5 % copy against 64.2 % ROWS; bf16
+  // 16,32,256,64: 65 % against 52-56 %)
+  int64_t l_max_bytes = plan.elem_bytes == 2 ? 128 : 256;
+  if( char const * l_env = std::getenv( "ETIR_PERM_ROWS_MAX_BYTES" ) ) l_max_bytes = std::atoll( l_env );
+  int const     l_n    = plan.num_dims;
+  int64_t const l_esz  = plan.elem_bytes;
+  int64_t const l_len  = plan.size[dim_u];
+  int64_t const l_rowb = l_len * l_esz;
+  if( l_rowb < 16 || l_rowb >= l_max_bytes ) return false;
+  int l_x = -1, l_y = -1;
+  for( int l_d = 0; l_d < l_n; l_d++ ) {
+    if( l_d == dim_u ) continue;
+    if( plan.s_in[l_d]  == l_len && l_x < 0 ) l_x = l_d;
+    if( plan.s_out[l_d] == l_len && l_y < 0 ) l_y = l_d;
+  }
+  if( l_x < 0 || l_y < 0 || l_x == l_y ) return false;
+  // chunk: the widest of 16, 8, 4 bytes that divides the row and every stride
+  auto fits = [&]( int64_t vw ) {
+    if( l_len % vw != 0 ) return false;
+    for( int l_d = 0; l_d < l_n; l_d++ ) {
+      if( l_d != dim_u && ( plan.s_in[l_d] % vw != 0 || plan.s_out[l_d] % vw != 0 ) ) return false;
+    }
+    return true;
+  };
+  int64_t l_vw = 16 / l_esz;
+  while( l_vw > 1 && !( l_vw * l_esz >= 4 && fits( l_vw ) ) ) l_vw /= 2;
+  if( !fits( l_vw ) ) l_vw = 1;
+  int64_t const l_g  = l_len / l_vw;
+  int64_t const l_cb = l_vw * l_esz;
+  int64_t const l_nx = plan.size[l_x], l_ny = plan.size[l_y];
+  // tile extents: at most 18 KB of rows and 1536 chunks (fp32 cabd-like
+  // shapes: 12-18 KB tiles 74-81 % of HBM peak, 24-32 KB 64-74 %, 6 KB
+  // 50-55 %; bf16 with 8-byte chunks: 1152-1536 chunks 70 %, 2304 chunks
+  // 58-61 %), runs of at least 256 bytes (or the whole dim), the fewest
+  // passes of the threads over all tiles, with two passes' worth added per
+  // tile for its index decode and barrier and half as much again per side
+  // whose runs are not whole 128-byte lines (bf16 abc->bac 2048,1024,12:
+  // 32 x 16 rows, runs of 768 and 384 bytes, 70 %; 22 x 23 rows, 528 and 552
+  // bytes, 59 %)
+  int64_t l_ex = 0, l_ey = 0;
+  {
+    int64_t l_best = -1;
+    int64_t const l_rx = std::min< int64_t >( 256, l_nx * l_rowb ), l_ry = std::min< int64_t >( 256, l_ny * l_rowb );
+    for( int64_t l_tx = 1; l_tx <= std::min< int64_t >( l_nx, 256 ); l_tx++ ) {
+      if( l_tx * l_rowb < l_rx ) continue;
+      for( int64_t l_ty = 1; l_ty <= std::min< int64_t >( l_ny, 256 ); l_ty++ ) {
+        if( l_tx * l_ty * l_rowb > 18432 || l_tx * l_ty * l_g > 1536 ) break;
+        if( l_ty * l_rowb < l_ry ) continue;
+        int64_t const l_tiles = ( ( l_nx + l_tx - 1 ) / l_tx ) * ( ( l_ny + l_ty - 1 ) / l_ty );
+        int64_t l_cost = l_tiles * ( ( l_tx * l_ty * l_g + kThreads - 1 ) / kThreads + 2 ) * 4;
+        if( l_tx < l_nx && ( l_tx * l_rowb ) % 128 != 0 ) l_cost += l_cost / 2;
+        if( l_ty < l_ny && ( l_ty * l_rowb ) % 128 != 0 ) l_cost += l_cost / 2;
+        if( l_best < 0 || l_cost < l_best || ( l_cost == l_best && l_tx * l_ty > l_ex * l_ey ) ) {
+          l_best = l_cost;
+          l_ex = l_tx;
+          l_ey = l_ty;
+        }
+      }
+    }
+  }
+  if( char const * l_env = std::getenv( "ETIR_PERM_ROWS_TILE" ) ) {
+    // diagnostic: tile extents "EXxEY", taken when within the dims and 64 KB
+    int64_t l_tx = 0, l_ty = 0;
+    if(    std::sscanf( l_env, "%ldx%ld", &l_tx, &l_ty ) == 2 && l_tx >= 1 && l_ty >= 1
+        && l_tx <= l_nx && l_ty <= l_ny && l_tx * l_ty * l_rowb <= 65536 ) {
+      l_ex = l_tx;
+      l_ey = l_ty;
+    }
+  }
+  if( l_ex == 0 ) return false;
+  // LDS pitch: simulate both phases' accesses of a full tile (128 bytes of
+  // lanes per LDS cycle, 64 four-byte banks) and take the padding with the
+  // fewest conflicts
+  {
+    int64_t const l_lanes  = std::max< int64_t >( 1, 128 / l_cb );
+    int64_t const l_words  = std::max< int64_t >( 1, l_cb / 4 );
+    int64_t const l_groups = 64 / l_words;
+    int64_t const l_n_ch   = l_ex * l_ey * l_g;
+    int64_t l_best = -1;
+    for( int64_t l_pad = 0; l_pad < 16; l_pad++ ) {
+      int64_t const l_pitch = l_ey * l_g + l_pad;
+      if( l_pad > 0 && l_ex * l_pitch * l_cb > 40960 ) break;
+      int64_t l_cost = 0;
+      for( int l_phase = 0; l_phase < 2; l_phase++ ) {
+        for( int64_t l_j0 = 0; l_j0 < l_n_ch; l_j0 += l_lanes ) {
+          int l_cnt[64] = { 0 };
+          int l_mx = 0;
+          for( int64_t l_j = l_j0; l_j < std::min( l_n_ch, l_j0 + l_lanes ); l_j++ ) {
+            int64_t l_slot;
+            if( l_phase == 0 ) {
+              int64_t const l_yy = l_j / ( l_ex * l_g ), l_r = l_j % ( l_ex * l_g );
+              l_slot = ( l_r / l_g ) * l_pitch + l_yy * l_g + l_r % l_g;
+            }
+            else {
+              l_slot = ( l_j / ( l_ey * l_g ) ) * l_pitch + l_j % ( l_ey * l_g );
+            }
+            int64_t const l_bank = ( l_cb >= 4 ? l_slot : l_slot * l_cb / 4 ) % l_groups;
+            l_mx = std::max( l_mx, ++l_cnt[l_bank] );
+          }
+          l_cost += l_mx;
+        }
+      }
+      if( l_best < 0 || l_cost < l_best ) {
+        l_best = l_cost;
+        plan.args.rows_pitch = int32_t( l_pitch );
+      }
+    }
+  }
+  PermArgs & a = plan.args;
+  plan.mode     = PermMode::ROWS;
+  plan.rows_vw  = int32_t( l_vw );
+  plan.rows_len = l_len;
+  a.rows_g       = int32_t( l_g );
+  a.rows_ex      = int32_t( l_ex );
+  a.rows_ey      = int32_t( l_ey );
+  a.rows_nx      = l_nx;
+  a.rows_ny      = l_ny;
+  a.rows_nbx     = ( l_nx + l_ex - 1 ) / l_ex;
+  a.rows_nby     = ( l_ny + l_ey - 1 ) / l_ey;
+  a.rows_s_in_y  = plan.s_in[l_y];
+  a.rows_s_out_x = plan.s_out[l_x];
+  a.num_batch = 0;
+  a.num_batch_total = 1;
+  for( int l_d = 0; l_d < l_n; l_d++ ) {
+    if( l_d == dim_u || l_d == l_x || l_d == l_y ) continue;
+    a.batch_size[a.num_batch]  = plan.size[l_d];
+    a.batch_s_in[a.num_batch]  = plan.s_in[l_d];
+    a.batch_s_out[a.num_batch] = plan.s_out[l_d];
+    a.num_batch_total *= plan.size[l_d];
+    a.num_batch++;
+  }
+  a.vec_ok = l_vw > 1 ? 1 : 0;
+  return true;
 }
 
 // TILED configuration of a fused permutation (plan.size/s_in/s_out set, dim_i /
@@ -1132,6 +1420,12 @@ int plan_permute( int64_t         num_dims,
     return ETIR_SUCCESS;
   }
 
+  if( l_dim_i >= 0 && l_dim_i == l_dim_o && l_n > 2 && plan_rows( plan, l_dim_i ) ) {
+    // a shared unit-stride dim of short rows: whole rows through LDS, no
+    // tables (abcd->cabd 48,36,512,36: xx against yy TB/s tiled)
+    return ETIR_SUCCESS;
+  }
+
   if(    l_dim_i >= 0 && l_dim_o >= 0 && l_n > 1
       && (    ( plan.size[l_dim_i] < kTile && plan.size[l_dim_o] < kTile )
            || std::min( plan.size[l_dim_i], plan.size[l_dim_o] ) <= 8
@@ -1207,7 +1501,8 @@ int launch_permute( PermutePlan const & plan,
   a.out = out;
   // the vector paths need their vectors aligned: 4 elements, REG4 one block
   // row (8 bf16 elements)
-  uintptr_t const l_align = uintptr_t( ( plan.mode == PermMode::REG4 ? plan.reg4_vb : 4 ) * plan.elem_bytes );
+  uintptr_t const l_align = uintptr_t( ( plan.mode == PermMode::REG4 ? plan.reg4_vb
+                                      : plan.mode == PermMode::ROWS ? plan.rows_vw : 4 ) * plan.elem_bytes );
   if( a.vec_ok ) {
     if(    ( uintptr_t( out ) % l_align ) != 0
         || ( plan.mode != PermMode::FILL && ( uintptr_t( in ) % l_align ) != 0 ) ) {
@@ -1221,6 +1516,12 @@ int launch_permute( PermutePlan const & plan,
   }
   PermutePlan l_plan = plan;
   if( plan.mode == PermMode::COPY_VEC && !a.vec_ok ) l_plan.mode = PermMode::GATHER;
+  if( plan.mode == PermMode::ROWS && !a.vec_ok && plan.rows_vw > 1 ) {
+    // unaligned pointers: chunks of one element (same tile, same LDS bytes)
+    l_plan.rows_vw = 1;
+    a.rows_g     = int32_t( plan.rows_len );
+    a.rows_pitch = int32_t( a.rows_ey * plan.rows_len );
+  }
 
   if( plan.elem_bytes == 4 ) return launch_typed< float    >( l_plan, a, stream );
   if( plan.elem_bytes == 8 ) return launch_typed< double   >( l_plan, a, stream );

@@ -133,8 +133,6 @@ TILED_CASES = [
     ("abcde->bdaec", dict(a=12, b=9, c=9, d=12, e=16)),
     ("abcde->bdaec", dict(a=3, b=5, c=6, d=7, e=4)),    # many short dims
     ("abc->cba", dict(a=40, b=2, c=20)),               # runs of two dims each
-    ("abcd->cabd", dict(a=6, b=5, c=70, d=36)),        # same short unit dim d in both
-    ("abcd->cabd", dict(a=3, b=7, c=9, d=5)),          # same unit dim, ragged
     ("abcd->acdb", dict(a=6, b=8, c=10, d=150)),       # one long unit dim, one of 8
     ("abc->cba", dict(a=4, b=100, c=130)),             # one long unit dim, one of 4
     ("abc->cba", dict(a=3, b=70, c=300)),              # ... of 3 (no 16-byte entries)
@@ -149,9 +147,77 @@ def test_permute_tiled(torch_cuda, oracle, expr, sizes, dtype):
     assert "tiled" in desc or (dtype == eir.BF16 and "reg4" in desc), desc
 
 
-@pytest.mark.parametrize("expr,sizes", [TILED_CASES[0], TILED_CASES[2], TILED_CASES[7]])
+@pytest.mark.parametrize("expr,sizes", [TILED_CASES[0], TILED_CASES[2], TILED_CASES[6]])
 def test_permute_tiled_add(torch_cuda, oracle, expr, sizes):
     _check(torch_cuda, oracle, expr, sizes, dtype=eir.FP32, ktype=eir.ADD)
+
+
+# a unit-stride dim shared by both tensors with short rows: whole rows
+# through LDS (ROWS), runs of the input's and the output's next dims
+ROWS_CASES = [
+    ("abcd->cabd", dict(a=6, b=5, c=70, d=36)),        # 144-byte fp32 rows, ragged tiles
+    ("abcd->cabd", dict(a=3, b=7, c=9, d=5)),          # 5-element rows: one-element chunks (fp32)
+    ("abc->bac", dict(a=37, b=300, c=12)),             # 3 chunks per row, ragged both ways
+    ("abc->bac", dict(a=300, b=2, c=12)),              # input runs of 2 rows: many runs per thread step
+    ("abcde->dbcae", dict(a=3, b=4, c=5, d=33, e=8)),  # batch dims b, c
+    ("abcd->cabd", dict(a=2, b=1, c=3000, d=4)),       # 16-byte rows, one long dim
+]
+
+
+@pytest.mark.parametrize("expr,sizes", ROWS_CASES)
+@pytest.mark.parametrize("dtype", [eir.FP32, eir.FP64, eir.BF16])
+@pytest.mark.parametrize("ktype", [eir.COPY, eir.ADD])
+def test_permute_rows(torch_cuda, oracle, expr, sizes, dtype, ktype):
+    desc = _check(torch_cuda, oracle, expr, sizes, dtype=dtype, ktype=ktype, seed=len(expr) + int(ktype))
+    rowb = sizes[expr.split("->")[0][-1]] * {eir.FP32: 4, eir.FP64: 8, eir.BF16: 2}[dtype]
+    # rows of 16 to 255 bytes (bf16: 127) take ROWS; shorter ones the tiled
+    # kernel, longer ones the vector copy
+    assert ("rows" in desc) == (16 <= rowb < (128 if dtype == eir.BF16 else 256)), desc
+
+
+@pytest.mark.parametrize("expr,sizes", [ROWS_CASES[0], ROWS_CASES[2], ROWS_CASES[4]])
+def test_permute_rows_switched_off(torch_cuda, oracle, monkeypatch, expr, sizes):
+    """With ROWS switched off the tiled kernel moves the same shapes."""
+    monkeypatch.setenv("ETIR_PERM_ROWS", "0")
+    for dtype in (eir.FP32, eir.BF16):
+        desc = _check(torch_cuda, oracle, expr, sizes, dtype=dtype, seed=3)
+        assert "tiled" in desc, desc
+
+
+def test_permute_rows_long(torch_cuda, oracle, monkeypatch):
+    """Rows longer than the default limit when the limit is raised: 600-byte
+    rows, more chunks per tile than one pass of the threads covers."""
+    monkeypatch.setenv("ETIR_PERM_ROWS_MAX_BYTES", "100000")
+    for dtype in (eir.FP32, eir.FP64):
+        desc = _check(torch_cuda, oracle, "abcd->cabd", dict(a=3, b=9, c=40, d=150), dtype=dtype, seed=9)
+        assert "rows" in desc, desc
+        desc = _check(torch_cuda, oracle, "abcd->cabd", dict(a=3, b=9, c=40, d=150), dtype=dtype, ktype=eir.ADD)
+        assert "rows" in desc, desc
+
+
+@pytest.mark.parametrize("dtype,offset", [(eir.FP32, 1), (eir.FP32, 2), (eir.BF16, 1), (eir.BF16, 2),
+                                          (eir.BF16, 4), (eir.FP64, 1)])
+def test_permute_rows_unaligned(torch_cuda, oracle, dtype, offset):
+    """ROWS on tensors whose base addresses are offset by a few elements:
+    chunks of one element where the plan's chunk width is not aligned."""
+    torch = torch_cuda
+    expr, sizes = "abcd->cabd", dict(a=6, b=5, c=70, d=28)
+    u = eir.unary_dims(expr, sizes)
+    n = 6 * 5 * 70 * 28
+    rng = np.random.default_rng(50 + offset)
+    x = _inputs(rng, n + offset, dtype)
+    o0 = _inputs(rng, n + offset, dtype)
+    ref = o0[offset:].copy()
+    oracle.permute(u["sizes"], u["strides_in"], u["strides_out"], x[offset:].copy(), ref, dtype=dtype)
+    plan = eir.PermutePlan(u["sizes"], u["strides_in"], u["strides_out"], dtype=dtype, ktype=eir.COPY)
+    dx, do = _to_dev(torch, x), _to_dev(torch, o0)
+    plan.execute(dx[offset:], do[offset:], stream=torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    desc = plan.describe()
+    plan.close()
+    assert "rows" in desc, desc
+    got = _from_dev(do, NPDT[dtype])[offset:]
+    np.testing.assert_array_equal(got.view(np.uint8), ref.view(np.uint8), err_msg=desc)
 
 
 # both unit-stride dims multiples of 4, the shorter <= 16: 4 x 4 register
@@ -308,9 +374,9 @@ def test_permute_4d_bench_shapes(torch_cuda):
 @pytest.mark.parametrize("pad", [0, 4])
 def test_permute_padded_shared_unit_dim(torch_cuda, oracle, pad):
     """A shared unit-stride dim of 36 (b a d <- a b d) whose neighbours sit
-    36 + pad elements apart in both tensors: packed, the tile spans b and a;
-    padded, no run extends past d and the vectorised copy moves it.  Gaps of
-    the output keep their initial values."""
+    36 + pad elements apart in both tensors: packed, the row tiles span b and
+    a; padded, no run extends past d and the vectorised copy moves it.  Gaps
+    of the output keep their initial values."""
     torch = torch_cuda
     a, b, d = 5, 7, 36
     row = d + pad
@@ -330,4 +396,4 @@ def test_permute_padded_shared_unit_dim(torch_cuda, oracle, pad):
     desc = plan.describe()
     plan.close()
     np.testing.assert_array_equal(do.cpu().numpy(), ref, err_msg=desc)
-    assert ("tiled" in desc) == (pad == 0), desc
+    assert ("rows" in desc) == (pad == 0), desc
