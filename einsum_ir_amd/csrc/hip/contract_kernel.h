@@ -416,15 +416,17 @@ __device__ __attribute__( ( always_inline ) ) inline P * uniform_ptr( P * p ) {
 // vector-memory counter on gfx9).  Accumulator layout of v_mfma_f32_32x32x*:
 // register r of lane l holds row = 8*(r/4) + 4*(l/32) + r%4, column = l%32.
 //
-// Fast path -- a full tile, fp32 output, first touch ZERO, last touch none
-// or RELU, output byte offsets below 2^32: no bounds checks, the four row
-// offsets r%4 = 0..3 of one accumulator group come from one ds_read_b128,
-// and every value is one non-temporal buffer_store_dword with a 32-bit byte
-// offset from a per-tile base in scalar registers.  When the output's column index is
-// unit-stride each store writes two 128-byte runs (lanes 0-31 and 32-63).
+// Fast path -- fp32 output, first touch ZERO, last touch none or RELU,
+// output byte offsets below 2^32: the four row offsets r%4 = 0..3 of one
+// accumulator group come from one ds_read_b128, and every value is one
+// non-temporal buffer_store_dword with a 32-bit byte offset from a per-tile
+// base in scalar registers; full tiles store without bounds checks, edge
+// tiles mask the stores of rows and columns past M and N.  When the output's
+// column index is unit-stride each store writes two 128-byte runs (lanes
+// 0-31 and 32-63).
 //
-// General path -- edge tiles, auxiliary tensors, accumulation into the
-// output, bf16 output: each wave stages one 32-row slab of its accumulators in
+// General path -- auxiliary tensors, accumulation into the output, bf16
+// output: each wave stages one 32-row slab of its accumulators in
 // its own LDS area and walks it in a rolled loop, consecutive lanes on
 // consecutive columns.
 template< int BM, int BN, int WM, int WN, int TM, int TN >
@@ -436,36 +438,50 @@ struct EpilogueLds {
   static constexpr int BYTES = TABS + WM * WN * SLAB;
 };
 
-// cache policy of the output stores: non-temporal (the output is written
-// once and not read by the kernel; streaming it keeps the operand tiles that
-// neighbouring workgroups still need in L2)
+// cache policy of the output stores where every store instruction writes
+// whole 128-byte runs: non-temporal (the output is written once and not read
+// by the kernel; streaming it keeps the operand tiles that neighbouring
+// workgroups still need in L2).  Where the columns are not unit-stride, the
+// lines are completed by several stores or workgroups, and temporal stores
+// let L2 merge them (eax,ebcdx->abcdx, the output's unit-stride dim x a C
+// dim: 3.1 TFLOP/s with non-temporal stores).
 constexpr int kStoreNt = 2;
 
-template< int TM, int TN, bool RELU >
+// PARTIAL: an edge tile; only the first l_rows rows and l_cols columns of
+// the tile (counted from the tile's origin) are stored
+template< int TM, int TN, bool RELU, bool PARTIAL = false, bool NT = true >
 __device__ __attribute__( ( always_inline ) ) inline void epilogue_fast_f32(
     float * l_base, f32x16 const ( &l_acc )[TM][TN], int32_t const * l_s_m_out,
-    int32_t const * l_s_n_out, int l_row0, int l_col0, int l_lane ) {
+    int32_t const * l_s_n_out, int l_row0, int l_col0, int l_lane, int l_rows = 0, int l_cols = 0 ) {
   int const l_lr = l_lane & 31;
   int const l_lg = l_lane >> 5;
   __amdgpu_buffer_rsrc_t const l_rs = __builtin_amdgcn_make_buffer_rsrc( uniform_ptr( l_base ), (short) 0,
                                                                          (int) 0xffffffff, 0x00020000 );
   uint32_t l_noff[TN];
+  bool     l_nok[TN];
 #pragma unroll
-  for( int l_j = 0; l_j < TN; l_j++ ) l_noff[l_j] = uint32_t( l_s_n_out[l_col0 + l_j * 32 + l_lr] ) * 4u;
+  for( int l_j = 0; l_j < TN; l_j++ ) {
+    l_noff[l_j] = uint32_t( l_s_n_out[l_col0 + l_j * 32 + l_lr] ) * 4u;
+    l_nok[l_j]  = !PARTIAL || ( l_col0 + l_j * 32 + l_lr < l_cols );
+  }
   static_for< TM >( [&]( auto ic ) __attribute__( ( always_inline ) ) {
     constexpr int l_i = decltype( ic )::value;
     static_for< 4 >( [&]( auto gc ) __attribute__( ( always_inline ) ) {
       constexpr int l_g = decltype( gc )::value;
       typedef int32_t i32x4v __attribute__( ( ext_vector_type( 4 ) ) );
-      i32x4v const l_m4 = *reinterpret_cast< i32x4v const * >( l_s_m_out + l_row0 + l_i * 32 + 8 * l_g + 4 * l_lg );
+      int const l_r0 = l_row0 + l_i * 32 + 8 * l_g + 4 * l_lg;
+      i32x4v const l_m4 = *reinterpret_cast< i32x4v const * >( l_s_m_out + l_r0 );
       static_for< TN >( [&]( auto jc ) __attribute__( ( always_inline ) ) {
         constexpr int l_j = decltype( jc )::value;
         static_for< 4 >( [&]( auto ec ) __attribute__( ( always_inline ) ) {
           constexpr int l_e = decltype( ec )::value;
           float l_v = l_acc[l_i][l_j][4 * l_g + l_e];
           if constexpr( RELU ) l_v = fmaxf( l_v, 0.0f );
-          __builtin_amdgcn_raw_buffer_store_b32( __builtin_bit_cast( uint32_t, l_v ), l_rs,
-                                                 uint32_t( l_m4[l_e] ) * 4u + l_noff[l_j], 0, kStoreNt );
+          if( !PARTIAL || ( l_nok[l_j] && l_r0 + l_e < l_rows ) ) {
+            __builtin_amdgcn_raw_buffer_store_b32( __builtin_bit_cast( uint32_t, l_v ), l_rs,
+                                                   uint32_t( l_m4[l_e] ) * 4u + l_noff[l_j], 0,
+                                                   NT ? kStoreNt : 0 );
+          }
         } );
       } );
     } );
@@ -553,15 +569,28 @@ __device__ __attribute__( ( always_inline ) ) inline void epilogue( ContractArgs
   int const l_row0 = l_wm * TM * 32;      // first tile row of this wave
   int const l_col0 = l_wn * TN * 32;
   bool const l_full = ( l_m0 + BM <= a.M ) && ( l_n0 + BN <= a.N );
-  if(    l_full && a.out_off32 && !a.out_bf16 && a.first_touch == ETIR_KTYPE_ZERO
+  if(    a.out_off32 && !a.out_bf16 && a.first_touch == ETIR_KTYPE_ZERO
       && ( a.last_touch == ETIR_KTYPE_UNDEFINED || a.last_touch == ETIR_KTYPE_RELU ) ) {
+    // plain fp32 output: stores straight from the accumulators, edge tiles
+    // with the rows and columns past M and N masked off (the staged table
+    // entries of those are 0, never stored through)
     float * l_base = reinterpret_cast< float * >( a.out ) + l_coff_out;
-    if( a.last_touch == ETIR_KTYPE_RELU ) {
-      epilogue_fast_f32< TM, TN, true >( l_base, l_acc, l_s_m_out, l_s_n_out, l_row0, l_col0, l_lane );
-    }
-    else {
-      epilogue_fast_f32< TM, TN, false >( l_base, l_acc, l_s_m_out, l_s_n_out, l_row0, l_col0, l_lane );
-    }
+    int const l_rows = int( min( int32_t( BM ), a.M - l_m0 ) );
+    int const l_cols = int( min( int32_t( BN ), a.N - l_n0 ) );
+    auto store = [&]( auto relu_c, auto partial_c, auto nt_c ) __attribute__( ( always_inline ) ) {
+      epilogue_fast_f32< TM, TN, decltype( relu_c )::value, decltype( partial_c )::value, decltype( nt_c )::value >(
+          l_base, l_acc, l_s_m_out, l_s_n_out, l_row0, l_col0, l_lane, l_rows, l_cols );
+    };
+    auto store_nt = [&]( auto relu_c, auto partial_c ) __attribute__( ( always_inline ) ) {
+      if( a.out_nt ) store( relu_c, partial_c, std::true_type() );
+      else           store( relu_c, partial_c, std::false_type() );
+    };
+    auto store_part = [&]( auto relu_c ) __attribute__( ( always_inline ) ) {
+      if( l_full ) store_nt( relu_c, std::false_type() );
+      else         store_nt( relu_c, std::true_type() );
+    };
+    if( a.last_touch == ETIR_KTYPE_RELU ) store_part( std::true_type() );
+    else                                  store_part( std::false_type() );
     return;
   }
 

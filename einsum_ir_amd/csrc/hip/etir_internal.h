@@ -203,7 +203,8 @@ enum TileCfg : int32_t {
   TILE_CPX_F32_64x64    = 9,  // complex (CPX_MADD) kernels, contract_cpx.hip
   TILE_CPX_F64_64x64    = 10,
   TILE_F32_KWAVE_32x32  = 11, // K split over the waves of one workgroup (contract_kwave.hip)
-  TILE_F32_DMA_128x128  = 12  // fp32 direct-to-LDS kernel (contract_f32_dma.hip)
+  TILE_F32_DMA_128x128  = 12, // fp32 direct-to-LDS kernel (contract_f32_dma.hip)
+  TILE_F32_32x256       = 13  // fp32, a short M side (up to 32) against a long N
 };
 
 struct ContractArgs {
@@ -236,6 +237,7 @@ struct ContractArgs {
   int32_t out_bf16;       // output stored as bf16 (RNE)
   int32_t out_off32;      // every output byte offset (M part + N part, C part excluded) is < 2^32
   int32_t c_inner;        // workgroup ids walk C fastest (the output's unit-stride dim is a C dim)
+  int32_t out_nt;         // output columns run in 32-element unit-stride groups: non-temporal stores
   // complex contractions: element offsets of the imaginary parts (A, B, out)
   int64_t cpx_a, cpx_b, cpx_out;
   // affine row tables (tm_a[i] == i * sm_a etc.; -1: not affine), used by
