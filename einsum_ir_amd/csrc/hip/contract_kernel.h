@@ -725,14 +725,17 @@ void contract_kernel( ContractArgs a ) {
     // next step are loaded from global memory between the MFMAs of the first
     // fragment step and stored to the other buffer between those of the last
     // one, so that neither the load issue nor the LDS stores leave the MFMA
-    // pipe idle.  The scheduling barriers keep that placement.
+    // pipe idle.  The scheduling barriers keep that placement.  The last
+    // step skips the fragment steps that lie wholly past K (l_kvalid valid k
+    // in it): their LDS rows are zero padding.
     typedef Loader< BM, BK, T, ESZ, MA > LdA;
     typedef Loader< BN, BK, T, ESZ, MB > LdB;
     constexpr int NS  = ( DT == ETIR_FP32 ) ? BK / 8 : BK / 16;        // fragment steps
     constexpr int NMF = ( DT == ETIR_FP32 ) ? 4 * TM * TN : TM * TN;   // MFMAs per fragment step
     constexpr int NG  = NMF < 4 ? NMF : 4;                              // MFMA groups per fragment step
     constexpr int NL  = LdA::NV + LdB::NV;                              // vectors per thread and step
-    auto l_step = [&]( int l_cur, int32_t l_knext, auto more_c ) __attribute__( ( always_inline ) ) {
+    constexpr int KF  = BK / NS;                                        // k per fragment step
+    auto l_step = [&]( int l_cur, int32_t l_knext, int32_t l_kvalid, auto more_c ) __attribute__( ( always_inline ) ) {
       constexpr bool MORE = decltype( more_c )::value;
       TE const * l_sa = l_lds_a[l_cur];
       TE const * l_sb = l_lds_b[l_cur];
@@ -744,6 +747,9 @@ void contract_kernel( ContractArgs a ) {
       }
       static_for< NS >( [&]( auto sc ) __attribute__( ( always_inline ) ) {
         constexpr int l_s = decltype( sc )::value;
+        if constexpr( !MORE && l_s > 0 ) {
+          if( l_s * KF >= l_kvalid ) return;
+        }
         // fragments of step s: fp32 f32x4 (4 MFMA k-pairs), bf16 bf16x8 (one MFMA)
         typedef typename std::conditional< DT == ETIR_FP32, f32x4, bf16x8 >::type FragT;
         FragT l_fa[TM];
@@ -806,10 +812,10 @@ void contract_kernel( ContractArgs a ) {
 
     int32_t l_kt = 0;
     for( ; l_kt + 1 < l_nk; l_kt++ ) {
-      l_step( l_kt & 1, ( l_kt + 1 ) * BK, std::true_type{} );
+      l_step( l_kt & 1, ( l_kt + 1 ) * BK, BK, std::true_type{} );
       __syncthreads();
     }
-    l_step( l_kt & 1, 0, std::false_type{} );
+    l_step( l_kt & 1, 0, a.K - l_kt * BK, std::false_type{} );
     __syncthreads();
   }
 

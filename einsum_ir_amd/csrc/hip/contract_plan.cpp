@@ -156,7 +156,6 @@ char const * tile_str( int32_t t ) {
     case TILE_CPX_F64_64x64: return "cpx_f64_64x64x16";
     case TILE_F32_KWAVE_32x32: return "f32_kwave_32x32";
     case TILE_F32_DMA_128x128: return "f32_dma_128x128x32";
-    case TILE_F32_32x256:   return "f32_32x256x32";
     default:                return "?";
   }
 }
@@ -172,7 +171,6 @@ void tile_shape( int32_t t, int64_t & bm, int64_t & bn ) {
     case TILE_F32_KWAVE_32x32: bm = 32; bn = 32; break;
     case TILE_BF16_128x128: bm = 128; bn = 128; break;
     case TILE_F32_DMA_128x128: bm = 128; bn = 128; break;
-    case TILE_F32_32x256:   bm = 32;  bn = 256; break;
     default:                bm = 64;  bn = 64;  break;
   }
 }
@@ -432,9 +430,6 @@ int plan_contraction_impl( int64_t            num_loops,
   else if( l_f32 ) {
     // the larger tile unless the smaller one wastes clearly less
     plan.tile = ( score( TILE_F32_128x128 ) >= 0.95 * score( TILE_F32_64x64 ) ) ? TILE_F32_128x128 : TILE_F32_64x64;
-    // a short M side against a long N (TCCG's M = 24 contractions): 32 x 256
-    // tiles waste a quarter of the M side instead of five eighths
-    if( l_kern_m <= 32 && score( TILE_F32_32x256 ) > 1.2 * score( plan.tile ) ) plan.tile = TILE_F32_32x256;
   }
   else {
     if(      n_tiles( TILE_BF16_256x128 ) >= 2 * l_cus ) plan.tile = TILE_BF16_256x128;
@@ -482,11 +477,10 @@ int plan_contraction_impl( int64_t            num_loops,
   if( char const * l_env = ( l_f64 || l_cpx ) ? nullptr : std::getenv( "ETIR_TILE" ) ) {
     // diagnostic override of the tile heuristic (must match the dtype)
     int32_t l_t = std::atoi( l_env );
-    bool const l_t_f32 = ( l_t == TILE_F32_128x128 || l_t == TILE_F32_64x64 || l_t == TILE_F32_32x256
+    bool const l_t_f32 = ( l_t == TILE_F32_128x128 || l_t == TILE_F32_64x64
                            || ( l_t == TILE_F32_DMA_128x128 && l_f32_dma_ok ) );
     bool const l_t_dma = ( l_t == TILE_BF16_DMA_256x256 || l_t == TILE_BF16_DMA_256x128 );
-    bool const l_t_ok = ( ( ( l_t >= 0 && l_t <= TILE_BF16_DMA_256x128 ) || l_t == TILE_F32_DMA_128x128
-                            || l_t == TILE_F32_32x256 )
+    bool const l_t_ok = ( ( ( l_t >= 0 && l_t <= TILE_BF16_DMA_256x128 ) || l_t == TILE_F32_DMA_128x128 )
                           && l_t != TILE_F64_64x64 && l_t_f32 == l_f32 )
                      && ( !l_t_dma || l_dma_ok )
                      && ( l_t != TILE_BF16_DMA_256x128
@@ -966,7 +960,6 @@ int launch_contraction( ContractionPlan const & plan,
   switch( l_tile ) {
     case TILE_F32_128x128:
     case TILE_F32_64x64:
-    case TILE_F32_32x256:
     case TILE_BF16_256x256:
     case TILE_BF16_256x128:
     case TILE_BF16_128x128:

@@ -1,4 +1,4 @@
-// The generic contraction kernel of contract_kernel.h at its seven tile shapes,
+// The generic contraction kernel of contract_kernel.h at its six tile shapes,
 // behind one dispatcher.  Each tile is instantiated for the nine pairs of
 // operand load modes, with and without an affine K offset; a workgroup has
 // one wave per (M, N) wave position.
@@ -6,7 +6,6 @@
 //   tile                 dtype  BM   BN   BK  waves (M x N)  min waves per SIMD (launch bound)
 //   TILE_F32_128x128     fp32   128  128  32  4 x 2          1
 //   TILE_F32_64x64       fp32    64   64  32  2 x 2          1
-//   TILE_F32_32x256      fp32    32  256  32  1 x 4          1
 //   TILE_BF16_256x256    bf16   256  256  64  2 x 4          2
 //   TILE_BF16_256x128    bf16   256  128  32  2 x 2          2
 //   TILE_BF16_128x128    bf16   128  128  64  2 x 2          1
@@ -39,7 +38,6 @@ int launch_contract_tile( int32_t tile, int32_t ma, int32_t mb, bool kaff, Contr
   switch( tile ) {
     case TILE_F32_128x128:  return launch_tile< ETIR_FP32, 128, 128, 32, 4, 2, 1 >( ma, mb, kaff, a, grid, stream );
     case TILE_F32_64x64:    return launch_tile< ETIR_FP32,  64,  64, 32, 2, 2, 1 >( ma, mb, kaff, a, grid, stream );
-    case TILE_F32_32x256:   return launch_tile< ETIR_FP32,  32, 256, 32, 1, 4, 1 >( ma, mb, kaff, a, grid, stream );
     case TILE_BF16_256x256: return launch_tile< ETIR_BF16, 256, 256, 64, 2, 4, 2 >( ma, mb, kaff, a, grid, stream );
     case TILE_BF16_256x128: return launch_tile< ETIR_BF16, 256, 128, 32, 2, 2, 2 >( ma, mb, kaff, a, grid, stream );
     case TILE_BF16_128x128: return launch_tile< ETIR_BF16, 128, 128, 64, 2, 2, 1 >( ma, mb, kaff, a, grid, stream );

@@ -203,8 +203,7 @@ enum TileCfg : int32_t {
   TILE_CPX_F32_64x64    = 9,  // complex (CPX_MADD) kernels, contract_cpx.hip
   TILE_CPX_F64_64x64    = 10,
   TILE_F32_KWAVE_32x32  = 11, // K split over the waves of one workgroup (contract_kwave.hip)
-  TILE_F32_DMA_128x128  = 12, // fp32 direct-to-LDS kernel (contract_f32_dma.hip)
-  TILE_F32_32x256       = 13  // fp32, a short M side (up to 32) against a long N
+  TILE_F32_DMA_128x128  = 12  // fp32 direct-to-LDS kernel (contract_f32_dma.hip)
 };
 
 struct ContractArgs {

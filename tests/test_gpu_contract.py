@@ -232,7 +232,7 @@ def test_missing_aux_is_an_error(torch_cuda):
 
 # every tile configuration on layouts that exercise all load modes, ragged edges
 # and the affine / table K paths (ETIR_TILE overrides the planner's tile choice)
-TILES_F32 = [0, 1, 13]
+TILES_F32 = [0, 1]
 TILES_BF16 = [2, 6, 3, 4]
 TILE_SHAPES = [
     ("zakm,zbkn->zabmn", dict(z=2, a=3, m=64, b=2, n=64, k=96)),   # vec_mn x vec_mn, affine K
@@ -248,14 +248,13 @@ def test_every_tile(torch_cuda, oracle, monkeypatch, tile, expr, sizes):
     monkeypatch.setenv("ETIR_TILE", str(tile))
     dtype = eir.FP32 if tile in TILES_F32 else eir.BF16
     _, desc = run_case(torch_cuda, oracle, expr, sizes, dtype=dtype, seed=tile * 7 + len(expr))
-    names = {0: "f32_128x128", 1: "f32_64x64", 13: "f32_32x256", 2: "bf16_256x256", 6: "bf16_256x128",
+    names = {0: "f32_128x128", 1: "f32_64x64", 2: "bf16_256x256", 6: "bf16_256x128",
              3: "bf16_128x128", 4: "bf16_64x64"}
     assert names[tile] in desc
 
 
-# a short M side (up to 32) against a long N: the 32 x 256 tile; M = 24 and
-# a ragged N make every tile an edge tile of the direct-store epilogue
-# (N of at least 256 tiles: with fewer the 64 x 64 tile's extra workgroups win)
+# a short M side (24) against a long N: every tile is an edge tile of the
+# direct-store epilogue; K = 36 and 40 leave most of the last k step padding
 SHORT_M_SHAPES = [
     ("ebadf,cf->abcde", dict(a=8, b=8, c=24, d=16, e=64, f=36)),     # vec_k x vec_k, K = 36
     ("efbad,cf->abcde", dict(a=8, b=8, c=24, d=16, e=64, f=36)),     # scalar N-side loads
@@ -267,13 +266,12 @@ SHORT_M_SHAPES = [
 @pytest.mark.parametrize("expr,sizes", SHORT_M_SHAPES)
 @pytest.mark.parametrize("first,last", [(eir.ZERO, eir.UNDEFINED_KTYPE), (eir.ZERO, eir.RELU),
                                         (eir.ADD, eir.UNDEFINED_KTYPE)])
-def test_short_m_tile(torch_cuda, oracle, expr, sizes, first, last):
-    _, desc = run_case(torch_cuda, oracle, expr, sizes, first=first, last=last, seed=len(expr) + first)
-    assert "f32_32x256" in desc, desc
+def test_short_m(torch_cuda, oracle, expr, sizes, first, last):
+    run_case(torch_cuda, oracle, expr, sizes, first=first, last=last, seed=len(expr) + first)
 
 
 @pytest.mark.parametrize("nt", ["0", "1"])
-@pytest.mark.parametrize("tile", [0, 1, 13])
+@pytest.mark.parametrize("tile", [0, 1])
 @pytest.mark.parametrize("expr,sizes", [
     ("mk,kn->mn", dict(m=100, k=40, n=300)),                         # unit-stride columns, ragged
     ("eax,ebcdx->abcdx", dict(e=12, a=9, b=5, c=6, d=7, x=8)),       # columns 8 apart (C innermost)
