@@ -318,7 +318,11 @@ void contract_f32_dma_kernel( ContractArgs a ) {
     wait_vmcnt< 0 >();
     barrier_lds();
 
-    for( int32_t l_kt = 0; l_kt < l_nk; l_kt++ ) {
+    // one k step; TAIL (the last step only): skip the fragment steps wholly
+    // past K, which hold zero padding (the first one always runs: it issues
+    // the next step's loads).  The other steps are compiled without the test.
+    auto l_step = [&]( int32_t l_kt, auto tail_c ) __attribute__( ( always_inline ) ) {
+      constexpr bool TAIL = decltype( tail_c )::value;
       int const l_cur = l_kt & 1;
       char const * l_sa = l_lds + l_cur * ( SA + SB );
       char const * l_sb = l_sa + SA;
@@ -327,9 +331,13 @@ void contract_f32_dma_kernel( ContractArgs a ) {
       // are drained by the wait below like all others
       uint32_t const l_nst = l_lds0 + uint32_t( l_cur ^ 1 ) * ( SA + SB );
       int32_t const  l_nk0 = ( l_kt + 1 ) * BK;
+      int32_t const  l_kval = l_K - l_kt * BK;
       l_tab( l_nk0 );
       static_for< NS >( [&]( auto sc ) __attribute__( ( always_inline ) ) {
         constexpr int l_s = decltype( sc )::value;
+        if constexpr( TAIL && l_s > 0 ) {
+          if( l_s * 8 >= l_kval ) return;
+        }
         f32x4 l_fa[TM];
         f32x4 l_fb[TN];
 #pragma unroll
@@ -359,7 +367,9 @@ void contract_f32_dma_kernel( ContractArgs a ) {
       wait_vmcnt< 0 >();
       wait_lgkmcnt0();
       barrier_lds();
-    }
+    };
+    for( int32_t l_kt = 0; l_kt + 1 < l_nk; l_kt++ ) l_step( l_kt, std::false_type() );
+    l_step( l_nk - 1, std::true_type() );
   }
 
   epilogue< BM, BN, WM, WN, TM, TN, T >( a, l_acc, l_tabs, l_lds, l_c, l_m0, l_n0, l_wm, l_wn, l_lane );
