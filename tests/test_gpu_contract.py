@@ -253,6 +253,16 @@ def test_every_tile(torch_cuda, oracle, monkeypatch, tile, expr, sizes):
     assert names[tile] in desc
 
 
+@pytest.mark.parametrize("tile", TILES_F32 + TILES_BF16)
+@pytest.mark.parametrize("k", [5, 40, 100])
+def test_every_tile_k_tail(torch_cuda, oracle, monkeypatch, tile, k):
+    """The last k step runs only its fragment steps that hold valid k (5, 8 or
+    4 of 32; 5, 40 or 36 of 64): results as with the full step."""
+    monkeypatch.setenv("ETIR_TILE", str(tile))
+    dtype = eir.FP32 if tile in TILES_F32 else eir.BF16
+    run_case(torch_cuda, oracle, "km,kn->mn", dict(k=k, m=136, n=264), dtype=dtype, seed=tile + k)
+
+
 # a short M side (24) against a long N: every tile is an edge tile of the
 # direct-store epilogue; K = 36 and 40 leave most of the last k step padding
 SHORT_M_SHAPES = [

@@ -34,6 +34,17 @@ def test_f32_dma_layouts(torch_cuda, oracle, monkeypatch, expr, sizes):
     assert "f32_dma_128x128x32" in desc, desc
 
 
+@pytest.mark.parametrize("k", [4, 20, 36, 44, 56, 88])
+@pytest.mark.parametrize("expr", ["km,kn->mn", "mk,nk->mn"])
+def test_f32_dma_k_tail(torch_cuda, oracle, monkeypatch, expr, k):
+    """The last k step skips its fragment steps wholly past K (4, 20, 4, 12,
+    24 and 24 valid k of 32 in its last step), both operand orientations
+    (K a multiple of 4 keeps K-contiguous rows 16-byte loadable)."""
+    monkeypatch.setenv("ETIR_TILE", "12")
+    _, desc = run_case(torch_cuda, oracle, expr, dict(k=k, m=136, n=264), seed=k)
+    assert "f32_dma_128x128x32" in desc, desc
+
+
 # K of two dims whose strides make it affine for one operand only: the K
 # offsets come from the plan's tables (staged in LDS by the kernel)
 F32_DMA_TABLE_K = [
