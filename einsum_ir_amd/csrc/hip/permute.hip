@@ -111,11 +111,21 @@ __device__ inline int64_t grid_digit( uint32_t & io_rest, int64_t i_size ) {
   return int64_t( l_r );
 }
 
-// LDS-tiled transpose of one 64x64 (i, o) tile per workgroup.
-template< typename T >
+// LDS-tiled transpose of one TI x TO (i, o) tile per workgroup (64 x 64, or
+// 128 x 32 / 32 x 128 when one unit-stride dim is at most 32 long and the
+// other at least 128: a 64 x 64 tile would be half empty).  Threads move 4
+// consecutive elements: reads run along i (TI / 4 threads per o row), writes
+// along o (TO / 4 threads per i row), four passes each.  The LDS pitch is
+// TI + 1 for square tiles and TI + 2 otherwise, which spreads the write
+// phase's column reads over distinct banks.
+template< typename T, int TI, int TO >
 __global__ __launch_bounds__( kThreads )
 void perm_transpose_kernel( PermArgs a ) {
-  __shared__ T l_tile[kTile][kTile + 1];
+  static_assert( TI * TO == 4 * 4 * kThreads, "four passes of 4 elements per thread" );
+  constexpr int PITCH = TI + ( TI == TO ? 1 : 2 );
+  constexpr int RT = TI / 4;              // read: threads per o row
+  constexpr int WT = TO / 4;              // write: threads per i row
+  __shared__ T l_tile[TO][PITCH];
 
   uint32_t l_bid = blockIdx.x;
   int64_t const l_ti = grid_digit( l_bid, a.tiles_i );
@@ -132,16 +142,16 @@ void perm_transpose_kernel( PermArgs a ) {
   T const * l_in  = reinterpret_cast< T const * >( a.in )  + l_off_in;
   T       * l_out = reinterpret_cast< T       * >( a.out ) + l_off_out;
 
-  int64_t const l_i0 = l_ti * kTile;
-  int64_t const l_o0 = l_to * kTile;
+  int64_t const l_i0 = l_ti * TI;
+  int64_t const l_o0 = l_to * TO;
   int const l_t  = threadIdx.x;
-  int const l_c4 = l_t & 15;
-  int const l_r  = l_t >> 4;
+  int const l_c4 = l_t % RT;
+  int const l_r  = l_t / RT;
 
   // read: rows along o, 4 consecutive i per thread
 #pragma unroll
   for( int l_p = 0; l_p < 4; l_p++ ) {
-    int const l_row = l_r + 16 * l_p;
+    int const l_row = l_r + ( kThreads / RT ) * l_p;
     int64_t const l_o = l_o0 + l_row;
     int64_t const l_i = l_i0 + 4 * l_c4;
     T l_v[4] = { T(0), T(0), T(0), T(0) };
@@ -167,14 +177,16 @@ void perm_transpose_kernel( PermArgs a ) {
   __syncthreads();
 
   // write: rows along i, 4 consecutive o per thread
+  int const l_wc4 = l_t % WT;
+  int const l_wr  = l_t / WT;
 #pragma unroll
   for( int l_p = 0; l_p < 4; l_p++ ) {
-    int const l_row = l_r + 16 * l_p;
+    int const l_row = l_wr + ( kThreads / WT ) * l_p;
     int64_t const l_i = l_i0 + l_row;
-    int64_t const l_o = l_o0 + 4 * l_c4;
+    int64_t const l_o = l_o0 + 4 * l_wc4;
     T l_v[4];
 #pragma unroll
-    for( int l_e = 0; l_e < 4; l_e++ ) l_v[l_e] = l_tile[4 * l_c4 + l_e][l_row];
+    for( int l_e = 0; l_e < 4; l_e++ ) l_v[l_e] = l_tile[4 * l_wc4 + l_e][l_row];
 
     if( a.vec_ok ) {
       if( l_i < a.size_i && l_o < a.size_o ) {
@@ -706,7 +718,10 @@ int launch_typed( PermutePlan const & p,
     if( l_blocks > 0x7fffffffLL ) {
       return fail( ETIR_UNDEFINED_ERROR, "permute: grid too large" );
     }
-    hipLaunchKernelGGL( perm_transpose_kernel< T >, dim3( (uint32_t) l_blocks ), dim3( kThreads ), 0, stream, a );
+    dim3 const l_g( (uint32_t) l_blocks );
+    if( p.tr_shape == 1 )      hipLaunchKernelGGL( ( perm_transpose_kernel< T, 128, 32 > ), l_g, dim3( kThreads ), 0, stream, a );
+    else if( p.tr_shape == 2 ) hipLaunchKernelGGL( ( perm_transpose_kernel< T, 32, 128 > ), l_g, dim3( kThreads ), 0, stream, a );
+    else                       hipLaunchKernelGGL( ( perm_transpose_kernel< T, 64, 64 > ), l_g, dim3( kThreads ), 0, stream, a );
   }
   else {
     // bf16 moves 8 elements (16 bytes) per vector where the planner allows it
@@ -1448,8 +1463,27 @@ int plan_permute( int64_t         num_dims,
     a.size_o  = plan.size[l_dim_o];
     a.s_in_o  = plan.s_in[l_dim_o];
     a.s_out_i = plan.s_out[l_dim_i];
-    a.tiles_i = ( a.size_i + kTile - 1 ) / kTile;
-    a.tiles_o = ( a.size_o + kTile - 1 ) / kTile;
+    // tile shape: the one whose padded tile grid wastes the least, 64 x 64
+    // unless another fills at least 1.25 times as much of its tiles (fp32
+    // dcba 32,32,128,128 on 128 x 32: 74 -> 76 % of HBM peak; dbca
+    // 32,64,256,96 61.5 % against 53 %, 96,64,256,32 on 32 x 128 58 %
+    // against 47 %)
+    auto util = [&]( int64_t ti, int64_t to ) {
+      return double( a.size_i ) / double( ( a.size_i + ti - 1 ) / ti * ti )
+           * double( a.size_o ) / double( ( a.size_o + to - 1 ) / to * to );
+    };
+    plan.tr_shape = 0;
+    double l_best = 1.25 * util( kTile, kTile );
+    if( util( 128, 32 ) >= l_best ) { plan.tr_shape = 1; l_best = util( 128, 32 ); }
+    if( util( 32, 128 ) > l_best )  plan.tr_shape = 2;
+    if( char const * l_env = std::getenv( "ETIR_PERM_TR_SHAPE" ) ) {
+      int const l_v = std::atoi( l_env );
+      if( l_v >= 0 && l_v <= 2 ) plan.tr_shape = l_v;
+    }
+    int64_t const l_ti = plan.tr_shape == 1 ? 128 : ( plan.tr_shape == 2 ? 32 : kTile );
+    int64_t const l_to = 4 * 4 * kThreads / l_ti;
+    a.tiles_i = ( a.size_i + l_ti - 1 ) / l_ti;
+    a.tiles_o = ( a.size_o + l_to - 1 ) / l_to;
     a.num_batch = 0;
     a.num_batch_total = 1;
     for( int l_di = 0; l_di < l_n; l_di++ ) {

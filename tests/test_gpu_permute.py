@@ -152,6 +152,24 @@ def test_permute_tiled_add(torch_cuda, oracle, expr, sizes):
     _check(torch_cuda, oracle, expr, sizes, dtype=eir.FP32, ktype=eir.ADD)
 
 
+# transposes whose unit-stride dims are a short one (<= 32) and a long one:
+# 128 x 32 or 32 x 128 tiles (a 64 x 64 tile would be half empty)
+TR_SHAPE_CASES = [
+    ("abcd->dcba", dict(a=20, b=3, c=5, d=200), "tile=128x32"),
+    ("abcd->dcba", dict(a=200, b=3, c=5, d=20), "tile=32x128"),
+    ("abc->cba", dict(a=31, b=6, c=130), "tile=128x32"),       # ragged: 31 of 32, 130 of 256
+    ("abc->cba", dict(a=129, b=4, c=29), "tile=32x128"),
+]
+
+
+@pytest.mark.parametrize("expr,sizes,tile", TR_SHAPE_CASES)
+@pytest.mark.parametrize("dtype", [eir.FP32, eir.FP64])
+@pytest.mark.parametrize("ktype", [eir.COPY, eir.ADD])
+def test_permute_transpose_shapes(torch_cuda, oracle, expr, sizes, tile, dtype, ktype):
+    desc = _check(torch_cuda, oracle, expr, sizes, dtype=dtype, ktype=ktype, seed=sizes["a"] + int(ktype))
+    assert "transpose" in desc and tile in desc, desc
+
+
 # a unit-stride dim shared by both tensors with short rows: whole rows
 # through LDS (ROWS), runs of the input's and the output's next dims
 ROWS_CASES = [
