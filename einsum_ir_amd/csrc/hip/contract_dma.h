@@ -718,14 +718,15 @@ void contract_dma_kernel( ContractArgs a ) {
 // bound.)
 //
 // Runs only contractions whose tiles are all full and take the plain fast
-// epilogue: fp32 output, 32-bit output offsets, ZERO first touch, no last
-// touch (persistent_dma_eligible; a second store variant in the kernel makes
-// the compiler copy the accumulators into VGPRs); the others use
+// epilogue with non-temporal stores: fp32 output, 32-bit output offsets,
+// output columns in unit-stride runs of 32, ZERO first touch, no last touch
+// (persistent_dma_eligible; a second store variant in the kernel makes the
+// compiler copy the accumulators into VGPRs); the others use
 // contract_dma_kernel.
 // ---------------------------------------------------------------------------
 __host__ __device__ inline bool persistent_dma_eligible( ContractArgs const & a, int BM, int BN ) {
-  return a.M % BM == 0 && a.N % BN == 0 && a.out_off32 && !a.out_bf16 && a.first_touch == ETIR_KTYPE_ZERO
-      && a.last_touch == ETIR_KTYPE_UNDEFINED;
+  return a.M % BM == 0 && a.N % BN == 0 && a.out_off32 && a.out_nt && !a.out_bf16
+      && a.first_touch == ETIR_KTYPE_ZERO && a.last_touch == ETIR_KTYPE_UNDEFINED;
 }
 
 template< int BM, int BN, int BK, int WM, int WN, int STAGES >

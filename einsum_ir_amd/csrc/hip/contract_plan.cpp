@@ -836,7 +836,8 @@ int plan_contraction_impl( int64_t            num_loops,
     if( char const * l_env = std::getenv( "ETIR_OUT_NT" ) ) a.out_nt = std::atoi( l_env ) != 0 ? 1 : 0;
   }
   if(    plan.tile == TILE_BF16_DMA_256x256 && plan.dma_variant == 3 && a.M % 256 == 0 && a.N % 256 == 0
-      && a.out_off32 && !a.out_bf16 && a.first_touch == ETIR_KTYPE_ZERO && a.last_touch == ETIR_KTYPE_UNDEFINED ) {
+      && a.out_off32 && a.out_nt && !a.out_bf16 && a.first_touch == ETIR_KTYPE_ZERO
+      && a.last_touch == ETIR_KTYPE_UNDEFINED ) {
     plan.desc += " persistent";
   }
   return ETIR_SUCCESS;
