@@ -286,7 +286,10 @@ einsum_ir::err_t einsum_ir::backend::BinaryPrimitives::reorder_gpu( bool        
   // the output's unit-stride run on the column side (its trailing dims of
   // the column side's type) and its innermost row-side dim: when the run is
   // shorter than a 32-lane store row, consecutive tile rows have to be
-  // neighbours in memory for the stores to fill whole lines
+  // neighbours in memory for the stores to fill whole lines -- worth a new
+  // layout of the row-side child only when the output outweighs that child
+  // (TCCG dega,gfbc->abcdef, 1 MB child, 442 MB output: 38 against 22-33
+  // TFLOP/s; bda,dc->abc, 226 MB child, 14 MB output: kept, 17 -> 34)
   dim_t const l_col_type = l_own[l_col_side];
   int64_t l_col_run = 1;
   for( int64_t l_o = i_num_dims_out - 1; l_o >= 0 && l_t_out[l_o] == l_col_type; l_o-- ) {
@@ -300,6 +303,8 @@ einsum_ir::err_t einsum_ir::backend::BinaryPrimitives::reorder_gpu( bool        
     }
   }
 
+  int64_t l_bytes_out = i_bytes_per_element;
+  for( int64_t l_o = 0; l_o < i_num_dims_out; l_o++ ) l_bytes_out *= size_of( io_dim_ids_out[l_o] );
   // per child: 0 = lay out again, 1 = keep (read along M/N), 2 = keep (read
   // along K), 3 = keep (gathered: little data)
   int l_keep[2] = { 0, 0 };
@@ -313,7 +318,8 @@ einsum_ir::err_t einsum_ir::backend::BinaryPrimitives::reorder_gpu( bool        
     int64_t const l_gathered = l_bytes[l_s] * std::max< int64_t >( 1, l_ext_mn[1 - l_s] / 128 );
     if( l_vec_ok && l_ty == dim_t::K ) l_keep[l_s] = 2;
     else if(    l_vec_ok && l_ty == l_own[l_s]
-             && ( l_s == l_col_side ? l_in == l_o_last : ( l_col_run >= 32 || l_in == l_o_row_last ) ) ) {
+             && ( l_s == l_col_side ? l_in == l_o_last
+                                    : ( l_col_run >= 32 || l_in == l_o_row_last || l_bytes_out < l_bytes[l_s] ) ) ) {
       l_keep[l_s] = 1;
     }
     else if( l_gathered < i_min_bytes_permute ) l_keep[l_s] = 3;
