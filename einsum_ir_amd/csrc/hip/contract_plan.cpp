@@ -508,12 +508,15 @@ int plan_contraction_impl( int64_t            num_loops,
   // tiles (4x the workgroups of 64 x 64) with K divided over the 16 waves of
   // each workgroup, whose partial tiles are added in LDS -- one launch, no
   // workspace (the alternative below, split K, sends S partial outputs
-  // through memory to a second kernel)
+  // through memory to a second kernel).  At most 512 of them, one round of
+  // two workgroups per CU (bench_mlp's 576-tile nodes: 95 us/eval with them,
+  // 90 on split K)
   {
     int64_t const l_t32 = n_tiles( TILE_F32_KWAVE_32x32 );
     bool const l_kw_ok = l_f32 && plan.mode_a == LOAD_VEC_K && plan.mode_b == LOAD_VEC_K && l_k_affine
                       && l_sk_a == 1 && l_sk_b == 1 && l_size_k % 16 == 0 && l_size_k >= 256
                       && l_size_k <= 4096 && n_tiles( plan.tile ) < l_cus && l_t32 >= l_cus / 2
+                      && l_t32 <= 2 * l_cus
                       && std::getenv( "ETIR_NO_KWAVE" ) == nullptr;
     if( l_kw_ok ) {
       // 8 waves up to K = 512, 16 above (config 1, K = 512: 7.58-7.65 us with
