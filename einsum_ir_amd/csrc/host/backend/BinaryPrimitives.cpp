@@ -312,7 +312,23 @@ einsum_ir::err_t einsum_ir::backend::BinaryPrimitives::reorder_gpu( bool        
     if( !l_fixed[l_s] || l_nd[l_s] == 0 ) continue;
     int64_t const l_in = l_ids[l_s][l_nd[l_s] - 1];
     dim_t const l_ty = l_t[l_s][l_nd[l_s] - 1];
-    bool const l_vec_ok = size_of( l_in ) % i_vec == 0;
+    // a K dim innermost is read in vectors along the run of the child's
+    // trailing K dims, which the planner fuses when the other child holds
+    // them in the same order back to back (a child laid out here takes this
+    // one's K order); bench_mlp's input, K = 8 x 98: 16-byte loads as it is
+    int64_t l_run = size_of( l_in );
+    if( l_ty == dim_t::K ) {
+      int const l_o = 1 - l_s;
+      int64_t l_pos = -1;
+      for( int64_t l_d = 0; l_d < l_nd[l_o]; l_d++ ) if( l_ids[l_o][l_d] == l_in ) l_pos = l_d;
+      for( int64_t l_q = 1; l_q < l_nd[l_s]; l_q++ ) {
+        int64_t const l_d = l_nd[l_s] - 1 - l_q;
+        if( l_t[l_s][l_d] != dim_t::K ) break;
+        if( l_fixed[l_o] && ( l_pos - l_q < 0 || l_ids[l_o][l_pos - l_q] != l_ids[l_s][l_d] ) ) break;
+        l_run *= size_of( l_ids[l_s][l_d] );
+      }
+    }
+    bool const l_vec_ok = l_run % i_vec == 0;
     // element gathers of this child are repeated for every tile of the other
     // side (128 columns or rows per tile)
     int64_t const l_gathered = l_bytes[l_s] * std::max< int64_t >( 1, l_ext_mn[1 - l_s] / 128 );
