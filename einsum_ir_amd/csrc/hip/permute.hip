@@ -28,6 +28,8 @@
 //   - anything else is a one-thread-per-element gather.
 #include "etir_internal.h"
 #include <algorithm>
+#include <cinttypes>
+#include <cstdio>
 #include <limits>
 #include <numeric>
 #include <sstream>
@@ -827,7 +829,7 @@ bool plan_rows( PermutePlan & plan, int dim_u ) {
   if( char const * l_env = std::getenv( "ETIR_PERM_ROWS_TILE" ) ) {
     // diagnostic: tile extents "EXxEY", taken when within the dims and 64 KB
     int64_t l_tx = 0, l_ty = 0;
-    if(    std::sscanf( l_env, "%ldx%ld", &l_tx, &l_ty ) == 2 && l_tx >= 1 && l_ty >= 1
+    if(    std::sscanf( l_env, "%" SCNd64 "x%" SCNd64, &l_tx, &l_ty ) == 2 && l_tx >= 1 && l_ty >= 1
         && l_tx <= l_nx && l_ty <= l_ny && l_tx * l_ty * l_rowb <= 65536 ) {
       l_ex = l_tx;
       l_ey = l_ty;
