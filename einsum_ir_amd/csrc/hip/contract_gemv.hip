@@ -1,0 +1,127 @@
+// Contractions with one free side of extent 1 (kernel M == 1 or N == 1):
+//   out[c][m][n] = touch( sum_k A[c][m][k] * B[c][n][k] ),  M == 1 or N == 1.
+//
+// Such a node is a batch of matrix-vector products (einsum-tree nodes whose
+// left or right tensor holds no M or N dims, e.g. the language-model series'
+// "...c,cn->...n" steps).  On an MFMA tile of 64 x 64 one of the two tile
+// sides is a single row, so 63/64 of every tile is padding, and each
+// workgroup stages a 64 x K operand through LDS for 64 outputs.  Here one
+// thread owns one output element and reduces its whole K range in registers:
+// consecutive threads take consecutive indices of the long side (n when
+// M == 1, m when N == 1), so the long operand's loads coalesce when it is
+// unit-stride along that side, and the short operand's address is the same
+// for every thread of a C index (one broadcast cache line).  The bound is the
+// long operand's HBM stream.
+//
+// The K sum runs in ascending k with one fp32 accumulator, the order of the
+// reference's scalar backend (reference src/basic/binary/
+// ContractionBackendScalar.cpp:30, kernel_madd, called once per K index by
+// the loop nest of ContractionBackend.cpp:296-515); the touch kernels are
+// applied once per output element as in the tiled kernels' epilogue
+// (ContractionBackendTpp.cpp:84-163).
+#include "etir_internal.h"
+#include "contract_kernel.h"
+
+namespace etir {
+
+namespace {
+
+template< typename T >
+__device__ inline float gemv_ld( T const * p, int64_t off );
+template<>
+__device__ inline float gemv_ld< float >( float const * p, int64_t off ) { return p[off]; }
+template<>
+__device__ inline float gemv_ld< uint16_t >( uint16_t const * p, int64_t off ) {
+  return kern::bf16_to_f32( p[off] );
+}
+
+template< typename T, bool KAFF >
+__global__ __launch_bounds__( 256 ) void contract_gemv_kernel( ContractArgs a ) {
+  uint64_t const l_total = uint64_t( a.C ) * uint64_t( a.M ) * uint64_t( a.N );
+  uint64_t const l_e = uint64_t( blockIdx.x ) * 256 + threadIdx.x;
+  if( l_e >= l_total ) return;
+  // element index -> (c, m, n), n fastest (m fastest when N == 1)
+  int32_t l_n, l_m, l_c;
+  if( l_total <= 0xffffffffull ) {
+    uint32_t const l_e32 = uint32_t( l_e );
+    uint32_t const l_cm = l_e32 / uint32_t( a.N );
+    l_n = int32_t( l_e32 - l_cm * uint32_t( a.N ) );
+    l_c = int32_t( l_cm / uint32_t( a.M ) );
+    l_m = int32_t( l_cm - uint32_t( l_c ) * uint32_t( a.M ) );
+  }
+  else {
+    uint64_t const l_cm = l_e / uint64_t( a.N );
+    l_n = int32_t( l_e - l_cm * uint64_t( a.N ) );
+    l_c = int32_t( l_cm / uint64_t( a.M ) );
+    l_m = int32_t( l_cm - uint64_t( l_c ) * uint64_t( a.M ) );
+  }
+
+  // the touch kernels' loads first, so they are in flight with the K loop's
+  bool const l_read_out  = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_UNDEFINED );
+  bool const l_aux_first = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_COPY );
+  bool const l_need_aux  = ( a.aux != nullptr ) && ( l_aux_first || a.last_touch == ETIR_KTYPE_ADD );
+  int64_t const l_off = a.tc_out[l_c] + a.tm_out[l_m] + a.tn_out[l_n];
+  float l_aux = 0.0f;
+  if( l_need_aux ) {
+    int64_t const l_aoff = a.tc_aux[l_c] + a.tm_aux[l_m] + a.tn_aux[l_n];
+    l_aux = a.out_bf16 ? kern::bf16_to_f32( reinterpret_cast< uint16_t const * >( a.aux )[l_aoff] )
+                       : reinterpret_cast< float const * >( a.aux )[l_aoff];
+  }
+  float l_old = 0.0f;
+  if( l_read_out ) {
+    l_old = a.out_bf16 ? kern::bf16_to_f32( reinterpret_cast< uint16_t const * >( a.out )[l_off] )
+                       : reinterpret_cast< float const * >( a.out )[l_off];
+  }
+
+  T const * l_pa = reinterpret_cast< T const * >( a.a ) + a.tc_a[l_c] + a.tm_a[l_m];
+  T const * l_pb = reinterpret_cast< T const * >( a.b ) + a.tc_b[l_c] + a.tn_b[l_n];
+  auto koff_a = [&]( int32_t k ) -> int64_t { return KAFF ? int64_t( k ) * a.sk_a : int64_t( a.tk_a[k] ); };
+  auto koff_b = [&]( int32_t k ) -> int64_t { return KAFF ? int64_t( k ) * a.sk_b : int64_t( a.tk_b[k] ); };
+
+  // chunks of 8 k with all 16 loads of a chunk issued before its FMAs (a
+  // rolled loop would wait for every pair), added in ascending k
+  float l_v = 0.0f;
+  int32_t l_k = 0;
+  for( ; l_k + 8 <= a.K; l_k += 8 ) {
+    float l_x[8], l_y[8];
+#pragma unroll
+    for( int l_i = 0; l_i < 8; l_i++ ) {
+      l_x[l_i] = gemv_ld< T >( l_pa, koff_a( l_k + l_i ) );
+      l_y[l_i] = gemv_ld< T >( l_pb, koff_b( l_k + l_i ) );
+    }
+#pragma unroll
+    for( int l_i = 0; l_i < 8; l_i++ ) l_v = fmaf( l_x[l_i], l_y[l_i], l_v );
+  }
+  for( ; l_k < a.K; l_k++ ) {
+    l_v = fmaf( gemv_ld< T >( l_pa, koff_a( l_k ) ), gemv_ld< T >( l_pb, koff_b( l_k ) ), l_v );
+  }
+
+  if( l_read_out ) l_v = l_old + l_v;
+  if( l_aux_first ) l_v = l_aux + l_v;
+  if( a.last_touch == ETIR_KTYPE_RELU ) l_v = fmaxf( l_v, 0.0f );
+  else if( a.last_touch == ETIR_KTYPE_ADD ) l_v = l_v + l_aux;
+  if( a.out_bf16 ) reinterpret_cast< uint16_t * >( a.out )[l_off] = kern::f32_to_bf16_rne( l_v );
+  else             reinterpret_cast< float * >( a.out )[l_off] = l_v;
+}
+
+}  // namespace
+
+int launch_contract_gemv( bool bf16_in, ContractArgs const & a, hipStream_t stream ) {
+  int64_t const l_total = int64_t( a.C ) * a.M * a.N;
+  if( l_total == 0 ) return ETIR_SUCCESS;
+  int64_t const l_blocks = ( l_total + 255 ) / 256;
+  if( l_blocks > 0x7fffffffLL ) return fail( ETIR_UNDEFINED_ERROR, "gemv contraction: grid too large" );
+  dim3 const l_grid( (uint32_t) l_blocks );
+  bool const l_kaff = ( a.k_affine != 0 );
+  if( bf16_in ) {
+    if( l_kaff ) hipLaunchKernelGGL( ( contract_gemv_kernel< uint16_t, true > ), l_grid, dim3( 256 ), 0, stream, a );
+    else         hipLaunchKernelGGL( ( contract_gemv_kernel< uint16_t, false > ), l_grid, dim3( 256 ), 0, stream, a );
+  }
+  else {
+    if( l_kaff ) hipLaunchKernelGGL( ( contract_gemv_kernel< float, true > ), l_grid, dim3( 256 ), 0, stream, a );
+    else         hipLaunchKernelGGL( ( contract_gemv_kernel< float, false > ), l_grid, dim3( 256 ), 0, stream, a );
+  }
+  return ETIR_SUCCESS;
+}
+
+}  // namespace etir

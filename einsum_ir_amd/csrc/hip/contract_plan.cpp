@@ -44,6 +44,7 @@ int launch_contract_bf16_dma( int32_t ma, int32_t mb, int32_t variant, ContractA
 int launch_contract_kwave( int32_t waves, int32_t kw, ContractArgs const & a, uint32_t grid,
                            hipStream_t stream );
 int launch_contract_f32_dma( int32_t ma, int32_t mb, ContractArgs const & a, uint32_t grid, hipStream_t stream );
+int launch_contract_gemv( bool bf16_in, ContractArgs const & a, hipStream_t stream );
 
 namespace {
 
@@ -156,6 +157,7 @@ char const * tile_str( int32_t t ) {
     case TILE_CPX_F64_64x64: return "cpx_f64_64x64x16";
     case TILE_F32_KWAVE_32x32: return "f32_kwave_32x32";
     case TILE_F32_DMA_128x128: return "f32_dma_128x128x32";
+    case TILE_GEMV:            return "gemv";
     default:                return "?";
   }
 }
@@ -500,6 +502,24 @@ int plan_contraction_impl( int64_t            num_loops,
     if( l_v >= 1 && plan.dma_variant == 3 ) plan.dma_variant = l_v;
   }
 
+  // ------------------------------------------------------- matrix-vector
+  // One free side of extent 1 pads every MFMA tile to one row in 64: one
+  // thread per output element instead, when the long side's operand is
+  // unit-stride along it (coalesced loads), K is short enough for a
+  // per-thread loop and the outputs fill the chip (256 CUs x 1024 threads).
+  // ETIR_TILE=13 forces it for any M == 1 or N == 1 shape.
+  {
+    bool const l_mv_shape = ( l_f32 || l_bf16 ) && !l_cpx && ( l_kern_m == 1 || l_kern_n == 1 );
+    char const * l_env_t = std::getenv( "ETIR_TILE" );
+    bool const l_forced = l_mv_shape && l_env_t != nullptr && std::atoi( l_env_t ) == TILE_GEMV;
+    bool const l_long_vec = ( l_kern_m == 1 && l_kern_n > 1 ) ? ( plan.mode_b == LOAD_VEC_MN )
+                          : ( l_kern_n == 1 && l_kern_m > 1 ) ? ( plan.mode_a == LOAD_VEC_MN ) : false;
+    bool const l_mv_ok = l_mv_shape && l_long_vec && l_size_k <= 256
+                      && l_size_c * l_kern_m * l_kern_n >= 1024 * l_cus
+                      && l_env_t == nullptr && std::getenv( "ETIR_NO_GEMV" ) == nullptr;
+    if( l_mv_ok || l_forced ) plan.tile = TILE_GEMV;
+  }
+
   int64_t l_bm, l_bn;
   tile_shape( plan.tile, l_bm, l_bn );
 
@@ -513,7 +533,7 @@ int plan_contraction_impl( int64_t            num_loops,
   // 90 on split K)
   {
     int64_t const l_t32 = n_tiles( TILE_F32_KWAVE_32x32 );
-    bool const l_kw_ok = l_f32 && plan.mode_a == LOAD_VEC_K && plan.mode_b == LOAD_VEC_K && l_k_affine
+    bool const l_kw_ok = l_f32 && plan.tile != TILE_GEMV && plan.mode_a == LOAD_VEC_K && plan.mode_b == LOAD_VEC_K && l_k_affine
                       && l_sk_a == 1 && l_sk_b == 1 && l_size_k % 16 == 0 && l_size_k >= 256
                       && l_size_k <= 4096 && n_tiles( plan.tile ) < l_cus && l_t32 >= l_cus / 2
                       && l_t32 <= 2 * l_cus
@@ -540,7 +560,8 @@ int plan_contraction_impl( int64_t            num_loops,
   // node with M = 64, N = 1024, K = 32768).  Then the outermost K loops (one
   // of them factored if needed) become C loops of a partial contraction that
   // writes one workspace slice per split, and split_reduce sums the slices.
-  if( allow_split && !l_f64 && !l_cpx && l_size_k >= 512 && plan.tile != TILE_F32_KWAVE_32x32 ) {
+  if( allow_split && !l_f64 && !l_cpx && l_size_k >= 512 && plan.tile != TILE_F32_KWAVE_32x32
+      && plan.tile != TILE_GEMV ) {
     int64_t const l_tiles = n_tiles( plan.tile );
     if( l_tiles > 0 && l_tiles < l_cus ) {
       // at least 128 k per split; aim for two workgroups per CU
@@ -984,6 +1005,9 @@ int launch_contraction( ContractionPlan const & plan,
       break;
     case TILE_F32_DMA_128x128:
       l_err = launch_contract_f32_dma( l_ma, l_mb, a, l_g, stream );
+      break;
+    case TILE_GEMV:
+      l_err = launch_contract_gemv( plan.dtype_in == ETIR_BF16, a, stream );
       break;
     default: return fail( ETIR_COMPILATION_FAILED, "contraction: unknown tile configuration" );
   }

@@ -204,7 +204,8 @@ enum TileCfg : int32_t {
   TILE_CPX_F32_64x64    = 9,  // complex (CPX_MADD) kernels, contract_cpx.hip
   TILE_CPX_F64_64x64    = 10,
   TILE_F32_KWAVE_32x32  = 11, // K split over the waves of one workgroup (contract_kwave.hip)
-  TILE_F32_DMA_128x128  = 12  // fp32 direct-to-LDS kernel (contract_f32_dma.hip)
+  TILE_F32_DMA_128x128  = 12, // fp32 direct-to-LDS kernel (contract_f32_dma.hip)
+  TILE_GEMV             = 13  // M == 1 or N == 1: one thread per output element (contract_gemv.hip)
 };
 
 struct ContractArgs {
