@@ -520,6 +520,17 @@ int plan_contraction_impl( int64_t            num_loops,
     if( l_mv_ok || l_forced ) plan.tile = TILE_GEMV;
   }
 
+  // ------------------------------------------- long K on few large tiles
+  // The 64 x 64 tile fills the chip where fewer than 256 of the 128 x 128
+  // tiles exist, but runs at about half the fp32 direct-to-LDS kernel's rate;
+  // with K >= 2048 the larger tile split over K (below) is faster (1024 x 1024
+  // x 8192: 148 us against 198; 1215 x 924 x 4620: 139 against 188).  Undone
+  // after the split block if K does not split.
+  int32_t const l_tile_unsplit = plan.tile;
+  bool const l_big_k_split = allow_split && l_f32_dma_ok && plan.tile == TILE_F32_64x64 && l_size_k >= 2048
+                          && n_tiles( TILE_F32_128x128 ) < l_cus && std::getenv( "ETIR_TILE" ) == nullptr;
+  if( l_big_k_split ) plan.tile = TILE_F32_DMA_128x128;
+
   int64_t l_bm, l_bn;
   tile_shape( plan.tile, l_bm, l_bn );
 
@@ -576,11 +587,20 @@ int plan_contraction_impl( int64_t            num_loops,
         int64_t const l_need = ( l_target + l_sf - 1 ) / l_sf;
         // factor of this loop: the smallest divisor that reaches the target,
         // else the largest one that stays within l_smax
+        // (first pass: where this is the innermost K loop and unit-stride in
+        // an operand, only factors that leave its inner part a multiple of 4,
+        // so that K rows stay 16-byte loadable: 4620 = 4 x 1155 on the fp32
+        // direct-to-LDS kernel measured 457 us, 5 x 924 the vector loads)
         int64_t l_f = 0;
-        for( int64_t l_d = 2; l_d <= l_lp.size; l_d++ ) {
-          if( l_lp.size % l_d != 0 || l_sf * l_d > l_smax ) continue;
-          l_f = l_d;
-          if( l_d >= l_need ) break;
+        bool const l_keep4 = l_i + 1 == l_kk.size() && l_lp.size % 4 == 0
+                          && ( l_lp.s[T_L] == 1 || l_lp.s[T_R] == 1 );
+        for( int l_pass = l_keep4 ? 0 : 1; l_pass < 2 && l_f == 0; l_pass++ ) {
+          for( int64_t l_d = 2; l_d <= l_lp.size; l_d++ ) {
+            if( l_lp.size % l_d != 0 || l_sf * l_d > l_smax ) continue;
+            if( l_pass == 0 && ( l_lp.size / l_d ) % 4 != 0 ) continue;
+            l_f = l_d;
+            if( l_d >= l_need ) break;
+          }
         }
         if( l_f == 0 ) break;
         if( l_f == l_lp.size ) {
@@ -671,6 +691,12 @@ int plan_contraction_impl( int64_t            num_loops,
         return ETIR_SUCCESS;
       }
     }
+  }
+  if( l_big_k_split && plan.tile == TILE_F32_DMA_128x128 ) {
+    // K did not split (and K over waves did not take the node): back to the
+    // tile that fills the chip by itself
+    plan.tile = l_tile_unsplit;
+    tile_shape( plan.tile, l_bm, l_bn );
   }
 
   plan.C = l_size_c;

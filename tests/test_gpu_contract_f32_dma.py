@@ -146,3 +146,18 @@ def test_unaligned_operands_fall_back(torch_cuda, oracle, monkeypatch, expr, siz
     if force:
         monkeypatch.setenv("ETIR_TILE", force)
     _run_offset(torch_cuda, oracle, expr, sizes, dtype, tile, seed=sizes.get("k", 1))
+
+
+@pytest.mark.parametrize("k,split", [(2048, "S=16 K'=128"), (2060, "S=5 K'=412"), (2053, None)])
+def test_long_k_split_on_large_tiles(torch_cuda, oracle, monkeypatch, k, split):
+    """K >= 2048 on fewer than 256 tiles of 128 x 128: the planner takes the
+    fp32 direct-to-LDS tile split over K, with factors that keep the K rows
+    16-byte loadable (2060 = 5 x 412, not 4 x 515; the partial contraction
+    picks its own tile); a prime K does not split and the node stays on the
+    64 x 64 tile."""
+    monkeypatch.delenv("ETIR_TILE", raising=False)
+    _, desc = run_case(torch_cuda, oracle, "mk,nk->mn", dict(m=264, k=k, n=200), seed=k)
+    if split is None:
+        assert "split-K" not in desc and "f32_64x64x32" in desc, desc
+    else:
+        assert split in desc, desc
