@@ -69,6 +69,39 @@ __device__ inline void dma16( i32x4 rsrc, uint32_t voff, uint32_t lds_addr ) {
 }
 #pragma clang diagnostic pop
 
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// The same load with the lane's row offset in voff and a wave-uniform byte
+// offset (the k step) in soff: global address base + voff + soff, LDS
+// address M0 + 16 i.  M0 must have been written beforehand (set_m0*);
+// INC > 0 advances M0 by INC after the load, for the next chunk (the
+// instructions between two issues cover the wait state an LDS-DMA
+// instruction needs after an SALU write of M0).  No instruction offset: it
+// would move the global and the LDS address alike.
+template< int INC >
+__device__ inline void dma16_so( i32x4 rsrc, uint32_t voff, uint32_t soff ) {
+  if constexpr( INC > 0 ) {
+    asm volatile( "buffer_load_dwordx4 %0, %1, %2 offen lds\n\ts_add_u32 m0, %3, m0"
+                  :: "v"( voff ), "s"( rsrc ), "s"( soff ), "n"( INC ) : "m0", "scc" );
+  }
+  else {
+    asm volatile( "buffer_load_dwordx4 %0, %1, %2 offen lds" :: "v"( voff ), "s"( rsrc ), "s"( soff ) );
+  }
+}
+
+// M0 = v (with the wait state an LDS-DMA instruction needs after an SALU
+// write of M0)
+__device__ inline void set_m0( uint32_t v ) {
+  asm volatile( "s_mov_b32 m0, %0\n\ts_nop 0" :: "s"( v ) : "m0" );
+}
+
+// M0 = base + IMM
+template< uint32_t IMM >
+__device__ inline void set_m0_add( uint32_t base ) {
+  asm volatile( "s_add_u32 m0, %0, %1\n\ts_nop 0" :: "s"( base ), "n"( IMM ) : "m0", "scc" );
+}
+#pragma clang diagnostic pop
+
 // LDS byte address of a generic pointer into a __shared__ array
 __device__ inline uint32_t lds_addr( void const * p ) {
   return uint32_t( reinterpret_cast< uintptr_t >( (__attribute__( ( address_space( 3 ) ) ) char const *) p ) );
@@ -164,6 +197,15 @@ struct DmaLoader< R, BK, W, LOAD_VEC_MN > {
     uint32_t l_off = m_off[J] + kstep_bytes;
     if( k0 + m_kk[J] >= K ) l_off = kDmaOob;
     dma16( rsrc, l_off, lds_stage + ( wave * NJ + J ) * 1024 );
+  }
+  // chunk J with M0 at this wave's chunk J of the stage (set_m0 before
+  // chunk 0, advanced by each issue) and the k step's bytes in soffset
+  template< int J, bool CHK >
+  __device__ __attribute__( ( always_inline ) ) inline void issue_so( i32x4 rsrc, uint32_t kstep_bytes, int32_t k0,
+                                                                      int32_t K ) {
+    uint32_t l_off = m_off[J];
+    if( CHK && k0 + m_kk[J] >= K ) l_off = kDmaOob;
+    dma16_so< ( J + 1 < NJ ) ? 1024 : 0 >( rsrc, l_off, kstep_bytes );
   }
   __device__ inline void issue( i32x4 rsrc, uint32_t lds_stage, int wave, int32_t k0,
                                 int32_t K, uint32_t kstep_bytes ) {
@@ -262,6 +304,27 @@ struct DmaFrag< R, BK, NB, LOAD_VEC_MN > {
   __device__ static __attribute__( ( always_inline ) ) inline bf16x8 value( Part const & f ) {
     return __builtin_bit_cast( bf16x8, __builtin_shufflevector( f.h[0], f.h[1], 0, 1, 2, 3, 4, 5, 6, 7 ) );
   }
+
+  // the same addresses + 64 KiB, for reads whose immediate offset would not
+  // fit the 16-bit field (made opaque so the compiler keeps them in registers
+  // instead of adding 64 KiB before every such read)
+  uint32_t m_addr_hi[NB];
+  __device__ inline void init_hi() {
+#pragma unroll
+    for( int l_i = 0; l_i < NB; l_i++ ) {
+      asm volatile( "v_add_u32 %0, 0x10000, %1" : "=v"( m_addr_hi[l_i] ) : "v"( m_addr[l_i] ) );
+    }
+  }
+  // unit U of the fragment of block i at compile-time byte offset OFF from
+  // the start of LDS (stage, operand and substep offsets folded into OFF)
+  template< int U, int OFF >
+  __device__ __attribute__( ( always_inline ) ) inline void read_unit_c( char const * lds, int i, Part & f ) const {
+    constexpr int l_off = OFF + U * 4 * R * 2;
+    static_assert( l_off < 2 * 65536, "LDS offset" );
+    uint32_t const l_a = ( l_off >= 65536 ) ? m_addr_hi[i] + uint32_t( l_off - 65536 ) : m_addr[i] + uint32_t( l_off );
+    f.h[U] = __builtin_amdgcn_ds_read_tr16_b64_v4i16( (lds_v4i16 *) ( lds + l_a ) );
+  }
+
 };
 
 template< int R, int BK, int NB >
@@ -362,6 +425,16 @@ struct ReadOrder {
 //              the barrier that ended step t - 1)
 // The last three steps issue no DMA (vmcnt(0) before the barrier) and the
 // final step has no barrier.
+//
+// Issue cost: with one wave per SIMD every instruction between two MFMAs
+// delays the next one, so the steady loop carries as few as it can (about
+// 100 per step of 32 MFMAs, from about 150): the steps whose loads are whole
+// k steps skip the per-lane K test; a DMA issue takes the k step's bytes in
+// soffset (no per-lane add) and M0 is written once per operand and step, then
+// advanced by 1 KiB after each issue; and the loop runs in groups of STAGES
+// steps whose stage index is a compile-time constant, so every fragment
+// read's LDS address is a base register plus an immediate (config 3:
+// 259.5 -> 244.5 us per launch, the K test alone 10 us of it).
 // ---------------------------------------------------------------------------
 // prologue of the main loop: the loads of k-steps 0 .. STAGES-2 (steps >= nk
 // load zeros) into stage buffers 0 .. STAGES-2
@@ -436,14 +509,31 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_body(
     else l_frb.template read_unit< kRo.unit[l_r] >( l_lds + SA, kRo.idx[l_r], 0, l_pb[0][kRo.idx[l_r]] );
   } );
 
-  auto iteration = [&]( int32_t l_t, auto dma_c, auto next_c ) __attribute__( ( always_inline ) ) {
+  // M0 of this wave's first DMA chunk in stage 0, per operand
+  uint32_t const l_m0a = l_lds0 + uint32_t( l_wave * LdA::NJ * 1024 );
+  uint32_t const l_m0b = l_lds0 + uint32_t( SA + l_wave * LdB::NJ * 1024 );
+
+  // ST >= 0: t % STAGES == ST known at compile time (stage offsets become
+  // instruction immediates); ST < 0: computed
+  // FG: 1 = the first STAGES steps (compile-time ST), 0 = a later group of
+  // them, -1 = unknown (checked at run time)
+  auto iteration = [&]( int32_t l_t, auto dma_c, auto next_c, auto chk_c, auto st_c, auto fg_c ) __attribute__( ( always_inline ) ) {
     constexpr bool DMA  = decltype( dma_c )::value;
     constexpr bool NEXT = decltype( next_c )::value;
-    char const * l_sa = l_lds + ( l_t % STAGES ) * ( SA + SB );
+    constexpr bool CHK  = decltype( chk_c )::value;
+    constexpr int  ST   = decltype( st_c )::value;
+    constexpr int  FG   = decltype( fg_c )::value;
+    constexpr int  OFF_CUR = ( ST >= 0 ? ST : 0 ) * ( SA + SB );
+    constexpr int  OFF_NXT = ( ST >= 0 ? ( ST + 1 ) % STAGES : 0 ) * ( SA + SB );
+    int32_t const l_cs = ( ST >= 0 ) ? ST : l_t % STAGES;
+    int32_t const l_ns = ( ST >= 0 ) ? ( ST + 1 ) % STAGES : ( l_t + 1 ) % STAGES;
+    int32_t const l_ds = ( ST >= 0 ) ? ( ST + STAGES - 1 ) % STAGES : ( l_t + STAGES - 1 ) % STAGES;
+    char const * l_sa = l_lds + l_cs * ( SA + SB );
     char const * l_sb = l_sa + SA;
-    char const * l_na = l_lds + ( ( l_t + 1 ) % STAGES ) * ( SA + SB );
+    char const * l_na = l_lds + l_ns * ( SA + SB );
     int32_t const l_tl = l_t + STAGES - 1;
-    uint32_t const l_st = l_lds0 + uint32_t( l_tl % STAGES ) * ( SA + SB );
+    uint32_t const l_soa = uint32_t( l_tl ) * l_kb_a;
+    uint32_t const l_sob = uint32_t( l_tl ) * l_kb_b;
 
     // both substeps as one sequence of 2 * NMF MFMAs; DMA issues spread
     // evenly over it (one per 2 * NMF / NJW MFMAs) so the address unit is
@@ -462,7 +552,13 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_body(
         static_for< U >( [&]( auto rc ) __attribute__( ( always_inline ) ) {
           constexpr int l_r = decltype( rc )::value;
           if constexpr( ( l_r * NMF ) / U == l_p ) {
-            if constexpr( kRo.isb[l_r] == 0 )
+            if constexpr( ST >= 0 ) {
+              if constexpr( kRo.isb[l_r] == 0 )
+                l_fra.template read_unit_c< kRo.unit[l_r], OFF_CUR + 16 * BM * 2 >( l_lds, kRo.idx[l_r], l_pa[1][kRo.idx[l_r]] );
+              else
+                l_frb.template read_unit_c< kRo.unit[l_r], OFF_CUR + SA + 16 * BN * 2 >( l_lds, kRo.idx[l_r], l_pb[1][kRo.idx[l_r]] );
+            }
+            else if constexpr( kRo.isb[l_r] == 0 )
               l_fra.template read_unit< kRo.unit[l_r] >( l_sa, kRo.idx[l_r], 1, l_pa[1][kRo.idx[l_r]] );
             else
               l_frb.template read_unit< kRo.unit[l_r] >( l_sb, kRo.idx[l_r], 1, l_pb[1][kRo.idx[l_r]] );
@@ -475,9 +571,23 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_body(
           // are in flight: all of steps t + 2 .. t + STAGES - 2 (issued in
           // earlier steps) and the DMA_BEFORE loads of step t + STAGES - 1
           // issued so far in this step
-          if( FIRST_VMCNT == 1 && l_pend && l_t + 1 <= STAGES - 2 ) wait_vmcnt< 63 >();
-          else if constexpr( DMA ) wait_vmcnt< ( STAGES - 3 ) * NJW + DMA_BEFORE >();
-          else                     wait_vmcnt< 0 >();
+          // (with FIRST_VMCNT 1 and l_pend, the prologue's steps have the
+          // previous tile's stores behind them: vmcnt(63), see above; FG
+          // says whether this is such a step at compile time)
+          auto wait_normal = [&]() __attribute__( ( always_inline ) ) {
+            if constexpr( DMA ) wait_vmcnt< ( STAGES - 3 ) * NJW + DMA_BEFORE >();
+            else                wait_vmcnt< 0 >();
+          };
+          if constexpr( FG == 0 || FIRST_VMCNT != 1 ) wait_normal();
+          else if constexpr( FG == 1 ) {
+            if constexpr( ST + 1 <= STAGES - 2 ) {
+              if( l_pend ) wait_vmcnt< 63 >();
+              else wait_normal();
+            }
+            else wait_normal();
+          }
+          else if( l_pend && l_t + 1 <= STAGES - 2 ) wait_vmcnt< 63 >();
+          else wait_normal();
           wait_lgkmcnt0();
           barrier_lds();
         }
@@ -485,7 +595,13 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_body(
         static_for< U >( [&]( auto rc ) __attribute__( ( always_inline ) ) {
           constexpr int l_r = decltype( rc )::value;
           if constexpr( l_p >= PB && PB + ( l_r * ( NMF - PB ) ) / U == l_p ) {
-            if constexpr( kRo.isb[l_r] == 0 )
+            if constexpr( ST >= 0 ) {
+              if constexpr( kRo.isb[l_r] == 0 )
+                l_fra.template read_unit_c< kRo.unit[l_r], OFF_NXT >( l_lds, kRo.idx[l_r], l_pa[0][kRo.idx[l_r]] );
+              else
+                l_frb.template read_unit_c< kRo.unit[l_r], OFF_NXT + SA >( l_lds, kRo.idx[l_r], l_pb[0][kRo.idx[l_r]] );
+            }
+            else if constexpr( kRo.isb[l_r] == 0 )
               l_fra.template read_unit< kRo.unit[l_r] >( l_na, kRo.idx[l_r], 0, l_pa[0][kRo.idx[l_r]] );
             else
               l_frb.template read_unit< kRo.unit[l_r] >( l_na + SA, kRo.idx[l_r], 0, l_pb[0][kRo.idx[l_r]] );
@@ -496,11 +612,15 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_body(
         static_for< NJW >( [&]( auto dc ) __attribute__( ( always_inline ) ) {
           constexpr int l_d = decltype( dc )::value;
           if constexpr( dma_slot< 2 * NMF, NJW >( l_d ) == l_q ) {
+            if constexpr( l_d == 0 || l_d == NJA ) {
+              uint32_t const l_base = ( l_d == 0 ) ? l_m0a : l_m0b;
+              if constexpr( ST >= 0 ) set_m0_add< uint32_t( ( ( ST + STAGES - 1 ) % STAGES ) * ( SA + SB ) ) >( l_base );
+              else set_m0( l_base + uint32_t( l_ds ) * ( SA + SB ) );
+            }
             if constexpr( l_d < NJA )
-              l_lda.template issue_one< l_d >( l_ra, l_st, l_wave, l_tl * BK, l_K, uint32_t( l_tl ) * l_kb_a );
+              l_lda.template issue_so< l_d, CHK >( l_ra, l_soa, l_tl * BK, l_K );
             else
-              l_ldb.template issue_one< l_d - NJA >( l_rb, l_st + SA, l_wave, l_tl * BK, l_K,
-                                                     uint32_t( l_tl ) * l_kb_b );
+              l_ldb.template issue_so< l_d - NJA, CHK >( l_rb, l_sob, l_tl * BK, l_K );
           }
         } );
       }
@@ -510,10 +630,29 @@ __device__ __attribute__( ( always_inline ) ) inline void mainloop_body(
 
   std::integral_constant< bool, true >  const l_yes{};
   std::integral_constant< bool, false > const l_no{};
+  std::integral_constant< int, -1 > const l_rt{};
+  std::integral_constant< int, 1 > const l_fg1{};
+  std::integral_constant< int, 0 > const l_fg0{};
   int32_t l_t = 0;
-  for( ; l_t < l_nk - ( STAGES - 1 ); l_t++ ) iteration( l_t, l_yes, l_yes );
-  for( ; l_t < l_nk - 1; l_t++ ) iteration( l_t, l_no, l_yes );
-  iteration( l_nk - 1, l_no, l_no );
+  // steps whose loads (step t + STAGES - 1 < nk - 1) are whole k steps, in
+  // groups of STAGES with compile-time stage indices (the first group, where
+  // the previous tile's stores may still be pending, separately)
+  if( l_nk - STAGES >= STAGES ) {
+    static_for< STAGES >( [&]( auto sc ) __attribute__( ( always_inline ) ) {
+      iteration( decltype( sc )::value, l_yes, l_yes, l_no, sc, l_fg1 );
+    } );
+    for( l_t = STAGES; l_t + STAGES <= l_nk - STAGES; l_t += STAGES ) {
+      static_for< STAGES >( [&]( auto sc ) __attribute__( ( always_inline ) ) {
+        iteration( l_t + decltype( sc )::value, l_yes, l_yes, l_no, sc, l_fg0 );
+      } );
+    }
+  }
+  // (an early return or a conditional last step here made the compiler
+  // spill the accumulators)
+  for( ; l_t < l_nk - STAGES; l_t++ ) iteration( l_t, l_yes, l_yes, l_no, l_rt, l_rt );
+  for( ; l_t < l_nk - ( STAGES - 1 ); l_t++ ) iteration( l_t, l_yes, l_yes, l_yes, l_rt, l_rt );
+  for( ; l_t < l_nk - 1; l_t++ ) iteration( l_t, l_no, l_yes, l_yes, l_rt, l_rt );
+  iteration( l_nk - 1, l_no, l_no, l_yes, l_rt, l_rt );
 }
 
 template< int BM, int BN, int BK, int WM, int WN, int MA, int MB, int STAGES, typename LdA, typename LdB,
@@ -601,6 +740,8 @@ void contract_dma_kernel( ContractArgs a ) {
   DmaFrag< BN, BK, TN, MB > l_frb;
   l_fra.init( l_wm * TM * 32, l_lane );
   l_frb.init( l_wn * TN * 32, l_lane );
+  if constexpr( MA == LOAD_VEC_MN ) l_fra.init_hi();
+  if constexpr( MB == LOAD_VEC_MN ) l_frb.init_hi();
 
   f32x16 l_acc[TM][TN];
 #pragma unroll
@@ -784,6 +925,8 @@ void contract_dma_persistent_kernel( ContractArgs a ) {
   DmaFrag< BN, BK, TN, MB > l_frb;
   l_fra.init( l_wm * TM * 32, l_lane );
   l_frb.init( l_wn * TN * 32, l_lane );
+  if constexpr( MA == LOAD_VEC_MN ) l_fra.init_hi();
+  if constexpr( MB == LOAD_VEC_MN ) l_frb.init_hi();
 
   int32_t const l_K  = a.K;
   int32_t const l_nk = ( l_K + BK - 1 ) / BK;

@@ -473,8 +473,7 @@ int plan_contraction_impl( int64_t            num_loops,
          l_f32 && !l_cpx
       && ( plan.mode_a == LOAD_VEC_MN || plan.mode_a == LOAD_VEC_K )
       && ( plan.mode_b == LOAD_VEC_MN || plan.mode_b == LOAD_VEC_K )
-      && l_f32_dma_k
-      && std::getenv( "ETIR_NO_F32_DMA" ) == nullptr;
+      && l_f32_dma_k;
   if( l_f32_dma_ok && plan.tile == TILE_F32_128x128 ) plan.tile = TILE_F32_DMA_128x128;
   if( char const * l_env = ( l_f64 || l_cpx ) ? nullptr : std::getenv( "ETIR_TILE" ) ) {
     // diagnostic override of the tile heuristic (must match the dtype)
@@ -495,11 +494,14 @@ int plan_contraction_impl( int64_t            num_loops,
   // runs -- all tiles full, plain fp32 stores -- decided at launch)
   plan.dma_variant = ( plan.mode_a == LOAD_VEC_MN && plan.mode_b == LOAD_VEC_MN ) ? 3 : 0;
   if( char const * l_env = std::getenv( "ETIR_DMA_VARIANT" ) ) {
-    // diagnostic override: 0 forces the generic BK 64 / 2-stage loop,
-    // 3 the persistent scheduled loop (VEC_MN x VEC_MN only)
+    // diagnostic override, only values whose kernel runs on this plan's
+    // 256 x 256 tile grid: 0 forces the generic BK 64 / 2-stage loop, 1 the
+    // one-tile scheduled loop and 3 its persistent form (both VEC_MN x
+    // VEC_MN only); anything else is ignored (the 256 x 128 kernel has a
+    // tile grid of its own and is chosen by ETIR_TILE)
     int32_t const l_v = std::atoi( l_env );
     if( l_v == 0 ) plan.dma_variant = 0;
-    if( l_v >= 1 && plan.dma_variant == 3 ) plan.dma_variant = l_v;
+    if( ( l_v == 1 || l_v == 3 ) && plan.dma_variant == 3 ) plan.dma_variant = l_v;
   }
 
   // ------------------------------------------------------- matrix-vector
@@ -553,11 +555,7 @@ int plan_contraction_impl( int64_t            num_loops,
       // 8 waves up to K = 512, 16 above (config 1, K = 512: 7.58-7.65 us with
       // 8 waves against 7.85-7.87 with 16 and 8.8 with 4; K = 256 and 1024:
       // 8 and 16 equal within 1 %)
-      int32_t l_w = ( l_size_k <= 512 ) ? 8 : 16;
-      if( char const * l_env = std::getenv( "ETIR_KWAVE_WAVES" ) ) {
-        int32_t const l_v = std::atoi( l_env );
-        if( l_v == 4 || l_v == 8 || l_v == 16 ) l_w = l_v;
-      }
+      int32_t const l_w = ( l_size_k <= 512 ) ? 8 : 16;
       plan.tile = TILE_F32_KWAVE_32x32;
       plan.tile_fallback = TILE_F32_64x64;
       plan.kwave_waves = l_w;

@@ -93,6 +93,21 @@ def test_dma_persistent(torch_cuda, oracle, monkeypatch, expr, sizes):
     assert (got_p == got_1).all(), "persistent and one-tile-per-workgroup kernels differ"
 
 
+@pytest.mark.parametrize("variant,persistent", [("0", False), ("1", False), ("2", True), ("3", True),
+                                                ("9", True)])
+def test_dma_variant_override(torch_cuda, oracle, monkeypatch, variant, persistent):
+    """ETIR_DMA_VARIANT takes only the values a 256 x 256 plan can run (0: BK 64
+    loop, 1: one-tile scheduled loop, 3: persistent); others (2, the 256 x 128
+    kernel with a tile grid of its own, and unknown values) leave the plan's
+    choice unchanged.  Every value gives the oracle's result."""
+    monkeypatch.setenv("ETIR_TILE", "7")
+    monkeypatch.setenv("ETIR_DMA_VARIANT", variant)
+    _, desc = run_case(torch_cuda, oracle, "zkm,zkn->zmn", dict(z=2, k=64, m=512, n=1024), dtype=eir.BF16,
+                       seed=31)
+    assert "bf16_dma_256x256" in desc, desc
+    assert ("persistent" in desc) == persistent, desc
+
+
 @pytest.mark.parametrize("phases,stagger", [("1", "0"), ("8", "2")])
 def test_dma_persistent_stagger(torch_cuda, oracle, monkeypatch, phases, stagger):
     """Start stagger settings other than the default do not change results."""
