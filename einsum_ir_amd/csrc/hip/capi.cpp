@@ -59,13 +59,6 @@ int etir_hip_contraction_create( int64_t         num_loops,
     delete l_plan;
     return l_err;
   }
-  if( char const * l_v = std::getenv( "ETIR_VERBOSE" ) ) {
-    // diagnostic: one line per compiled contraction plan
-    if( l_v[0] != '\0' && l_v[0] != '0' ) {
-      std::fprintf( stderr, "etir plan %p: %s (%.3f GFLOP)\n", (void *) l_plan, l_plan->cont.desc.c_str(),
-                    double( l_plan->cont.flops ) * 1e-9 );
-    }
-  }
   *plan = l_plan;
   return ETIR_SUCCESS;
 }

@@ -77,14 +77,11 @@ constexpr int kTile = 64;
 constexpr int kThreads = 256;
 
 // REG4 takes permutations whose shorter unit-stride dim is at most this long
-// (ETIR_PERM_REG4_MAX_SHORT overrides, for measurements), and those whose two
+// (kReg4MaxShort elements of 4 bytes), and those whose two
 // unit-stride dims are at most 32 long and whole 128-byte lines each (fp32
 // 32 x 32: 74 % of HBM peak against 58 % tiled; 24 x 32, whose 96-byte input
 // runs split lines: 47 % against 53 % tiled)
-inline int64_t reg4_max_short() {
-  char const * l_env = std::getenv( "ETIR_PERM_REG4_MAX_SHORT" );
-  return l_env ? std::atoi( l_env ) : 16;
-}
+constexpr int64_t kReg4MaxShort = 16;
 constexpr int kPermTileMax = 4096;   // elements of a TILED tile
 
 // 16-byte store that does not keep the line in the caches (the output is
@@ -688,10 +685,17 @@ int launch_typed( PermutePlan const & p,
     if( l_blocks > 0x7fffffffLL ) {
       return fail( ETIR_UNDEFINED_ERROR, "permute: grid too large" );
     }
+    // the launch's own errors (no kernel for the workgroup size) return at
+    // once; launch failures fall through to the shared check below
+    int l_rc = ETIR_SUCCESS;
     if constexpr( sizeof( T ) == 2 ) {
-      if( p.reg4_vb == 8 ) return launch_reg4< T, 8 >( p, a, l_blocks, stream );
+      if( p.reg4_vb == 8 ) l_rc = launch_reg4< T, 8 >( p, a, l_blocks, stream );
+      else                 l_rc = launch_reg4< T, 4 >( p, a, l_blocks, stream );
     }
-    return launch_reg4< T, 4 >( p, a, l_blocks, stream );
+    else {
+      l_rc = launch_reg4< T, 4 >( p, a, l_blocks, stream );
+    }
+    if( l_rc != ETIR_SUCCESS ) return l_rc;
   }
   else if( p.mode == PermMode::ROWS ) {
     int64_t const l_blocks = a.rows_nbx * a.rows_nby * a.num_batch_total;
@@ -824,15 +828,6 @@ bool plan_rows( PermutePlan & plan, int dim_u ) {
           l_ey = l_ty;
         }
       }
-    }
-  }
-  if( char const * l_env = std::getenv( "ETIR_PERM_ROWS_TILE" ) ) {
-    // diagnostic: tile extents "EXxEY", taken when within the dims and 64 KB
-    int64_t l_tx = 0, l_ty = 0;
-    if(    std::sscanf( l_env, "%" SCNd64 "x%" SCNd64, &l_tx, &l_ty ) == 2 && l_tx >= 1 && l_ty >= 1
-        && l_tx <= l_nx && l_ty <= l_ny && l_tx * l_ty * l_rowb <= 65536 ) {
-      l_ex = l_tx;
-      l_ey = l_ty;
     }
   }
   if( l_ex == 0 ) return false;
@@ -1270,7 +1265,7 @@ int plan_permute( int64_t         num_dims,
   int64_t const l_vb = (    plan.elem_bytes == 2 && l_dim_i >= 0 && l_dim_o >= 0
                          && plan.size[l_dim_i] % 8 == 0 && plan.size[l_dim_o] % 8 == 0 ) ? 8 : 4;
   int64_t const l_scale = plan.elem_bytes == 2 ? 2 : 1;
-  int64_t const l_short = reg4_max_short() * l_scale;
+  int64_t const l_short = kReg4MaxShort * l_scale;
   int64_t const l_both = 32 * l_scale;
 
   // a long input unit-stride dim with a short output one: split it into an
@@ -1278,8 +1273,7 @@ int plan_permute( int64_t         num_dims,
   // outer part (the REG4 tiles below take the inner part whole)
   if(    l_dim_i >= 0 && l_dim_o >= 0 && l_dim_i != l_dim_o && l_n < kPermMaxDims
       && plan.size[l_dim_o] % l_vb == 0 && plan.size[l_dim_o] <= l_short
-      && ( plan.size[l_dim_i] / l_vb ) * ( plan.size[l_dim_o] / l_vb ) > 64
-      && std::getenv( "ETIR_NO_PERM_REG4" ) == nullptr ) {
+      && ( plan.size[l_dim_i] / l_vb ) * ( plan.size[l_dim_o] / l_vb ) > 64 ) {
     int64_t const l_lo = l_vb * ( 64 / ( plan.size[l_dim_o] / l_vb ) );
     if( plan.size[l_dim_i] % l_lo == 0 ) {
       for( int l_di = l_n; l_di > l_dim_i; l_di-- ) {
@@ -1305,8 +1299,7 @@ int plan_permute( int64_t         num_dims,
            || (    std::max( plan.size[l_dim_i], plan.size[l_dim_o] ) <= l_both
                 && ( plan.size[l_dim_i] * plan.elem_bytes ) % 128 == 0
                 && ( plan.size[l_dim_o] * plan.elem_bytes ) % 128 == 0 ) )
-      && ( plan.size[l_dim_i] / l_vb ) * ( plan.size[l_dim_o] / l_vb ) <= kThreads
-      && std::getenv( "ETIR_NO_PERM_REG4" ) == nullptr ) {
+      && ( plan.size[l_dim_i] / l_vb ) * ( plan.size[l_dim_o] / l_vb ) <= kThreads ) {
     // a short unit-stride dim: register-transposed blocks.  The dim that
     // continues the input's run (input stride size_i), else the output's,
     // else the largest other dim, is walked by consecutive lanes after i
@@ -1478,10 +1471,6 @@ int plan_permute( int64_t         num_dims,
     double l_best = 1.25 * util( kTile, kTile );
     if( util( 128, 32 ) >= l_best ) { plan.tr_shape = 1; l_best = util( 128, 32 ); }
     if( util( 32, 128 ) > l_best )  plan.tr_shape = 2;
-    if( char const * l_env = std::getenv( "ETIR_PERM_TR_SHAPE" ) ) {
-      int const l_v = std::atoi( l_env );
-      if( l_v >= 0 && l_v <= 2 ) plan.tr_shape = l_v;
-    }
     int64_t const l_ti = plan.tr_shape == 1 ? 128 : ( plan.tr_shape == 2 ? 32 : kTile );
     int64_t const l_to = 4 * 4 * kThreads / l_ti;
     a.tiles_i = ( a.size_i + l_ti - 1 ) / l_ti;
@@ -1500,7 +1489,6 @@ int plan_permute( int64_t         num_dims,
                  && a.s_in_o % 4 == 0 && a.s_out_i % 4 == 0
                  && all_div4( l_dim_i, l_dim_o ) ) ? 1 : 0;
     a.nt_store = 1;
-    if( char const * l_env = std::getenv( "ETIR_PERM_NT" ) ) a.nt_store = std::atoi( l_env ) != 0;
     return ETIR_SUCCESS;
   }
 

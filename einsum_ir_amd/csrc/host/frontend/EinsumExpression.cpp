@@ -259,13 +259,14 @@ std::string einsum_ir::frontend::EinsumExpression::to_string_exchange_format( ba
   if( !m_compiled || m_nodes.empty() ) return "Error: Expression not compiled.";
   backend::EinsumNode const & l_node = ( i_node != nullptr ) ? *i_node : m_nodes.back();
   std::string const l_ids = join_ids( l_node.m_dim_ids_int.data(), l_node.m_num_dims, ',' );
-  if( !l_node.m_children.empty() ) {
-    std::string l_s;
-    for( std::size_t l_ch = 0; l_ch < l_node.m_children.size(); l_ch++ ) {
-      l_s += ( l_ch > 0 ? ",[" : "[" ) + to_string_exchange_format( l_node.m_children[l_ch] ) + "]";
-    }
-    return l_s + "->[" + l_ids + "]";
+  if( l_node.m_children.size() == 2 ) {
+    return "[" + to_string_exchange_format( l_node.m_children[0] ) + "],["
+         + to_string_exchange_format( l_node.m_children[1] ) + "]->[" + l_ids + "]";
   }
+  // a one-child node (the complex BATCH_INNER root's conversion) is written
+  // as its own ids only, its subtree left out, as the reference writes it
+  // (src/frontend/EinsumExpression.cpp:504-563)
+  if( l_node.m_children.size() == 1 ) return l_ids;
   if(    l_node.m_dim_ids_ext != nullptr
       && !std::equal( l_node.m_dim_ids_ext, l_node.m_dim_ids_ext + l_node.m_num_dims, l_node.m_dim_ids_int.begin() ) ) {
     return "[" + join_ids( l_node.m_dim_ids_ext, l_node.m_num_dims, ',' ) + "]->[" + l_ids + "]";

@@ -116,6 +116,22 @@ def test_print_tree_round_trip():
     assert any(set(line.split()) >= {"d", "c", "b", "a"} for line in drawn[first:first + 8])
 
 
+def test_print_tree_one_child_root():
+    """A complex BATCH_INNER tree ends in a one-child node (the conversion of
+    the complex-outermost result); the exchange format writes such a node as
+    its own ids only, without its subtree, as the reference does
+    (src/frontend/EinsumExpression.cpp:504-563).  The real tree of the same
+    expression keeps its full nesting."""
+    args = ("ab,bc->ac", "3,4,5", "(0,1)")
+    real = _run("bench_expression", *args, "FP32", "0", "1").splitlines()
+    real_tree = real[real.index("*** benchmarking einsum_ir ***") + 1]
+    assert real_tree.startswith("[") and "],[" in real_tree and real_tree.endswith("->[0,2]"), real_tree
+    cpx = _run("bench_expression", *args, "CPX_FP32", "0", "1").splitlines()
+    cpx_tree = cpx[cpx.index("*** benchmarking einsum_ir ***") + 1]
+    assert re.fullmatch(r"\d+(,\d+)*", cpx_tree) and "->" not in cpx_tree, cpx_tree
+    assert cpx_tree.split(",")[:2] == ["0", "2"], cpx_tree
+
+
 @pytest.mark.parametrize("args", [
     ("[[3,0]->[0,3]],[[3,2,4],[1,4,2]->[1,2,3]]->[0,1,2]", "2,3,4,5,6", "FP32"),   # the reference's example
     ("[[3,0]->[0,3]],[[3,2,4],[1,4,2]->[1,2,3]]->[0,1,2]", "20,30,40,50,60", "FP64"),

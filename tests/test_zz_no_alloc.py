@@ -97,6 +97,64 @@ def test_noalloc_bf16_layout(torch_cuda):
     assert rel_frobenius(exact, got) <= TOL_BF16
 
 
+def _run_both_aux(torch, expr, sizes, aux_outer, first, last, seed):
+    """As _run_both, with an aux tensor (first touch COPY/ADD or last touch
+    ADD) whose outer sizes broadcast it; returns both outputs, the plan's
+    description and the inputs."""
+    loops = loops_for(expr, sizes, sizes_outer_aux=aux_outer)
+    a, b, n_out = _inputs(torch, expr, sizes, eir.FP32, seed)
+    _, _, out = parse_binary(expr)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 100)
+    x = torch.rand(tensor_numel(out, aux_outer), device="cuda", generator=g) * 2 - 1
+    # first touch ADD adds to what the output holds: both start from the same
+    # values (NaN otherwise, so that an unwritten element shows)
+    init = (torch.rand(n_out, device="cuda", generator=g) * 2 - 1) if first == eir.ADD \
+        else torch.full((n_out,), float("nan"), device="cuda")
+    stream = torch.cuda.current_stream()
+    plan = eir.ContractionPlan(loops["dim_types"], loops["sizes"], loops["strides_left"],
+                               loops["strides_right"], loops["strides_out"],
+                               strides_out_aux=loops["strides_out_aux"], ktype_first_touch=first,
+                               ktype_last_touch=last)
+    desc = plan.describe()
+    ref = init.clone()
+    plan.execute(a, b, ref, aux=x, stream=stream)
+    plan.close()
+    got = init.clone()
+    rc = _noalloc_fn()(len(loops["sizes"]), _lib.i32_array(loops["dim_types"]), _lib.i64_array(loops["sizes"]),
+                       _lib.i64_array(loops["strides_left"]), _lib.i64_array(loops["strides_right"]),
+                       _lib.i64_array(loops["strides_out_aux"]), _lib.i64_array(loops["strides_out"]),
+                       eir.FP32, eir.FP32, eir.FP32, eir.FP32, first, eir.MADD, last,
+                       a.data_ptr(), b.data_ptr(), x.data_ptr(), got.data_ptr(), stream.cuda_stream)
+    assert rc == 0, _last_error()
+    torch.cuda.synchronize()
+    return ref.cpu().numpy(), got.cpu().numpy(), desc, (a, b, x)
+
+
+def test_noalloc_aux_and_k_tables(torch_cuda):
+    """The device-side fills of the aux tables and of a K that is not one
+    affine index (K = (k, l) with l outermost in the right operand): a bias
+    broadcast over the rows (first touch COPY, last touch RELU), then a
+    column-broadcast aux with first touch ADD over the same scratch array.
+    Bit for bit against create + execute, and the first against float64."""
+    torch = torch_cuda
+    sizes1 = dict(m=96, k=12, l=20, n=200)
+    ref1, got1, desc1, (a1, b1, x1) = _run_both_aux(torch, "mkl,lkn->mn", sizes1, dict(m=1, n=200),
+                                                     eir.COPY, eir.RELU, seed=5)
+    assert "k_affine=0" in desc1, desc1
+    assert np.array_equal(ref1, got1), "aux/K-table call differs from the allocating path"
+    A = a1.double().cpu().numpy().reshape(96, 12, 20)
+    B = b1.double().cpu().numpy().reshape(20, 12, 200)
+    exact = np.maximum(np.einsum("mkl,lkn->mn", A, B) + x1.double().cpu().numpy().reshape(1, 200), 0.0)
+    assert rel_frobenius(exact.ravel(), got1) <= TOL_FP32
+    sizes2 = dict(m=40, k=6, l=16, n=72)
+    ref2, got2, desc2, _ = _run_both_aux(torch, "mkl,lkn->mn", sizes2, dict(m=40, n=1), eir.ADD,
+                                         eir.UNDEFINED_KTYPE, seed=6)
+    assert "k_affine=0" in desc2, desc2
+    assert not np.isnan(got2).any()
+    assert np.array_equal(ref2, got2), "second aux/K-table call differs from the allocating path"
+
+
 def test_noalloc_rejects_oversized_plan(torch_cuda):
     """Offset tables beyond the 64 MiB array: a clear error, nothing launched."""
     torch = torch_cuda
