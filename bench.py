@@ -266,28 +266,41 @@ PERMUTES_4D = [
 ]
 
 
-def bench_permutes_4d(torch, eir, stream):
-    """Config 2's permutation kind over other 4-D shapes (fp32 COPY, 16.8-31.9 M
-    elements, unit-stride dims from 8 to 512 wide): GB/s per shape."""
+# tensors larger than the 256 MB Infinity Cache (MALL) in front of HBM: every
+# launch reads and writes HBM itself (128^4 elements: 1 GiB each way in fp32,
+# 512 MiB in bf16)
+PERMUTES_BEYOND_CACHE = [("abcd->dbca", (128, 128, 128, 128))]
+
+
+def bench_permutes_4d(torch, eir, stream, dtype="fp32", shapes=None, steps=SHORT_STEPS):
+    """Config 2's permutation kind over other 4-D shapes (COPY, 16.8-31.9 M
+    elements, unit-stride dims from 8 to 512 wide): GB/s per shape, bytes =
+    read + write of every element (reference src/bench_unary.cpp:230-306).
+    The shapes of PERMUTES_4D move 67-255 MB per launch (fp32), so part of a
+    run of launches can be served by the Infinity Cache; PERMUTES_BEYOND_CACHE
+    cannot."""
+    shapes = PERMUTES_4D if shapes is None else shapes
+    tdt, edt, esz = (torch.float32, eir.FP32, 4) if dtype == "fp32" else (torch.bfloat16, eir.BF16, 2)
     rows = []
     # one input and one output buffer for all shapes: every shape runs on
     # memory the process already uses (freshly mapped pages are slower for
     # the first hundreds of launches, which the timed region would catch)
-    n_max = max(s[0] * s[1] * s[2] * s[3] for _, s in PERMUTES_4D)
-    x_all = torch.rand(n_max, device="cuda")
+    n_max = max(s[0] * s[1] * s[2] * s[3] for _, s in shapes)
+    x_all = torch.rand(n_max, device="cuda").to(tdt)
     y_all = torch.empty_like(x_all)
-    for expr, shape in PERMUTES_4D:
+    for expr, shape in shapes:
         sizes = dict(zip("abcd", shape))
         u = eir.unary_dims(expr, sizes)
         n = shape[0] * shape[1] * shape[2] * shape[3]
         x = x_all[:n]
         y = y_all[:n]
-        plan = eir.PermutePlan(u["sizes"], u["strides_in"], u["strides_out"], dtype=eir.FP32, ktype=eir.COPY)
-        _, per = time_launches(torch, stream, lambda: plan.execute(x, y, stream=stream), SHORT_STEPS, 20)
-        gbs = 8 * n / per * 1e-9
+        plan = eir.PermutePlan(u["sizes"], u["strides_in"], u["strides_out"], dtype=edt, ktype=eir.COPY)
+        _, per = time_launches(torch, stream, lambda: plan.execute(x, y, stream=stream), steps, min(20, steps))
+        gbs = 2 * esz * n / per * 1e-9
         rows.append(dict(expr=expr, sizes=list(shape), gbs=round(gbs, 1), frac_hbm_peak=round(gbs / PEAK_HBM_GBS, 4),
-                         kernel=plan.describe().split(" dims")[0]))
+                         us_per_launch=round(per * 1e6, 2), kernel=plan.describe().split(" dims")[0]))
         plan.close()
+    del x_all, y_all
     return rows
 
 
@@ -625,6 +638,17 @@ def main():
         extra["permutes_4d_fp32"] = dict(unit="GB/s", min_frac_hbm_peak=min(r["frac_hbm_peak"] for r in p4),
                                          cases=p4)
         log("permutes 4-D: " + ", ".join(f"{r['expr']}{r['sizes']} {r['gbs']:.0f}" for r in p4))
+        p4b = bench_permutes_4d(torch, eir, stream, dtype="bf16")
+        extra["permutes_4d_bf16"] = dict(unit="GB/s", min_frac_hbm_peak=min(r["frac_hbm_peak"] for r in p4b),
+                                         cases=p4b)
+        log("permutes 4-D bf16: " + ", ".join(f"{r['expr']}{r['sizes']} {r['gbs']:.0f}" for r in p4b))
+        big = [dict(r, dtype=dt) for dt in ("fp32", "bf16")
+               for r in bench_permutes_4d(torch, eir, stream, dtype=dt, shapes=PERMUTES_BEYOND_CACHE, steps=20)]
+        extra["permutes_beyond_infinity_cache"] = dict(
+            unit="GB/s", note="tensors larger than the 256 MB Infinity Cache: HBM-resident every launch",
+            cases=big)
+        log("permutes beyond the Infinity Cache: "
+            + ", ".join(f"{r['dtype']} {r['expr']}{r['sizes']} {r['gbs']:.0f}" for r in big))
     if run("c1"):
         c1 = bench_c1(torch, eir, stream, max(args.steps, SHORT_STEPS), args.warmup)
         gf = c1["flops"] / c1["per_launch"] * 1e-9

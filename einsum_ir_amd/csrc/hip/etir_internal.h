@@ -135,7 +135,8 @@ struct PermutePlan {
   void *   d_tables = nullptr;           // TILED: device offset tables (owned)
   int32_t  tile_vw = 1;                  // TILED: elements per table entry (1 or 4)
   int32_t  rows_vw = 1;                  // ROWS: elements per chunk (16, 8 or 4 bytes; 1 element when unaligned)
-  int32_t  tr_shape = 0;                 // TRANSPOSE: tile 64 x 64 (0), 128 x 32 (1) or 32 x 128 (2), i x o
+  int32_t  tr_shape = 0;                 // TRANSPOSE: tile 64 x 64 (0), 128 x 32 (1) or 32 x 128 (2), i x o;
+                                         // 2-byte elements with 16-byte reads: 128 x 64 (3), 128 x 32 (4)
   int64_t  rows_len = 0;                 // ROWS: row length (elements of the shared unit-stride dim)
 };
 

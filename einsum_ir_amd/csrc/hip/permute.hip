@@ -117,6 +117,112 @@ __device__ inline int64_t grid_digit( uint32_t & io_rest, int64_t i_size ) {
 // along o (TO / 4 threads per i row), four passes each.  The LDS pitch is
 // TI + 1 for square tiles and TI + 2 otherwise, which spreads the write
 // phase's column reads over distinct banks.
+// The transpose for 2-byte elements with 16-byte reads: a TI x TO tile
+// (TI = 128 along the input's unit-stride dim i) read as 8 elements per
+// vector, written as 4 per vector along the output's unit-stride dim o
+// (output runs may be as short as 4 elements).  With 8-byte reads the same
+// moves ran at 41-51 % of HBM peak (bf16 abcd->bdac 36,48,36,512: 41 -> 51 %;
+// 72,96,72,1024 on TO = 32: 42 -> 54 %; abcd->dbca 128^4, beyond the
+// Infinity Cache: 51 -> 59 %).  LDS rows are padded by 4 bytes so that the
+// column reads of the write phase step one bank per row.  VEC false (no
+// vector alignment, a.vec_ok 0): every access is one element (a separate
+// instantiation: the run-time choice inside one kernel cost 10 %).
+template< typename T, int TI, int TO, bool VEC >
+__global__ __launch_bounds__( kThreads )
+void perm_transpose16_kernel( PermArgs a ) {
+  static_assert( sizeof( T ) == 2, "16-byte reads of 8 elements" );
+  constexpr int VR = 8;
+  constexpr int VW = 4;
+  constexpr int PITCH = TI + 2;
+  constexpr int RT = TI / VR;             // read: threads per o row
+  constexpr int WT = TO / VW;             // write: threads per i row
+  constexpr int RP = TI * TO / ( VR * kThreads );
+  constexpr int WP = TI * TO / ( VW * kThreads );
+  static_assert( RP * VR * kThreads == TI * TO && WP * VW * kThreads == TI * TO, "whole passes" );
+  __shared__ T l_tile[TO][PITCH];
+
+  uint32_t l_bid = blockIdx.x;
+  int64_t const l_ti = grid_digit( l_bid, a.tiles_i );
+  int64_t const l_to = grid_digit( l_bid, a.tiles_o );
+  int64_t l_off_in  = 0;
+  int64_t l_off_out = 0;
+  for( int l_d = a.num_batch - 1; l_d >= 0; l_d-- ) {
+    int64_t const l_idx = grid_digit( l_bid, a.batch_size[l_d] );
+    l_off_in  += l_idx * a.batch_s_in[l_d];
+    l_off_out += l_idx * a.batch_s_out[l_d];
+  }
+  T const * l_in  = reinterpret_cast< T const * >( a.in )  + l_off_in;
+  T       * l_out = reinterpret_cast< T       * >( a.out ) + l_off_out;
+  int64_t const l_i0 = l_ti * TI;
+  int64_t const l_o0 = l_to * TO;
+  int const l_t = threadIdx.x;
+
+  // read: rows along o, VR consecutive i per thread (all loads of the
+  // thread in flight before the first LDS store)
+  int const l_c = l_t % RT;
+  int const l_r = l_t / RT;
+  VecN< T, VR > l_v[RP];
+#pragma unroll
+  for( int l_p = 0; l_p < RP; l_p++ ) {
+    int64_t const l_o = l_o0 + l_r + ( kThreads / RT ) * l_p;
+    int64_t const l_i = l_i0 + VR * l_c;
+#pragma unroll
+    for( int l_e = 0; l_e < VR; l_e++ ) l_v[l_p].v[l_e] = T( 0 );
+    if constexpr( VEC ) {
+      if( l_o < a.size_o && l_i < a.size_i ) {
+        l_v[l_p] = *reinterpret_cast< VecN< T, VR > const * >( l_in + l_o * a.s_in_o + l_i );
+      }
+    }
+    else {
+#pragma unroll
+      for( int l_e = 0; l_e < VR; l_e++ ) {
+        if( l_o < a.size_o && l_i + l_e < a.size_i ) l_v[l_p].v[l_e] = l_in[l_o * a.s_in_o + l_i + l_e];
+      }
+    }
+  }
+#pragma unroll
+  for( int l_p = 0; l_p < RP; l_p++ ) {
+    int const l_row = l_r + ( kThreads / RT ) * l_p;
+#pragma unroll
+    for( int l_e = 0; l_e < VR; l_e++ ) l_tile[l_row][VR * l_c + l_e] = l_v[l_p].v[l_e];
+  }
+
+  __syncthreads();
+
+  // write: rows along i, VW consecutive o per thread
+  int const l_wc = l_t % WT;
+  int const l_wr = l_t / WT;
+#pragma unroll
+  for( int l_p = 0; l_p < WP; l_p++ ) {
+    int const l_row = l_wr + ( kThreads / WT ) * l_p;
+    int64_t const l_i = l_i0 + l_row;
+    int64_t const l_o = l_o0 + VW * l_wc;
+    VecN< T, VW > l_w;
+#pragma unroll
+    for( int l_e = 0; l_e < VW; l_e++ ) l_w.v[l_e] = l_tile[VW * l_wc + l_e][l_row];
+    if constexpr( VEC ) {
+      if( l_i < a.size_i && l_o < a.size_o ) {
+        VecN< T, VW > * l_ptr = reinterpret_cast< VecN< T, VW > * >( l_out + l_i * a.s_out_i + l_o );
+        if( a.add ) {
+          VecN< T, VW > const l_old = *l_ptr;
+#pragma unroll
+          for( int l_e = 0; l_e < VW; l_e++ ) l_w.v[l_e] = Elem< T >::add( l_old.v[l_e], l_w.v[l_e] );
+        }
+        *l_ptr = l_w;
+      }
+    }
+    else {
+#pragma unroll
+      for( int l_e = 0; l_e < VW; l_e++ ) {
+        if( l_i < a.size_i && l_o + l_e < a.size_o ) {
+          T * l_ptr = l_out + l_i * a.s_out_i + l_o + l_e;
+          *l_ptr = a.add ? Elem< T >::add( *l_ptr, l_w.v[l_e] ) : l_w.v[l_e];
+        }
+      }
+    }
+  }
+}
+
 template< typename T, int TI, int TO >
 __global__ __launch_bounds__( kThreads )
 void perm_transpose_kernel( PermArgs a ) {
@@ -725,7 +831,28 @@ int launch_typed( PermutePlan const & p,
       return fail( ETIR_UNDEFINED_ERROR, "permute: grid too large" );
     }
     dim3 const l_g( (uint32_t) l_blocks );
-    if( p.tr_shape == 1 )      hipLaunchKernelGGL( ( perm_transpose_kernel< T, 128, 32 > ), l_g, dim3( kThreads ), 0, stream, a );
+    if( p.tr_shape == 3 || p.tr_shape == 4 ) {
+      if constexpr( sizeof( T ) == 2 ) {
+        auto go = [&]( auto to_c, auto vec_c ) {
+          hipLaunchKernelGGL( ( perm_transpose16_kernel< T, 128, decltype( to_c )::value, decltype( vec_c )::value > ),
+                              l_g, dim3( kThreads ), 0, stream, a );
+        };
+        std::integral_constant< int, 64 > const l_to64{};
+        std::integral_constant< int, 32 > const l_to32{};
+        if( p.tr_shape == 3 ) {
+          if( a.vec_ok ) go( l_to64, std::true_type() );
+          else           go( l_to64, std::false_type() );
+        }
+        else {
+          if( a.vec_ok ) go( l_to32, std::true_type() );
+          else           go( l_to32, std::false_type() );
+        }
+      }
+      else {
+        return fail( ETIR_UNDEFINED_ERROR, "permute: 16-byte transpose tile for a non-2-byte type" );
+      }
+    }
+    else if( p.tr_shape == 1 ) hipLaunchKernelGGL( ( perm_transpose_kernel< T, 128, 32 > ), l_g, dim3( kThreads ), 0, stream, a );
     else if( p.tr_shape == 2 ) hipLaunchKernelGGL( ( perm_transpose_kernel< T, 32, 128 > ), l_g, dim3( kThreads ), 0, stream, a );
     else                       hipLaunchKernelGGL( ( perm_transpose_kernel< T, 64, 64 > ), l_g, dim3( kThreads ), 0, stream, a );
   }
@@ -1471,8 +1598,22 @@ int plan_permute( int64_t         num_dims,
     double l_best = 1.25 * util( kTile, kTile );
     if( util( 128, 32 ) >= l_best ) { plan.tr_shape = 1; l_best = util( 128, 32 ); }
     if( util( 32, 128 ) > l_best )  plan.tr_shape = 2;
-    int64_t const l_ti = plan.tr_shape == 1 ? 128 : ( plan.tr_shape == 2 ? 32 : kTile );
-    int64_t const l_to = 4 * 4 * kThreads / l_ti;
+    int64_t l_ti = plan.tr_shape == 1 ? 128 : ( plan.tr_shape == 2 ? 32 : kTile );
+    int64_t l_to = 4 * 4 * kThreads / l_ti;
+    // 2-byte elements whose input rows allow 8-element vectors (and output
+    // rows 4-element ones): the 16-byte-read transpose, 128 x 64 unless
+    // 128 x 32 fills strictly more of its padded tile grid
+    bool l_v16 = plan.elem_bytes == 2 && a.size_i % 8 == 0 && a.s_in_o % 8 == 0 && a.size_o % 4 == 0
+              && a.s_out_i % 4 == 0;
+    for( int l_di = 0; l_di < l_n; l_di++ ) {
+      if( l_di != l_dim_i && plan.s_in[l_di] % 8 != 0 ) l_v16 = false;
+      if( l_di != l_dim_o && plan.s_out[l_di] % 4 != 0 ) l_v16 = false;
+    }
+    if( l_v16 ) {
+      plan.tr_shape = ( util( 128, 32 ) > util( 128, 64 ) ) ? 4 : 3;
+      l_ti = 128;
+      l_to = ( plan.tr_shape == 3 ) ? 64 : 32;
+    }
     a.tiles_i = ( a.size_i + l_ti - 1 ) / l_ti;
     a.tiles_o = ( a.size_o + l_to - 1 ) / l_to;
     a.num_batch = 0;
@@ -1532,6 +1673,8 @@ int launch_permute( PermutePlan const & plan,
         || ( plan.mode != PermMode::FILL && ( uintptr_t( in ) % l_align ) != 0 ) ) {
       a.vec_ok = 0;
     }
+    // the 16-byte-read transpose reads 8 elements per vector
+    if( plan.mode == PermMode::TRANSPOSE && plan.tr_shape >= 3 && uintptr_t( in ) % 16 != 0 ) a.vec_ok = 0;
   }
   if(    a.vec_wide
       && (    ( uintptr_t( out ) % 16 ) != 0

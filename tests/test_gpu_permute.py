@@ -170,6 +170,47 @@ def test_permute_transpose_shapes(torch_cuda, oracle, expr, sizes, tile, dtype, 
     assert "transpose" in desc and tile in desc, desc
 
 
+# bf16 transposes with 16-byte reads (input rows in groups of 8 elements,
+# output rows in groups of 4): 128 x 64 tiles, or 128 x 32 where those fill
+# more of their padded grid; ragged extents on both sides
+TR16_CASES = [
+    ("abcd->bdac", dict(a=36, b=5, c=36, d=512), "tile=128x64 v16"),
+    ("abcd->bdac", dict(a=7, b=3, c=72, d=256), "tile=128x32 v16"),     # o = 72: 72/96 of 32-row tiles
+    ("abcd->dbca", dict(a=64, b=3, c=5, d=200), "tile=128x64 v16"),     # i = 200: 200 of 256
+    ("abc->cba", dict(a=100, b=3, c=136), "tile=128x64 v16"),           # o = 100: 100 of 128
+]
+
+
+@pytest.mark.parametrize("expr,sizes,tile", TR16_CASES)
+@pytest.mark.parametrize("ktype", [eir.COPY, eir.ADD])
+def test_permute_transpose16_bf16(torch_cuda, oracle, expr, sizes, tile, ktype):
+    desc = _check(torch_cuda, oracle, expr, sizes, dtype=eir.BF16, ktype=ktype, seed=sizes["a"] + int(ktype))
+    assert "transpose" in desc and tile in desc, desc
+
+
+@pytest.mark.parametrize("offset", [1, 4])
+def test_permute_transpose16_unaligned(torch_cuda, oracle, offset):
+    """The 16-byte-read bf16 transpose on tensors whose base addresses are
+    not 16-byte aligned (offset by 1 or 4 elements): one element per access,
+    same result."""
+    torch = torch_cuda
+    sizes = dict(a=36, b=5, c=36, d=512)
+    u = eir.unary_dims("abcd->bdac", sizes)
+    n = 36 * 5 * 36 * 512
+    rng = np.random.default_rng(70 + offset)
+    x = rng.integers(0, 2 ** 16, n + offset, dtype=np.uint64).astype(np.uint16)
+    o0 = rng.integers(0, 2 ** 14, n + offset, dtype=np.uint64).astype(np.uint16)
+    ref = o0[offset:].copy()
+    oracle.permute(u["sizes"], u["strides_in"], u["strides_out"], x[offset:].copy(), ref, dtype=eir.BF16)
+    plan = eir.PermutePlan(u["sizes"], u["strides_in"], u["strides_out"], dtype=eir.BF16)
+    assert "tile=128x64 v16" in plan.describe(), plan.describe()
+    dx, do = _to_dev(torch, x), _to_dev(torch, o0)
+    plan.execute(dx[offset:], do[offset:], stream=torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    plan.close()
+    np.testing.assert_array_equal(do[offset:].cpu().numpy().view(np.uint16), ref)
+
+
 # a unit-stride dim shared by both tensors with short rows: whole rows
 # through LDS (ROWS), runs of the input's and the output's next dims
 ROWS_CASES = [
