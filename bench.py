@@ -269,7 +269,10 @@ PERMUTES_4D = [
 # tensors larger than the 256 MB Infinity Cache (MALL) in front of HBM: every
 # launch reads and writes HBM itself (128^4 elements: 1 GiB each way in fp32,
 # 512 MiB in bf16)
-PERMUTES_BEYOND_CACHE = [("abcd->dbca", (128, 128, 128, 128))]
+PERMUTES_BEYOND_CACHE = [("abcd->dbca", (128, 128, 128, 128)),
+                         # same unit-stride dim on both sides: the vector copy,
+                         # the ceiling any permutation of these bytes meets
+                         ("abcd->bacd", (128, 128, 128, 128))]
 
 
 def bench_permutes_4d(torch, eir, stream, dtype="fp32", shapes=None, steps=SHORT_STEPS):
@@ -644,8 +647,15 @@ def main():
         log("permutes 4-D bf16: " + ", ".join(f"{r['expr']}{r['sizes']} {r['gbs']:.0f}" for r in p4b))
         big = [dict(r, dtype=dt) for dt in ("fp32", "bf16")
                for r in bench_permutes_4d(torch, eir, stream, dtype=dt, shapes=PERMUTES_BEYOND_CACHE, steps=20)]
+        # torch's copy of the same 1 GiB: the device's own read + write rate
+        src = torch.rand(128 ** 4, device="cuda")
+        dst = torch.empty_like(src)
+        _, per = time_launches(torch, stream, lambda: dst.copy_(src), 20, 5)
+        del src, dst
+        torch_copy = round(2 * 4 * 128 ** 4 / per * 1e-9, 1)
         extra["permutes_beyond_infinity_cache"] = dict(
             unit="GB/s", note="tensors larger than the 256 MB Infinity Cache: HBM-resident every launch",
+            torch_copy_1GiB_fp32_gbs=torch_copy, torch_copy_frac_hbm_peak=round(torch_copy / PEAK_HBM_GBS, 4),
             cases=big)
         log("permutes beyond the Infinity Cache: "
             + ", ".join(f"{r['dtype']} {r['expr']}{r['sizes']} {r['gbs']:.0f}" for r in big))

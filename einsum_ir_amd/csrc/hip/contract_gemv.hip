@@ -26,6 +26,10 @@ namespace etir {
 
 namespace {
 
+// four consecutive elements moved as one vector
+template< typename T >
+struct alignas( 4 * sizeof( T ) ) V4 { T v[4]; };
+
 template< typename T >
 __device__ inline float gemv_ld( T const * p, int64_t off );
 template<>
@@ -104,22 +108,144 @@ __global__ __launch_bounds__( 256 ) void contract_gemv_kernel( ContractArgs a ) 
   else             reinterpret_cast< float * >( a.out )[l_off] = l_v;
 }
 
+// Kernel M == 1 with the long operand B and the output unit-stride along N
+// (a.gemv_v4): each thread takes 4 consecutive n, one 4-element vector of B
+// per k (16 bytes fp32, 8 bytes bf16) and one vector store, each output
+// summed in ascending k with its own accumulator exactly as above.  The
+// short operand A is one value per k for all four.  Aux values are read per
+// element (the aux tensor may broadcast along n).
+template< typename T, bool KAFF >
+__global__ __launch_bounds__( 256 ) void contract_gemv4_kernel( ContractArgs a ) {
+  typedef float f4 __attribute__( ( ext_vector_type( 4 ) ) );
+  typedef V4< T > TV;
+  int32_t const l_n4 = a.N / 4;
+  uint64_t const l_total = uint64_t( a.C ) * uint64_t( l_n4 );
+  uint64_t const l_e = uint64_t( blockIdx.x ) * 256 + threadIdx.x;
+  if( l_e >= l_total ) return;
+  int32_t l_c, l_q;
+  if( l_total <= 0xffffffffull ) {
+    l_c = int32_t( uint32_t( l_e ) / uint32_t( l_n4 ) );
+    l_q = int32_t( uint32_t( l_e ) - uint32_t( l_c ) * uint32_t( l_n4 ) );
+  }
+  else {
+    l_c = int32_t( l_e / uint64_t( l_n4 ) );
+    l_q = int32_t( l_e - uint64_t( l_c ) * uint64_t( l_n4 ) );
+  }
+  int32_t const l_n = 4 * l_q;
+
+  bool const l_read_out  = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_UNDEFINED );
+  bool const l_aux_first = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_COPY );
+  bool const l_need_aux  = ( a.aux != nullptr ) && ( l_aux_first || a.last_touch == ETIR_KTYPE_ADD );
+  int64_t const l_off = a.tc_out[l_c] + a.tm_out[0] + l_n;
+  float l_aux[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
+  if( l_need_aux ) {
+    int64_t const l_ab = a.tc_aux[l_c] + a.tm_aux[0];
+#pragma unroll
+    for( int l_i = 0; l_i < 4; l_i++ ) {
+      int64_t const l_aoff = l_ab + a.tn_aux[l_n + l_i];
+      l_aux[l_i] = a.out_bf16 ? kern::bf16_to_f32( reinterpret_cast< uint16_t const * >( a.aux )[l_aoff] )
+                              : reinterpret_cast< float const * >( a.aux )[l_aoff];
+    }
+  }
+  float l_old[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
+  if( l_read_out ) {
+    if( a.out_bf16 ) {
+      V4< uint16_t > const l_o = *reinterpret_cast< V4< uint16_t > const * >(
+          reinterpret_cast< uint16_t const * >( a.out ) + l_off );
+#pragma unroll
+      for( int l_i = 0; l_i < 4; l_i++ ) l_old[l_i] = kern::bf16_to_f32( l_o.v[l_i] );
+    }
+    else {
+      f4 const l_o = *reinterpret_cast< f4 const * >( reinterpret_cast< float const * >( a.out ) + l_off );
+#pragma unroll
+      for( int l_i = 0; l_i < 4; l_i++ ) l_old[l_i] = l_o[l_i];
+    }
+  }
+
+  T const * l_pa = reinterpret_cast< T const * >( a.a ) + a.tc_a[l_c] + a.tm_a[0];
+  T const * l_pb = reinterpret_cast< T const * >( a.b ) + a.tc_b[l_c] + l_n;
+  auto koff_a = [&]( int32_t k ) -> int64_t { return KAFF ? int64_t( k ) * a.sk_a : int64_t( a.tk_a[k] ); };
+  auto koff_b = [&]( int32_t k ) -> int64_t { return KAFF ? int64_t( k ) * a.sk_b : int64_t( a.tk_b[k] ); };
+  auto ld4 = [&]( int64_t off ) {
+    TV const l_t = *reinterpret_cast< TV const * >( l_pb + off );
+    f4 l_r;
+#pragma unroll
+    for( int l_i = 0; l_i < 4; l_i++ ) l_r[l_i] = gemv_ld< T >( l_t.v, l_i );
+    return l_r;
+  };
+
+  float l_v[4] = { 0.0f, 0.0f, 0.0f, 0.0f };
+  int32_t l_k = 0;
+  for( ; l_k + 8 <= a.K; l_k += 8 ) {
+    float l_x[8];
+    f4    l_y[8];
+#pragma unroll
+    for( int l_j = 0; l_j < 8; l_j++ ) {
+      l_x[l_j] = gemv_ld< T >( l_pa, koff_a( l_k + l_j ) );
+      l_y[l_j] = ld4( koff_b( l_k + l_j ) );
+    }
+#pragma unroll
+    for( int l_j = 0; l_j < 8; l_j++ )
+#pragma unroll
+      for( int l_i = 0; l_i < 4; l_i++ ) l_v[l_i] = fmaf( l_x[l_j], l_y[l_j][l_i], l_v[l_i] );
+  }
+  for( ; l_k < a.K; l_k++ ) {
+    float const l_x = gemv_ld< T >( l_pa, koff_a( l_k ) );
+    f4 const l_y = ld4( koff_b( l_k ) );
+#pragma unroll
+    for( int l_i = 0; l_i < 4; l_i++ ) l_v[l_i] = fmaf( l_x, l_y[l_i], l_v[l_i] );
+  }
+
+  float l_r[4];
+#pragma unroll
+  for( int l_i = 0; l_i < 4; l_i++ ) {
+    float l_w = l_v[l_i];
+    if( l_read_out ) l_w = l_old[l_i] + l_w;
+    if( l_aux_first ) l_w = l_aux[l_i] + l_w;
+    if( a.last_touch == ETIR_KTYPE_RELU ) l_w = fmaxf( l_w, 0.0f );
+    else if( a.last_touch == ETIR_KTYPE_ADD ) l_w = l_w + l_aux[l_i];
+    l_r[l_i] = l_w;
+  }
+  if( a.out_bf16 ) {
+    V4< uint16_t > l_o;
+#pragma unroll
+    for( int l_i = 0; l_i < 4; l_i++ ) l_o.v[l_i] = kern::f32_to_bf16_rne( l_r[l_i] );
+    *reinterpret_cast< V4< uint16_t > * >( reinterpret_cast< uint16_t * >( a.out ) + l_off ) = l_o;
+  }
+  else {
+    *reinterpret_cast< f4 * >( reinterpret_cast< float * >( a.out ) + l_off ) = f4{ l_r[0], l_r[1], l_r[2], l_r[3] };
+  }
+}
+
 }  // namespace
 
 int launch_contract_gemv( bool bf16_in, ContractArgs const & a, hipStream_t stream ) {
   int64_t const l_total = int64_t( a.C ) * a.M * a.N;
   if( l_total == 0 ) return ETIR_SUCCESS;
-  int64_t const l_blocks = ( l_total + 255 ) / 256;
+  int64_t const l_esz = bf16_in ? 2 : 4;
+  // vector accesses need the long operand's and the output's base addresses
+  // aligned to one vector
+  bool const l_v4 = a.gemv_v4 && a.M == 1 && reinterpret_cast< uintptr_t >( a.b ) % uintptr_t( 4 * l_esz ) == 0
+                 && reinterpret_cast< uintptr_t >( a.out ) % uintptr_t( a.out_bf16 ? 8 : 16 ) == 0;
+  int64_t const l_blocks = ( ( l_v4 ? l_total / 4 : l_total ) + 255 ) / 256;
   if( l_blocks > 0x7fffffffLL ) return fail( ETIR_UNDEFINED_ERROR, "gemv contraction: grid too large" );
   dim3 const l_grid( (uint32_t) l_blocks );
   bool const l_kaff = ( a.k_affine != 0 );
+  auto go = [&]( auto t_c, auto kaff_c ) {
+    typedef typename decltype( t_c )::type T;
+    constexpr bool KA = decltype( kaff_c )::value;
+    if( l_v4 ) hipLaunchKernelGGL( ( contract_gemv4_kernel< T, KA > ), l_grid, dim3( 256 ), 0, stream, a );
+    else       hipLaunchKernelGGL( ( contract_gemv_kernel< T, KA > ), l_grid, dim3( 256 ), 0, stream, a );
+  };
+  struct F32 { typedef float type; };
+  struct BF16 { typedef uint16_t type; };
   if( bf16_in ) {
-    if( l_kaff ) hipLaunchKernelGGL( ( contract_gemv_kernel< uint16_t, true > ), l_grid, dim3( 256 ), 0, stream, a );
-    else         hipLaunchKernelGGL( ( contract_gemv_kernel< uint16_t, false > ), l_grid, dim3( 256 ), 0, stream, a );
+    if( l_kaff ) go( BF16(), std::true_type() );
+    else         go( BF16(), std::false_type() );
   }
   else {
-    if( l_kaff ) hipLaunchKernelGGL( ( contract_gemv_kernel< float, true > ), l_grid, dim3( 256 ), 0, stream, a );
-    else         hipLaunchKernelGGL( ( contract_gemv_kernel< float, false > ), l_grid, dim3( 256 ), 0, stream, a );
+    if( l_kaff ) go( F32(), std::true_type() );
+    else         go( F32(), std::false_type() );
   }
   return ETIR_SUCCESS;
 }

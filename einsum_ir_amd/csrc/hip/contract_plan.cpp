@@ -865,6 +865,10 @@ int plan_contraction_impl( int64_t            num_loops,
   a.sn_b   = affine_stride( l_tn_b );
   a.sm_out = affine_stride( l_tm_out );
   a.sn_out = affine_stride( l_tn_out );
+  a.gemv_v4 = ( plan.tile == TILE_GEMV && l_tm_out.size() == 1 && l_tn_out.size() % 4 == 0 && a.sn_b == 1
+                && a.sn_out == 1 && all_multiple( l_tc_b, 4 ) && all_multiple( l_tk_b, 4 )
+                && all_multiple( l_tc_out, 4 ) && all_multiple( l_tm_out, 4 ) ) ? 1 : 0;
+  if( a.gemv_v4 ) plan.desc += " v4";
   if( l_cpx ) {
     a.cpx_a   = l_x[0].s[l_sa];
     a.cpx_b   = l_x[0].s[l_sb];

@@ -248,6 +248,10 @@ struct ContractArgs {
   // persistent direct-to-LDS kernel: start-time stagger, dma_phases groups of
   // workgroups, group p starts p * dma_stagger sleep units (~1 us) late
   int32_t dma_phases, dma_stagger;
+  // matrix-vector kernel (kernel M == 1): the long operand B and the output
+  // are unit-stride along N with every offset a multiple of 4 elements and
+  // N % 4 == 0, so a thread takes 4 consecutive outputs with vector accesses
+  int32_t gemv_v4;
 };
 
 struct ContractionPlan {

@@ -80,3 +80,66 @@ def test_gemv_switched_off(torch_cuda, oracle, monkeypatch):
     monkeypatch.setenv("ETIR_NO_GEMV", "1")
     _, desc = run_case(torch_cuda, oracle, "zk,zkn->zn", dict(z=64, k=11, n=8192), seed=2)
     assert "gemv" not in desc, desc
+
+
+@pytest.mark.parametrize("dtype,dtype_out,first,last", [
+    (eir.FP32, eir.FP32, eir.ZERO, eir.UNDEFINED_KTYPE),
+    (eir.FP32, eir.FP32, eir.COPY, eir.RELU),
+    (eir.FP32, eir.FP32, eir.ADD, eir.UNDEFINED_KTYPE),
+    (eir.BF16, eir.FP32, eir.ZERO, eir.UNDEFINED_KTYPE),
+    (eir.BF16, eir.BF16, eir.UNDEFINED_KTYPE, eir.ADD),
+])
+def test_gemv_four_outputs_per_thread(torch_cuda, oracle, monkeypatch, dtype, dtype_out, first, last):
+    """Kernel M == 1 with the long operand and the output unit-stride along n
+    ('v4': 4 outputs per thread, vector loads and stores) against the
+    one-output kernel, which runs when the long operand's base address is not
+    vector-aligned (offset by one element): the same bits, and the oracle's
+    result.  K = 11 (one 8-wide chunk and a tail), a bias broadcast over the
+    batch dim for the aux touches."""
+    import numpy as np
+    from tests.helpers import loops_for, rel_frobenius
+    torch = torch_cuda
+    monkeypatch.delenv("ETIR_TILE", raising=False)
+    z, k, n = 64, 11, 8192
+    loops = loops_for("zk,zkn->zn", dict(z=z, k=k, n=n), sizes_outer_aux=dict(z=1, n=n))
+    rng = np.random.default_rng(80 + first + 10 * last)
+    tdt = torch.bfloat16 if dtype == eir.BF16 else torch.float32
+    odt = torch.bfloat16 if dtype_out == eir.BF16 else torch.float32
+    a = torch.from_numpy(rng.uniform(-1, 1, z * k).astype(np.float32)).cuda().to(tdt)
+    b0 = torch.from_numpy(rng.uniform(-1, 1, z * k * n).astype(np.float32)).cuda().to(tdt)
+    b_all = torch.empty(z * k * n + 1, device="cuda", dtype=tdt)
+    b_all[1:].copy_(b0)
+    b1 = b_all[1:]                              # same values, base address one element off
+    aux = torch.from_numpy(rng.uniform(-1, 1, n).astype(np.float32)).cuda().to(odt)
+    o0 = torch.from_numpy(rng.uniform(-1, 1, z * n).astype(np.float32)).cuda().to(odt)
+    plan = eir.ContractionPlan(loops["dim_types"], loops["sizes"], loops["strides_left"], loops["strides_right"],
+                               loops["strides_out"], strides_out_aux=loops["strides_out_aux"], dtype_left=dtype,
+                               dtype_right=dtype, dtype_out=dtype_out, ktype_first_touch=first,
+                               ktype_last_touch=last)
+    desc = plan.describe()
+    assert "contract gemv" in desc and " v4" in desc, desc
+    outs = []
+    for b in (b0, b1):
+        o = o0.clone()
+        plan.execute(a, b, o, aux=aux, stream=torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        outs.append(o.float().cpu().numpy())
+    plan.close()
+    assert np.array_equal(outs[0], outs[1]), "4-output and 1-output kernels differ"
+    A = a.float().double().cpu().numpy().reshape(z, k)
+    B = b0.float().double().cpu().numpy().reshape(z, k, n)
+    ref = np.einsum("zk,zkn->zn", A, B)
+    x = aux.float().double().cpu().numpy().reshape(1, n)
+    old = o0.float().double().cpu().numpy().reshape(z, n)
+    if first == eir.COPY:
+        ref = ref + x
+    elif first == eir.ADD:
+        ref = ref + x + old
+    elif first == eir.UNDEFINED_KTYPE:
+        ref = ref + old
+    if last == eir.RELU:
+        ref = np.maximum(ref, 0.0)
+    elif last == eir.ADD:
+        ref = ref + x
+    tol = 2e-3 if (dtype == eir.BF16 or dtype_out == eir.BF16) else 1e-5
+    assert rel_frobenius(ref.ravel(), outs[0].ravel()) <= tol
