@@ -175,6 +175,77 @@ struct Loader< R, BK, T, ESZ, LOAD_VEC_K > {
   }
 };
 
+// 8-byte vectors along K (fp32: two consecutive k), for K runs of even length
+// that are not multiples of 4; LOAD_VEC_K's [row][k] LDS layout and pitch.
+// Every K run has even length, so a vector is wholly inside K or past it.
+template< int R, int BK, int T, int ESZ >
+struct Loader< R, BK, T, ESZ, LOAD_VEC8_K > {
+  static constexpr int V      = 8 / ESZ;            // elements per vector
+  static constexpr int VPR    = BK / V;             // vectors per row
+  static constexpr int COUNT  = R * VPR;
+  static constexpr int NV     = ( COUNT + T - 1 ) / T;
+  static constexpr int LDK    = BK + 16 / ESZ;
+  static_assert( NV <= 32, "validity mask" );
+
+  u32x2    m_reg[NV];
+  int32_t  m_row_off[NV];
+  uint32_t m_row_ok;
+  uint32_t m_ok;
+  int32_t  m_koff;
+  int      m_kv;
+
+  __device__ inline void init( int32_t const * tab_rows, int32_t rows, int32_t row0 ) {
+    int const l_t = threadIdx.x;
+    m_kv = ( l_t % VPR ) * V;
+    m_row_ok = 0;
+#pragma unroll
+    for( int l_i = 0; l_i < NV; l_i++ ) {
+      int const l_idx = l_t + l_i * T;
+      int const l_row = l_idx / VPR;
+      int const l_g   = row0 + l_row;
+      bool const l_ok = l_idx < COUNT && l_g < rows;
+      if( l_ok ) m_row_ok |= 1u << l_i;
+      m_row_off[l_i] = tab_rows[l_ok ? l_g : 0];
+    }
+  }
+
+  template< bool KAFF >
+  __device__ inline void setup( int32_t k0, int32_t K, int32_t const * tab_k, int32_t sk ) {
+    int32_t const l_k  = k0 + m_kv;
+    bool const    l_ok = l_k < K;
+    int32_t const l_kc = l_ok ? l_k : 0;
+    m_koff = KAFF ? l_kc * sk : tab_k[l_kc];
+    m_ok   = l_ok ? m_row_ok : 0u;
+  }
+
+  template< int I, typename TE >
+  __device__ inline void issue( TE const * base ) {
+    m_reg[I] = *reinterpret_cast< u32x2 const * >( base + m_row_off[I] + m_koff );
+  }
+
+  template< int I, typename TE >
+  __device__ inline void put( TE * lds ) {
+    int const l_idx = int( threadIdx.x ) + I * T;
+    if( COUNT % T == 0 || l_idx < COUNT ) {
+      int const l_row = l_idx / VPR;
+      u32x2 const l_v = ( ( m_ok >> I ) & 1u ) ? m_reg[I] : u32x2{ 0u, 0u };
+      *reinterpret_cast< u32x2 * >( lds + l_row * LDK + m_kv ) = l_v;
+    }
+  }
+
+  template< bool KAFF, typename TE >
+  __device__ inline void load( TE const * base, int32_t k0, int32_t K,
+                               int32_t const * tab_k, int32_t sk ) {
+    setup< KAFF >( k0, K, tab_k, sk );
+    static_for< NV >( [&]( auto ic ) __attribute__( ( always_inline ) ) { issue< decltype( ic )::value >( base ); } );
+  }
+
+  template< typename TE >
+  __device__ inline void store( TE * lds ) {
+    static_for< NV >( [&]( auto ic ) __attribute__( ( always_inline ) ) { put< decltype( ic )::value >( lds ); } );
+  }
+};
+
 // element gathers through the tables; same thread layout as LOAD_VEC_K
 template< int R, int BK, int T, int ESZ >
 struct Loader< R, BK, T, ESZ, LOAD_SCALAR > {
@@ -305,6 +376,74 @@ struct Loader< R, BK, T, ESZ, LOAD_VEC_MN > {
     int const l_k = m_k + I * ( T / VPK );
     u32x4 const l_v = ( ( m_ok >> I ) & 1u ) ? m_reg[I] : u32x4{ 0u, 0u, 0u, 0u };
     *reinterpret_cast< u32x4 * >( lds + l_k * PK + m_mv * V ) = l_v;
+  }
+
+  template< bool KAFF, typename TE >
+  __device__ inline void load( TE const * base, int32_t k0, int32_t K,
+                               int32_t const * tab_k, int32_t sk ) {
+    setup< KAFF >( k0, K, tab_k, sk );
+    static_for< NV >( [&]( auto ic ) __attribute__( ( always_inline ) ) { issue< decltype( ic )::value >( base ); } );
+  }
+
+  template< typename TE >
+  __device__ inline void store( TE * lds ) {
+    static_for< NV >( [&]( auto ic ) __attribute__( ( always_inline ) ) { put< decltype( ic )::value >( lds ); } );
+  }
+};
+
+// 8-byte vectors of two consecutive rows (fp32), for row runs of even length
+// that are not multiples of 4; LOAD_VEC_MN's [k][row] LDS layout and pitch.
+// The operand's row count is even, so a vector is wholly inside or past it.
+template< int R, int BK, int T, int ESZ >
+struct Loader< R, BK, T, ESZ, LOAD_VEC8_MN > {
+  static constexpr int V      = 8 / ESZ;            // rows per vector
+  static constexpr int VPK    = R / V;              // vectors per k row
+  static constexpr int COUNT  = BK * VPK;
+  static constexpr int NV     = COUNT / T;
+  static constexpr int PK     = KmPitch< R, ESZ >::value;
+  static_assert( COUNT % T == 0 && T % VPK == 0, "VEC8_MN loader: tile/threads mismatch" );
+  static_assert( NV <= 32, "validity mask" );
+
+  u32x2    m_reg[NV];
+  int32_t  m_koff[NV];
+  int32_t  m_row_off;
+  bool     m_row_ok;
+  uint32_t m_ok;
+  int      m_mv;
+  int      m_k;
+
+  __device__ inline void init( int32_t const * tab_rows, int32_t rows, int32_t row0 ) {
+    int const l_t = threadIdx.x;
+    m_mv = l_t % VPK;
+    m_k  = l_t / VPK;
+    int const l_g = row0 + m_mv * V;
+    m_row_ok  = l_g < rows;
+    m_row_off = tab_rows[m_row_ok ? l_g : 0];
+  }
+
+  template< bool KAFF >
+  __device__ inline void setup( int32_t k0, int32_t K, int32_t const * tab_k, int32_t sk ) {
+    m_ok = 0;
+#pragma unroll
+    for( int l_i = 0; l_i < NV; l_i++ ) {
+      int32_t const l_k  = k0 + m_k + l_i * ( T / VPK );
+      bool const    l_ok = l_k < K;
+      int32_t const l_kc = l_ok ? l_k : 0;
+      m_koff[l_i] = KAFF ? l_kc * sk : tab_k[l_kc];
+      if( l_ok && m_row_ok ) m_ok |= 1u << l_i;
+    }
+  }
+
+  template< int I, typename TE >
+  __device__ inline void issue( TE const * base ) {
+    m_reg[I] = *reinterpret_cast< u32x2 const * >( base + m_row_off + m_koff[I] );
+  }
+
+  template< int I, typename TE >
+  __device__ inline void put( TE * lds ) {
+    int const l_k = m_k + I * ( T / VPK );
+    u32x2 const l_v = ( ( m_ok >> I ) & 1u ) ? m_reg[I] : u32x2{ 0u, 0u };
+    *reinterpret_cast< u32x2 * >( lds + l_k * PK + m_mv * V ) = l_v;
   }
 
   template< bool KAFF, typename TE >
@@ -653,8 +792,10 @@ void contract_kernel( ContractArgs a ) {
   constexpr int ESZ  = sizeof( TE );
   constexpr int TM   = BM / WM / 32;
   constexpr int TN   = BN / WN / 32;
-  constexpr int SZA  = LdsSize< ESZ, MA, BM, BK >::value;
-  constexpr int SZB  = LdsSize< ESZ, MB, BN, BK >::value;
+  constexpr int LA   = lds_layout( MA );     // LDS layout of A and B
+  constexpr int LB   = lds_layout( MB );
+  constexpr int SZA  = LdsSize< ESZ, LA, BM, BK >::value;
+  constexpr int SZB  = LdsSize< ESZ, LB, BN, BK >::value;
   static_assert( TM >= 1 && TN >= 1, "wave tile must hold at least one 32x32 block" );
 
   // one allocation: double-buffered A and B tiles, reused by the epilogue
@@ -718,8 +859,8 @@ void contract_kernel( ContractArgs a ) {
     __syncthreads();
 
     // rows of this wave's blocks; VEC_MN readers take the block base row
-    int const l_ra = l_wm * TM * 32 + ( MA == LOAD_VEC_MN ? 0 : l_lr );
-    int const l_rb = l_wn * TN * 32 + ( MB == LOAD_VEC_MN ? 0 : l_lr );
+    int const l_ra = l_wm * TM * 32 + ( LA == LOAD_VEC_MN ? 0 : l_lr );
+    int const l_rb = l_wn * TN * 32 + ( LB == LOAD_VEC_MN ? 0 : l_lr );
 
     // One K step on LDS buffer l_cur.  With MORE, the operand vectors of the
     // next step are loaded from global memory between the MFMAs of the first
@@ -757,18 +898,18 @@ void contract_kernel( ContractArgs a ) {
 #pragma unroll
         for( int l_i = 0; l_i < TM; l_i++ ) {
           if constexpr( DT == ETIR_FP32 )
-            l_fa[l_i] = Frag< 4, MA, BM, BK >::read4( l_sa, l_ra + l_i * 32 + ( MA == LOAD_VEC_MN ? l_lr : 0 ),
+            l_fa[l_i] = Frag< 4, LA, BM, BK >::read4( l_sa, l_ra + l_i * 32 + ( LA == LOAD_VEC_MN ? l_lr : 0 ),
                                                       l_s, l_lane );
           else
-            l_fa[l_i] = Frag< 2, MA, BM, BK >::read8( l_sa, l_ra + l_i * 32, l_s, l_lane );
+            l_fa[l_i] = Frag< 2, LA, BM, BK >::read8( l_sa, l_ra + l_i * 32, l_s, l_lane );
         }
 #pragma unroll
         for( int l_j = 0; l_j < TN; l_j++ ) {
           if constexpr( DT == ETIR_FP32 )
-            l_fb[l_j] = Frag< 4, MB, BN, BK >::read4( l_sb, l_rb + l_j * 32 + ( MB == LOAD_VEC_MN ? l_lr : 0 ),
+            l_fb[l_j] = Frag< 4, LB, BN, BK >::read4( l_sb, l_rb + l_j * 32 + ( LB == LOAD_VEC_MN ? l_lr : 0 ),
                                                       l_s, l_lane );
           else
-            l_fb[l_j] = Frag< 2, MB, BN, BK >::read8( l_sb, l_rb + l_j * 32, l_s, l_lane );
+            l_fb[l_j] = Frag< 2, LB, BN, BK >::read8( l_sb, l_rb + l_j * 32, l_s, l_lane );
         }
         static_for< NG >( [&]( auto gc ) __attribute__( ( always_inline ) ) {
           constexpr int l_g = decltype( gc )::value;

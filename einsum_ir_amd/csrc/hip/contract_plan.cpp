@@ -139,6 +139,8 @@ std::string dims_str( std::vector< Loop > const & dims ) {
 char const * mode_str( int32_t m ) {
   if( m == LOAD_VEC_MN ) return "vec_mn";
   if( m == LOAD_VEC_K )  return "vec_k";
+  if( m == LOAD_VEC8_MN ) return "vec8_mn";
+  if( m == LOAD_VEC8_K )  return "vec8_k";
   return "scalar";
 }
 
@@ -386,6 +388,19 @@ int plan_contraction_impl( int64_t            num_loops,
     if(    tk.size() > 0 && runs_contiguous( tk, l_vk, l_vk )
         && all_multiple( rows, l_vk ) && all_multiple( tc, l_vk ) ) {
       return LOAD_VEC_K;
+    }
+    // fp32 runs of even length that are not multiples of 4 (odd mode sizes
+    // times 2, as in the einsum_benchmark MERA network): 8-byte vectors on
+    // the generic fp32 tiles
+    if( l_f32 && !l_cpx ) {
+      if(    rows.size() > 0 && runs_contiguous( rows, 2, 2 )
+          && all_multiple( tk, 2 ) && all_multiple( tc, 2 ) ) {
+        return LOAD_VEC8_MN;
+      }
+      if(    tk.size() > 0 && runs_contiguous( tk, 2, 2 )
+          && all_multiple( rows, 2 ) && all_multiple( tc, 2 ) ) {
+        return LOAD_VEC8_K;
+      }
     }
     return LOAD_SCALAR;
   };
@@ -985,6 +1000,7 @@ int launch_contraction( ContractionPlan const & plan,
   int64_t const l_esz = ( plan.dtype_in == ETIR_BF16 ) ? 2 : ( plan.dtype_in == ETIR_FP64 ? 8 : 4 );
   auto align_of = [&]( int32_t mode ) -> uintptr_t {
     if( mode == LOAD_VEC_K || mode == LOAD_VEC_MN ) return 16;
+    if( mode == LOAD_VEC8_K || mode == LOAD_VEC8_MN ) return 8;
     return uintptr_t( l_esz );
   };
   if( uintptr_t( a.a ) % align_of( l_ma ) != 0 ) l_ma = LOAD_SCALAR;

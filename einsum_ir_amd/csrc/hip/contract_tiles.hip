@@ -1,7 +1,8 @@
 // The generic contraction kernel of contract_kernel.h at its six tile shapes,
-// behind one dispatcher.  Each tile is instantiated for the nine pairs of
-// operand load modes, with and without an affine K offset; a workgroup has
-// one wave per (M, N) wave position.
+// behind one dispatcher.  Each tile is instantiated for every pair of operand
+// load modes (nine for bf16; 25 for fp32, whose tiles also take the 8-byte
+// vector modes), with and without an affine K offset; a workgroup has one
+// wave per (M, N) wave position.
 //
 //   tile                 dtype  BM   BN   BK  waves (M x N)  min waves per SIMD (launch bound)
 //   TILE_F32_128x128     fp32   128  128  32  4 x 2          1
@@ -23,7 +24,7 @@ namespace {
 template< int DT, int BM, int BN, int BK, int WM, int WN, int WPE >
 int launch_tile( int32_t ma, int32_t mb, bool kaff, ContractArgs const & a, uint32_t grid,
                  hipStream_t stream ) {
-  return with_load_modes( ma, mb, kaff, [&]( auto i_ma, auto i_mb, auto i_kaff ) {
+  return with_load_modes< DT == ETIR_FP32 >( ma, mb, kaff, [&]( auto i_ma, auto i_mb, auto i_kaff ) {
     hipLaunchKernelGGL( ( kern::contract_kernel< DT, BM, BN, BK, WM, WN, decltype( i_ma )::value,
                                                  decltype( i_mb )::value, decltype( i_kaff )::value, WPE > ),
                         dim3( grid ), dim3( 64 * WM * WN ), 0, stream, a );

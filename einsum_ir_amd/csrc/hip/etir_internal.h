@@ -161,16 +161,26 @@ int  launch_permute( PermutePlan const & plan,
 // Operand load modes of the contraction kernel.  "A" is the operand whose
 // dimension indexes the MFMA rows (kernel-M), "B" the MFMA columns (kernel-N).
 enum LoadMode : int32_t {
-  LOAD_SCALAR = 0,   // element gathers through the offset tables
-  LOAD_VEC_MN = 1,   // 16-byte vectors along the operand's M (or N) index
-  LOAD_VEC_K  = 2    // 16-byte vectors along K
+  LOAD_SCALAR  = 0,  // element gathers through the offset tables
+  LOAD_VEC_MN  = 1,  // 16-byte vectors along the operand's M (or N) index
+  LOAD_VEC_K   = 2,  // 16-byte vectors along K
+  LOAD_VEC8_MN = 3,  // 8-byte vectors along M (or N): fp32 runs of even length
+  LOAD_VEC8_K  = 4   // 8-byte vectors along K (generic fp32 tiles only)
 };
+
+// LDS layout of a load mode: [k][row] for the M/N vector modes, [row][k]
+// otherwise
+constexpr int32_t lds_layout( int32_t mode ) {
+  return ( mode == LOAD_VEC_MN || mode == LOAD_VEC8_MN ) ? LOAD_VEC_MN
+       : ( mode == LOAD_VEC8_K ) ? LOAD_VEC_K : mode;
+}
 
 // Calls fn( MA, MB, KAFF ) with std::integral_constant arguments equal to the
 // run-time operand load modes and affine-K flag, so that a launcher names its
 // kernel template once and every mode combination is instantiated from it.
-// Unknown modes fail with ETIR_COMPILATION_FAILED.
-template< class Fn >
+// The 8-byte modes are instantiated only where VEC8 is set.  Unknown modes
+// fail with ETIR_COMPILATION_FAILED.
+template< bool VEC8 = false, class Fn >
 int with_load_modes( int32_t ma, int32_t mb, bool kaff, Fn && fn ) {
   auto pick_k = [&]( auto i_ma, auto i_mb ) -> int {
     if( kaff ) return fn( i_ma, i_mb, std::true_type() );
@@ -181,15 +191,25 @@ int with_load_modes( int32_t ma, int32_t mb, bool kaff, Fn && fn ) {
       case LOAD_SCALAR: return pick_k( i_ma, std::integral_constant< int32_t, LOAD_SCALAR >() );
       case LOAD_VEC_MN: return pick_k( i_ma, std::integral_constant< int32_t, LOAD_VEC_MN >() );
       case LOAD_VEC_K:  return pick_k( i_ma, std::integral_constant< int32_t, LOAD_VEC_K >() );
-      default: return fail( ETIR_COMPILATION_FAILED, "contraction: unknown load mode of operand B" );
+      default: break;
     }
+    if constexpr( VEC8 ) {
+      if( mb == LOAD_VEC8_MN ) return pick_k( i_ma, std::integral_constant< int32_t, LOAD_VEC8_MN >() );
+      if( mb == LOAD_VEC8_K )  return pick_k( i_ma, std::integral_constant< int32_t, LOAD_VEC8_K >() );
+    }
+    return fail( ETIR_COMPILATION_FAILED, "contraction: unknown load mode of operand B" );
   };
   switch( ma ) {
     case LOAD_SCALAR: return pick_b( std::integral_constant< int32_t, LOAD_SCALAR >() );
     case LOAD_VEC_MN: return pick_b( std::integral_constant< int32_t, LOAD_VEC_MN >() );
     case LOAD_VEC_K:  return pick_b( std::integral_constant< int32_t, LOAD_VEC_K >() );
-    default: return fail( ETIR_COMPILATION_FAILED, "contraction: unknown load mode of operand A" );
+    default: break;
   }
+  if constexpr( VEC8 ) {
+    if( ma == LOAD_VEC8_MN ) return pick_b( std::integral_constant< int32_t, LOAD_VEC8_MN >() );
+    if( ma == LOAD_VEC8_K )  return pick_b( std::integral_constant< int32_t, LOAD_VEC8_K >() );
+  }
+  return fail( ETIR_COMPILATION_FAILED, "contraction: unknown load mode of operand A" );
 }
 
 enum TileCfg : int32_t {

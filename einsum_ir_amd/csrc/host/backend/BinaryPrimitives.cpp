@@ -362,6 +362,14 @@ einsum_ir::err_t einsum_ir::backend::BinaryPrimitives::reorder_gpu( bool        
     bool l_mn_inner = ( l_s != l_col_side );
     if( l_mn_inner && l_ext_mn[l_s] % i_vec != 0 && l_ext_k % i_vec == 0 ) l_mn_inner = false;
     if( !l_mn_inner && l_ext_k % i_vec != 0 && l_ext_mn[l_s] % i_vec == 0 ) l_mn_inner = true;
+    // neither way gives 16-byte vectors: fp32 takes 8-byte ones along an even
+    // run, K first (einsum_benchmark MERA root, M = 3^11, K = 50: 74 us with
+    // 8-byte K vectors, 102 with the odd M run gathered; its M = 810, N =
+    // 12474, K = 154 node: 47 us either way, 94 gathered)
+    if( i_bytes_per_element == 4 && l_ext_mn[l_s] % i_vec != 0 && l_ext_k % i_vec != 0 ) {
+      if( l_ext_k % 2 == 0 )              l_mn_inner = false;
+      else if( l_ext_mn[l_s] % 2 == 0 )   l_mn_inner = true;
+    }
 
     std::vector< int64_t > l_c, l_mn, l_x;
     for( dim_t l_ty : { dim_t::C, l_own[l_s] } ) {
