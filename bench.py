@@ -376,6 +376,11 @@ def _expression_rate(torch, stream, expr, sizes_arg, path_arg, steps, warmup, se
     data = harness.scaled_randn(torch, ins, out, sizes, seed, torch.float32)
     dout = torch.empty([sizes[d] for d in out], device="cuda", dtype=torch.float32)
     e = host.Expression(expr, sizes, path, data + [dout], stream=stream)
+    if steps is None:
+        # as many evaluations as fill about 0.1 s (3 to 50): a short tree
+        # needs several in flight for the host to enqueue ahead of the GPU
+        _, per = time_launches(torch, stream, e.eval_async, 1, warmup)
+        steps, warmup = max(3, min(50, int(0.1 / max(per, 1e-6)))), 0
     _, per = time_launches(torch, stream, e.eval_async, steps, warmup)
     n = e.num_ops()
     e.close()
@@ -401,7 +406,7 @@ def bench_samples(torch, eir, stream):
                 min=[round(lo[0], 1), lo[1]], max=[round(hi[0], 1), hi[1]])
     nets = {}
     for name, c in fx["einsum_benchmark"].items():
-        n, per = _expression_rate(torch, stream, c["expr"], c["sizes"], c["path"], 3, 1, 11)
+        n, per = _expression_rate(torch, stream, c["expr"], c["sizes"], c["path"], None, 1, 11)
         nets[name] = dict(gflop=round(n * 1e-9, 2), ms_per_eval=round(per * 1e3, 3),
                           value=round(n / per * 1e-9, 1), unit="GFLOP/s",
                           frac_fp32_peak=round(n / per * 1e-12 / PEAK_FP32_TFLOPS, 4))

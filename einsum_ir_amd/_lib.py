@@ -65,6 +65,10 @@ _HIP_SIGS = {
     "etir_hip_graph_abort": (ctypes.c_int, [ctypes.c_void_p]),
     "etir_hip_graph_launch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "etir_hip_graph_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+    "etir_hip_event_create": (ctypes.c_int, [ctypes.POINTER(ctypes.c_void_p)]),
+    "etir_hip_event_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+    "etir_hip_event_record": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
+    "etir_hip_stream_wait_event": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
 }
 
 _lib_hip = None

@@ -268,6 +268,33 @@ int etir_hip_stream_destroy( void * stream ) {
   return ETIR_SUCCESS;
 }
 
+int etir_hip_event_create( void ** event ) {
+  if( event == nullptr ) return fail( ETIR_UNDEFINED_ERROR, "event_create: invalid arguments" );
+  *event = nullptr;
+  hipEvent_t l_ev = nullptr;
+  ETIR_HIP_CHECK( hipEventCreateWithFlags( &l_ev, hipEventDisableTiming ) );
+  *event = l_ev;
+  return ETIR_SUCCESS;
+}
+
+int etir_hip_event_destroy( void * event ) {
+  if( event == nullptr ) return ETIR_SUCCESS;
+  ETIR_HIP_CHECK( hipEventDestroy( reinterpret_cast< hipEvent_t >( event ) ) );
+  return ETIR_SUCCESS;
+}
+
+int etir_hip_event_record( void * event, void * stream ) {
+  if( event == nullptr ) return fail( ETIR_UNDEFINED_ERROR, "event_record: invalid arguments" );
+  ETIR_HIP_CHECK( hipEventRecord( reinterpret_cast< hipEvent_t >( event ), reinterpret_cast< hipStream_t >( stream ) ) );
+  return ETIR_SUCCESS;
+}
+
+int etir_hip_stream_wait_event( void * stream, void * event ) {
+  if( event == nullptr ) return fail( ETIR_UNDEFINED_ERROR, "stream_wait_event: invalid arguments" );
+  ETIR_HIP_CHECK( hipStreamWaitEvent( reinterpret_cast< hipStream_t >( stream ), reinterpret_cast< hipEvent_t >( event ), 0 ) );
+  return ETIR_SUCCESS;
+}
+
 int etir_hip_graph_begin( void * stream ) {
   if( stream == nullptr ) return fail( ETIR_UNDEFINED_ERROR, "graph_begin: the null stream cannot be recorded" );
   ETIR_HIP_CHECK( hipStreamBeginCapture( reinterpret_cast< hipStream_t >( stream ),

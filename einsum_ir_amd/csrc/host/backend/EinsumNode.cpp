@@ -18,6 +18,7 @@
 #include "einsum_ir_hip.h"
 #include <algorithm>
 #include <cstdio>
+#include <functional>
 #include <cstdlib>
 #include <cstring>
 
@@ -30,6 +31,12 @@ namespace {
 }
 
 einsum_ir::backend::EinsumNode::~EinsumNode() {
+  // this node's own share of the schedule (the subtree's nodes free theirs)
+  for( void * l_s : m_pool ) etir_hip_synchronize( l_s );
+  etir_hip_event_destroy( m_ev_fork );
+  etir_hip_event_destroy( m_ev_done );
+  delete m_fork_memory;
+  for( void * l_s : m_pool ) etir_hip_stream_destroy( l_s );
   delete m_unary;
   delete m_cont;
   if( m_data_ptr_int != nullptr ) {
@@ -144,8 +151,160 @@ einsum_ir::err_t einsum_ir::backend::EinsumNode::compile() {
   err_t l_err = compile_recursive();
   if( l_err != err_t::SUCCESS ) return l_err;
   if( m_memory == nullptr ) return err_t::UNDEFINED_ERROR;
+  release_schedule();
+  l_err = schedule_streams();
+  if( l_err != err_t::SUCCESS ) return l_err;
   compile_memory_usage();
-  return m_memory->alloc_all_memory();
+  l_err = m_memory->alloc_all_memory();
+  if( l_err != err_t::SUCCESS ) return l_err;
+  return alloc_fork_memory();
+}
+
+void einsum_ir::backend::EinsumNode::assign( void * i_stream, MemoryManager * i_memory ) {
+  m_stream = i_stream;
+  m_memory = i_memory;
+  if( m_cont != nullptr ) static_cast< BinaryContractionHip * >( m_cont )->set_stream( i_stream );
+  if( m_unary != nullptr ) static_cast< UnaryHip * >( m_unary )->set_stream( i_stream );
+  for( EinsumNode * l_ch : m_children ) l_ch->assign( i_stream, i_memory );
+}
+
+double einsum_ir::backend::EinsumNode::est_node_us() const {
+  // per kernel: 5 us of launch and latency, then the longer of its flops at
+  // 60 TFLOP/s and its tensors' bytes at 3 TB/s (a rough order, used only to
+  // place subtrees)
+  if( m_children.size() == 2 ) {
+    double const l_bytes = double( m_size + m_children[0]->m_size + m_children[1]->m_size );
+    return 5.0 + std::max( double( m_num_ops_node ) / 60.0e6, l_bytes / 3.0e6 );
+  }
+  return has_work() ? 5.0 + 2.0 * double( m_size ) / 3.0e6 : 0.0;
+}
+
+double einsum_ir::backend::EinsumNode::est_subtree_us() const {
+  double l_t = est_node_us();
+  for( EinsumNode const * l_ch : m_children ) l_t += l_ch->est_subtree_us();
+  return l_t;
+}
+
+bool einsum_ir::backend::EinsumNode::has_work() const {
+  if( !m_children.empty() ) return true;
+  // a leaf: the copy into its internal layout (see eval_async)
+  return !m_data_locked && m_data_ptr_ext != nullptr && m_req_mem != 0;
+}
+
+einsum_ir::err_t einsum_ir::backend::EinsumNode::schedule_streams() {
+  assign( m_stream, m_memory );
+  // streams in the pool: at most this many forked subtrees run at once
+  // (three: with the tree's stream, the four hardware queues a process gets
+  // by default; more streams share queues and serialise behind each other's
+  // waits -- einsum_benchmark MERA 0.53 ms/eval with 3 or 4, 0.56 with 5 or 6)
+  int64_t l_max = 3;
+  if( char const * l_env = std::getenv( "ETIR_TREE_STREAMS" ) ) l_max = std::max( 0, std::atoi( l_env ) );
+  // a forked subtree's arena is its own: no fork above this peak
+  int64_t const l_mem_max = int64_t( 1 ) << 30;
+
+  // Depth first, in enqueue order, with estimated times (est_node_us): at a
+  // binary node whose children both enqueue work, the child whose subtree
+  // takes less time is forked onto the pool stream whose enqueued work ends
+  // first (a new one while the pool has room), unless waiting for that
+  // stream would take as long as running the other child first.  A stream is
+  // not taken while a subtree enqueued on it is being scheduled; once that
+  // subtree is placed, later forks may queue behind it.
+  std::vector< void * > l_str = { m_stream };   // slot 0: the tree's stream
+  std::vector< double > l_end = { 0.0 };        // estimated end of each slot's work
+  std::vector< char >   l_busy = { 1 };
+  err_t l_err = err_t::SUCCESS;
+  std::function< double( EinsumNode *, std::size_t, double ) > l_sched =
+    [&]( EinsumNode * i_n, std::size_t i_slot, double i_t ) -> double {
+    double const l_own = i_n->est_node_us();
+    int64_t l_p = -1;
+    EinsumNode * l_f = nullptr;
+    EinsumNode * l_o = nullptr;
+    if( i_n->m_children.size() == 2 ) {
+      EinsumNode * l_a = i_n->m_children[0];
+      EinsumNode * l_b = i_n->m_children[1];
+      bool const l_a_light = l_a->est_subtree_us() <= l_b->est_subtree_us();
+      l_f = l_a_light ? l_a : l_b;
+      l_o = l_a_light ? l_b : l_a;
+      // a fork costs two event records and two waits: only subtrees that run
+      // long enough to hide them (synthetic einsum_benchmark tree, one 6 us
+      // node forked: 95.5 -> 98.5 us/eval)
+      if(    l_f->has_work() && l_o->has_work() && l_f->m_mem_subtree <= l_mem_max
+          && l_f->est_subtree_us() >= 10.0 ) {
+        double l_best = 0.0;
+        for( std::size_t l_k = 1; l_k < l_str.size(); l_k++ ) {
+          if( !l_busy[l_k] && ( l_p < 0 || l_end[l_k] < l_best ) ) {
+            l_p = (int64_t) l_k;
+            l_best = l_end[l_k];
+          }
+        }
+        if( ( l_p < 0 || l_best > i_t ) && (int64_t) l_str.size() - 1 < l_max ) {
+          void * l_new = nullptr;
+          if( etir_hip_stream_create( &l_new ) != ETIR_SUCCESS ) {
+            l_err = err_t::UNDEFINED_ERROR;
+            return i_t;
+          }
+          m_pool.push_back( l_new );
+          l_str.push_back( l_new );
+          l_end.push_back( 0.0 );
+          l_busy.push_back( 0 );
+          l_p = (int64_t) l_str.size() - 1;
+          l_best = 0.0;
+        }
+        if( l_p >= 0 && std::max( i_t, l_best ) - i_t >= l_o->est_subtree_us() ) l_p = -1;
+      }
+    }
+    if( l_p < 0 ) {
+      double l_t = i_t;
+      for( std::size_t l_c = 0; l_c < i_n->m_children.size(); l_c++ ) {
+        l_t = l_sched( i_n->m_children[ i_n->m_exec_order[l_c] ], i_slot, l_t );
+      }
+      return l_t + l_own;
+    }
+    if(    etir_hip_event_create( &l_f->m_ev_fork ) != ETIR_SUCCESS
+        || etir_hip_event_create( &l_f->m_ev_done ) != ETIR_SUCCESS ) {
+      l_err = err_t::UNDEFINED_ERROR;
+      return i_t;
+    }
+    l_f->m_forked = true;
+    l_f->m_fork_memory = new MemoryManager();
+    l_f->m_fork_memory->share_allocator( *m_memory );
+    l_f->assign( l_str[l_p], l_f->m_fork_memory );
+    l_busy[l_p] = 1;
+    double const l_tf = l_sched( l_f, (std::size_t) l_p, std::max( i_t, l_end[l_p] ) );
+    l_busy[l_p] = 0;
+    l_end[l_p] = l_tf;
+    double const l_to = l_sched( l_o, i_slot, i_t );
+    return std::max( l_tf, l_to ) + l_own;
+  };
+  l_sched( this, 0, 0.0 );
+  return l_err;
+}
+
+void einsum_ir::backend::EinsumNode::release_schedule() {
+  // nothing may still run on the pool when the arenas go
+  for( void * l_s : m_pool ) etir_hip_synchronize( l_s );
+  for( EinsumNode * l_ch : m_children ) l_ch->release_schedule();
+  etir_hip_event_destroy( m_ev_fork );
+  etir_hip_event_destroy( m_ev_done );
+  m_ev_fork = nullptr;
+  m_ev_done = nullptr;
+  delete m_fork_memory;
+  m_fork_memory = nullptr;
+  m_forked = false;
+  for( void * l_s : m_pool ) etir_hip_stream_destroy( l_s );
+  m_pool.clear();
+}
+
+einsum_ir::err_t einsum_ir::backend::EinsumNode::alloc_fork_memory() {
+  if( m_fork_memory != nullptr ) {
+    err_t l_err = m_fork_memory->alloc_all_memory();
+    if( l_err != err_t::SUCCESS ) return l_err;
+  }
+  for( EinsumNode * l_ch : m_children ) {
+    err_t l_err = l_ch->alloc_fork_memory();
+    if( l_err != err_t::SUCCESS ) return l_err;
+  }
+  return err_t::SUCCESS;
 }
 
 einsum_ir::err_t einsum_ir::backend::EinsumNode::compile_recursive() {
@@ -384,10 +543,53 @@ einsum_ir::err_t einsum_ir::backend::EinsumNode::unlock_data() {
 }
 
 einsum_ir::err_t einsum_ir::backend::EinsumNode::eval_async() {
+  return eval_tree( true );
+}
+
+einsum_ir::err_t einsum_ir::backend::EinsumNode::eval_one_stream_async() {
+  kernels_on( m_stream );
+  err_t const l_err = eval_tree( false );
+  kernels_on( nullptr );
+  return l_err;
+}
+
+void einsum_ir::backend::EinsumNode::kernels_on( void * i_stream ) {
+  void * l_s = ( i_stream != nullptr ) ? i_stream : m_stream;
+  if( m_cont != nullptr ) static_cast< BinaryContractionHip * >( m_cont )->set_stream( l_s );
+  if( m_unary != nullptr ) static_cast< UnaryHip * >( m_unary )->set_stream( l_s );
+  for( EinsumNode * l_ch : m_children ) l_ch->kernels_on( i_stream );
+}
+
+einsum_ir::err_t einsum_ir::backend::EinsumNode::eval_tree( bool i_forks ) {
   if( !m_compiled ) return err_t::CALLED_BEFORE_COMPILATION;
+  // forked children first, each on its own stream from this point of this
+  // node's stream on; then the others on this stream; then this stream waits
+  // for the forked ones
+  auto forked = [i_forks]( EinsumNode const * i_c ) { return i_forks && i_c->m_forked && i_c->has_work(); };
+  bool l_joins = false;
   for( std::size_t l_ch = 0; l_ch < m_children.size(); l_ch++ ) {
-    err_t l_err = m_children[ m_exec_order[l_ch] ]->eval_async();
+    EinsumNode * l_c = m_children[ m_exec_order[l_ch] ];
+    if( !forked( l_c ) ) continue;
+    if(    etir_hip_event_record( l_c->m_ev_fork, m_stream ) != ETIR_SUCCESS
+        || etir_hip_stream_wait_event( l_c->m_stream, l_c->m_ev_fork ) != ETIR_SUCCESS ) {
+      return err_t::UNDEFINED_ERROR;
+    }
+    err_t l_err = l_c->eval_tree( i_forks );
     if( l_err != err_t::SUCCESS ) return l_err;
+    if( etir_hip_event_record( l_c->m_ev_done, l_c->m_stream ) != ETIR_SUCCESS ) return err_t::UNDEFINED_ERROR;
+    l_joins = true;
+  }
+  for( std::size_t l_ch = 0; l_ch < m_children.size(); l_ch++ ) {
+    EinsumNode * l_c = m_children[ m_exec_order[l_ch] ];
+    if( forked( l_c ) ) continue;
+    err_t l_err = l_c->eval_tree( i_forks );
+    if( l_err != err_t::SUCCESS ) return l_err;
+  }
+  if( l_joins ) {
+    for( EinsumNode * l_c : m_children ) {
+      if( !forked( l_c ) ) continue;
+      if( etir_hip_stream_wait_event( m_stream, l_c->m_ev_done ) != ETIR_SUCCESS ) return err_t::UNDEFINED_ERROR;
+    }
   }
 
   if( m_data_locked ) {

@@ -89,6 +89,20 @@ class einsum_ir::backend::EinsumNode {
     //! HIP stream of the whole tree (hipStream_t as void*, nullptr = null stream)
     void * m_stream = nullptr;
 
+    //! Concurrent evaluation of independent subtrees, set up by compile() on
+    //! the node it is called on (the root).  A forked node's subtree runs on
+    //! its own stream (m_stream, one of the root's pool) from m_ev_fork,
+    //! recorded on the parent's stream, to m_ev_done, which the parent's
+    //! stream waits for before the parent's kernels; its intermediates live
+    //! in an arena of their own (m_fork_memory), as the subtree runs while
+    //! its sibling's does.
+    bool m_forked = false;
+    void * m_ev_fork = nullptr;
+    void * m_ev_done = nullptr;
+    MemoryManager * m_fork_memory = nullptr;
+    //! the root's pool of streams for forked subtrees (owned by the root)
+    std::vector< void * > m_pool;
+
     //! complex trees: id of the complex dim of this node's contraction (-1:
     //! the contraction's default, the first C dim of the output)
     int64_t m_cpx_dim_id = -1;
@@ -171,8 +185,41 @@ class einsum_ir::backend::EinsumNode {
     /** Enqueues the evaluation of the tree on the stream without waiting. **/
     err_t eval_async();
 
+    /** eval_async() with every kernel on this node's stream, in the order of
+        the one-stream evaluation (forked subtrees keep their arenas); for
+        recording the tree as a graph. **/
+    err_t eval_one_stream_async();
+
+    /** Enqueues the subtree; i_forks: forked subtrees on their streams. **/
+    err_t eval_tree( bool i_forks );
+
+    /** Kernels of the subtree on i_stream (nullptr: each node's own stream). **/
+    void kernels_on( void * i_stream );
+
     /** Sets the stream of this node and its subtree (before compile()). **/
     void set_stream( void * i_stream );
+
+    /** Puts this node's subtree on a stream and an arena (its kernels included). **/
+    void assign( void * i_stream, MemoryManager * i_memory );
+
+    /** Chooses the subtrees that run concurrently and sets up their streams,
+        events and arenas (root only, after compile_recursive). **/
+    err_t schedule_streams();
+
+    /** Frees what schedule_streams() set up in this subtree. **/
+    void release_schedule();
+
+    /** Allocates the arenas of the forked subtrees below this node. **/
+    err_t alloc_fork_memory();
+
+    /** True if evaluating this node enqueues work on the GPU. **/
+    bool has_work() const;
+
+    /** Rough run time of this node's own kernel (us), to place subtrees. **/
+    double est_node_us() const;
+
+    /** Rough run time of the subtree on one stream (us). **/
+    double est_subtree_us() const;
 
     int64_t num_ops( bool i_children = true );
 

@@ -86,6 +86,12 @@ class einsum_ir::backend::MemoryManager {
       m_free  = i_free;
     }
 
+    /** Takes the allocator of another manager (an arena planned beside it). **/
+    void share_allocator( MemoryManager const & i_other ) {
+      m_alloc = i_other.m_alloc;
+      m_free  = i_other.m_free;
+    }
+
     /** Bytes of the current device allocation (0 before alloc_all_memory). **/
     int64_t get_allocated_memory() const { return m_arena_bytes; }
 };

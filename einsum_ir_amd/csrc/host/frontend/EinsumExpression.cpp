@@ -227,7 +227,9 @@ einsum_ir::err_t einsum_ir::frontend::EinsumExpression::eval_graph_async() {
     // through temporary device copies) cannot take part
     if( m_nodes.back().has_host_ext() ) return err_t::NO_DATA_PTR_PROVIDED;
     if( etir_hip_graph_begin( m_stream ) != ETIR_SUCCESS ) return err_t::UNDEFINED_ERROR;
-    err_t l_err = m_nodes.back().eval_async();
+    // recorded on the one stream: a recording that followed the forked
+    // subtrees onto their streams ended in a crash of the host process
+    err_t l_err = m_nodes.back().eval_one_stream_async();
     if( l_err != err_t::SUCCESS ) {
       etir_hip_graph_abort( m_stream );
       return l_err;

@@ -262,6 +262,20 @@ int etir_hip_graph_abort( void * stream );
 int etir_hip_graph_launch( etir_graph_t graph, void * stream );
 int etir_hip_graph_destroy( etir_graph_t graph );
 
+/* Events for concurrent tree evaluation.  No counterpart in the reference,
+ * whose tree evaluates node after node (reference
+ * src/backend/EinsumNode.cpp:496-540): EinsumNode runs an independent subtree
+ * on a stream of its own, started after an event recorded on its parent's
+ * stream and joined back through an event recorded at its end.
+ *   etir_hip_event_create       an event without timing data
+ *   etir_hip_event_record       records it on `stream` (NULL: the null stream)
+ *   etir_hip_stream_wait_event  makes work enqueued later on `stream` wait
+ *                               for the event's last recording */
+int etir_hip_event_create( void ** event );
+int etir_hip_event_destroy( void * event );
+int etir_hip_event_record( void * event, void * stream );
+int etir_hip_stream_wait_event( void * stream, void * event );
+
 #ifdef __cplusplus
 }
 #endif
