@@ -45,6 +45,7 @@ int launch_contract_kwave( int32_t waves, int32_t kw, ContractArgs const & a, ui
                            hipStream_t stream );
 int launch_contract_f32_dma( int32_t ma, int32_t mb, ContractArgs const & a, uint32_t grid, hipStream_t stream );
 int launch_contract_gemv( bool bf16_in, ContractArgs const & a, hipStream_t stream );
+int launch_contract_skinny( bool bf16_in, ContractArgs const & a, hipStream_t stream );
 
 namespace {
 
@@ -160,6 +161,7 @@ char const * tile_str( int32_t t ) {
     case TILE_F32_KWAVE_32x32: return "f32_kwave_32x32";
     case TILE_F32_DMA_128x128: return "f32_dma_128x128x32";
     case TILE_GEMV:            return "gemv";
+    case TILE_SKINNY:          return "skinny";
     default:                return "?";
   }
 }
@@ -537,6 +539,36 @@ int plan_contraction_impl( int64_t            num_loops,
     if( l_mv_ok || l_forced ) plan.tile = TILE_GEMV;
   }
 
+  // ------------------------------------------------- one short free side
+  // A free side of 2 to 64 pads most of every MFMA tile, and with a short K
+  // the tiles are bound by their load round trip and stores: one thread per
+  // index of the long side instead, the short side's outputs in registers
+  // (einsum_benchmark MERA, M = 11, N = 415800, K = 24: 28 us on 64 x 64
+  // tiles).  Where the short side is 17-64, only with K <= 64 (the FMAs per
+  // long-operand byte grow with the short side); at least 256 workgroups of
+  // 256 threads.  ETIR_TILE=14 forces it for any short side of 2 to 64.
+  {
+    int64_t const l_sh = std::min( l_kern_m, l_kern_n );
+    int64_t const l_lo = std::max( l_kern_m, l_kern_n );
+    bool const l_sk_shape = ( l_f32 || l_bf16 ) && !l_cpx && plan.tile != TILE_GEMV && l_sh >= 2 && l_sh <= 64
+                         && l_size_c <= 65535;
+    char const * l_env_t = std::getenv( "ETIR_TILE" );
+    bool const l_forced = l_sk_shape && l_env_t != nullptr && std::atoi( l_env_t ) == TILE_SKINNY;
+    // not where the output's unit-stride dim is a C dim: a thread's stores
+    // would then be C elements apart (TCCG efbadx,cfx->abcdex: 2.3 against
+    // 7.8 TFLOP/s on the tiles, which walk C fastest there)
+    int64_t l_os_c = std::numeric_limits< int64_t >::max();
+    int64_t l_os_mn = std::numeric_limits< int64_t >::max();
+    for( Loop const & l_x : l_c ) if( l_x.size > 1 ) l_os_c = std::min( l_os_c, l_x.s[T_OUT] );
+    for( auto const * l_set : { &l_m, &l_n } ) {
+      for( Loop const & l_x : *l_set ) if( l_x.size > 1 ) l_os_mn = std::min( l_os_mn, l_x.s[T_OUT] );
+    }
+    bool const l_sk_ok = l_sk_shape && ( l_sh <= 16 || l_size_k <= 64 ) && l_os_mn < l_os_c
+                      && l_size_c * ( ( l_lo + 255 ) / 256 ) >= l_cus && l_env_t == nullptr
+                      && std::getenv( "ETIR_NO_SKINNY" ) == nullptr;
+    if( l_sk_ok || l_forced ) plan.tile = TILE_SKINNY;
+  }
+
   // ------------------------------------------- long K on few large tiles
   // The 64 x 64 tile fills the chip where fewer than 256 of the 128 x 128
   // tiles exist, but runs at about half the fp32 direct-to-LDS kernel's rate;
@@ -561,7 +593,7 @@ int plan_contraction_impl( int64_t            num_loops,
   // 90 on split K)
   {
     int64_t const l_t32 = n_tiles( TILE_F32_KWAVE_32x32 );
-    bool const l_kw_ok = l_f32 && plan.tile != TILE_GEMV && plan.mode_a == LOAD_VEC_K && plan.mode_b == LOAD_VEC_K && l_k_affine
+    bool const l_kw_ok = l_f32 && plan.tile != TILE_GEMV && plan.tile != TILE_SKINNY && plan.mode_a == LOAD_VEC_K && plan.mode_b == LOAD_VEC_K && l_k_affine
                       && l_sk_a == 1 && l_sk_b == 1 && l_size_k % 16 == 0 && l_size_k >= 256
                       && l_size_k <= 4096 && n_tiles( plan.tile ) < l_cus && l_t32 >= l_cus / 2
                       && l_t32 <= 2 * l_cus
@@ -585,7 +617,7 @@ int plan_contraction_impl( int64_t            num_loops,
   // of them factored if needed) become C loops of a partial contraction that
   // writes one workspace slice per split, and split_reduce sums the slices.
   if( allow_split && !l_f64 && !l_cpx && l_size_k >= 512 && plan.tile != TILE_F32_KWAVE_32x32
-      && plan.tile != TILE_GEMV ) {
+      && plan.tile != TILE_GEMV && plan.tile != TILE_SKINNY ) {
     int64_t const l_tiles = n_tiles( plan.tile );
     if( l_tiles > 0 && l_tiles < l_cus ) {
       // at least 128 k per split; aim for two workgroups per CU
@@ -884,6 +916,15 @@ int plan_contraction_impl( int64_t            num_loops,
                 && a.sn_out == 1 && all_multiple( l_tc_b, 4 ) && all_multiple( l_tk_b, 4 )
                 && all_multiple( l_tc_out, 4 ) && all_multiple( l_tm_out, 4 ) ) ? 1 : 0;
   if( a.gemv_v4 ) plan.desc += " v4";
+  {
+    bool const l_short_a = l_kern_m <= l_kern_n;
+    std::vector< int64_t > const & l_tl = l_short_a ? l_tn_b : l_tm_a;
+    std::vector< int64_t > const & l_tcl = l_short_a ? l_tc_b : l_tc_a;
+    int64_t const l_skl = l_short_a ? l_sk_b : l_sk_a;
+    a.skinny_kvec = ( plan.tile == TILE_SKINNY && l_k_affine && ( l_size_k <= 1 || l_skl == 1 ) && l_size_k % 4 == 0
+                      && all_multiple( l_tl, 4 ) && all_multiple( l_tcl, 4 ) ) ? 1 : 0;
+    if( a.skinny_kvec ) plan.desc += " kvec";
+  }
   if( l_cpx ) {
     a.cpx_a   = l_x[0].s[l_sa];
     a.cpx_b   = l_x[0].s[l_sb];
@@ -1052,6 +1093,9 @@ int launch_contraction( ContractionPlan const & plan,
       break;
     case TILE_GEMV:
       l_err = launch_contract_gemv( plan.dtype_in == ETIR_BF16, a, stream );
+      break;
+    case TILE_SKINNY:
+      l_err = launch_contract_skinny( plan.dtype_in == ETIR_BF16, a, stream );
       break;
     default: return fail( ETIR_COMPILATION_FAILED, "contraction: unknown tile configuration" );
   }

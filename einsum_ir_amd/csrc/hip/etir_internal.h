@@ -226,7 +226,8 @@ enum TileCfg : int32_t {
   TILE_CPX_F64_64x64    = 10,
   TILE_F32_KWAVE_32x32  = 11, // K split over the waves of one workgroup (contract_kwave.hip)
   TILE_F32_DMA_128x128  = 12, // fp32 direct-to-LDS kernel (contract_f32_dma.hip)
-  TILE_GEMV             = 13  // M == 1 or N == 1: one thread per output element (contract_gemv.hip)
+  TILE_GEMV             = 13, // M == 1 or N == 1: one thread per output element (contract_gemv.hip)
+  TILE_SKINNY           = 14  // one free side of 2-64: one thread per long index (contract_skinny.hip)
 };
 
 struct ContractArgs {
@@ -272,6 +273,10 @@ struct ContractArgs {
   // are unit-stride along N with every offset a multiple of 4 elements and
   // N % 4 == 0, so a thread takes 4 consecutive outputs with vector accesses
   int32_t gemv_v4;
+  // one-short-side kernel: the long operand is unit-stride along an affine
+  // K, every row offset a multiple of 4 elements and K % 4 == 0, so a thread
+  // reads its K range in 4-element vectors
+  int32_t skinny_kvec;
 };
 
 struct ContractionPlan {

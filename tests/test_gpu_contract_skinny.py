@@ -1,0 +1,109 @@
+"""GPU parity of the one-short-side kernel (tile "skinny": kernel M or N of 2
+to 64, one thread per index of the long side).  Checker: the CPU oracle (fp64
+accumulation) on the same seeded inputs; fp32 relative Frobenius <= 1e-5,
+bf16 inputs or output <= 2e-3."""
+import numpy as np
+import pytest
+
+import einsum_ir_amd as eir
+from tests.helpers import TOL_FP32, loops_for, parse_binary, rel_frobenius, tensor_numel
+from tests.test_gpu_contract import run_case
+
+pytestmark = pytest.mark.gpu
+
+# shapes the planner gives the kernel by itself
+DEFAULT_SHAPES = [
+    # short M, long operand K-contiguous: 16-byte vectors along K
+    ("mk,nk->mn", dict(m=11, k=24, n=70000), "kvec"),
+    # short N (the output's unit-stride side), long operand A K-contiguous
+    ("mk,nk->mn", dict(m=70000, k=40, n=9), "kvec"),
+    # long operand unit-stride along the long side: coalesced scalar loads
+    ("km,kn->mn", dict(k=11, m=5, n=80000), ""),
+    # short side 45 with K <= 64, the MERA shape
+    ("mk,kn->mn", dict(m=45, k=11, n=70000), ""),
+    # K over several 32-k chunks with a tail, K % 4 != 0: no vectors
+    ("mk,nk->mn", dict(m=16, k=102, n=70000), ""),
+    # a C dim (grid rows)
+    ("zmk,znk->zmn", dict(z=3, m=10, k=20, n=90000), "kvec"),
+    # two K dims in different orders: K offsets from the table
+    ("mlk,nkl->mn", dict(m=12, k=5, l=6, n=70000), ""),
+]
+
+
+@pytest.mark.parametrize("expr,sizes,flag", DEFAULT_SHAPES)
+def test_skinny_default(torch_cuda, oracle, monkeypatch, expr, sizes, flag):
+    monkeypatch.delenv("ETIR_TILE", raising=False)
+    _, desc = run_case(torch_cuda, oracle, expr, sizes, seed=sum(sizes.values()) % 1000)
+    assert "skinny" in desc, desc
+    assert (" kvec" in desc) == (flag == "kvec"), desc
+
+
+# shapes the planner leaves to the MFMA tiles, forced (ETIR_TILE=14): short
+# sides from 2 to 64, K up to several chunks, every SMAX instantiation
+FORCED_SHAPES = [
+    ("mk,nk->mn", dict(m=2, k=7, n=3000)),
+    ("mk,kn->mn", dict(m=30, k=300, n=1000)),
+    ("km,nk->mn", dict(k=65, m=64, n=2000)),
+    ("mk,nk->mn", dict(m=1500, k=33, n=24)),
+]
+
+
+@pytest.mark.parametrize("expr,sizes", FORCED_SHAPES)
+def test_skinny_forced(torch_cuda, oracle, monkeypatch, expr, sizes):
+    monkeypatch.setenv("ETIR_TILE", "14")
+    _, desc = run_case(torch_cuda, oracle, expr, sizes, seed=7)
+    assert "skinny" in desc, desc
+
+
+@pytest.mark.parametrize("first,last", [(eir.COPY, eir.RELU), (eir.ADD, eir.UNDEFINED_KTYPE),
+                                        (eir.UNDEFINED_KTYPE, eir.ADD), (eir.ZERO, eir.RELU)])
+def test_skinny_touch_kernels(torch_cuda, oracle, first, last):
+    _, desc = run_case(torch_cuda, oracle, "mk,nk->mn", dict(m=11, k=24, n=70000), first=first, last=last,
+                       seed=first + 5 * last)
+    assert "skinny" in desc, desc
+
+
+def test_skinny_bf16(torch_cuda, oracle):
+    _, desc = run_case(torch_cuda, oracle, "mk,nk->mn", dict(m=11, k=24, n=70000), dtype=eir.BF16, seed=3)
+    assert "skinny" in desc and "kvec" in desc, desc
+    _, desc = run_case(torch_cuda, oracle, "km,kn->mn", dict(k=11, m=5, n=80000), dtype=eir.BF16,
+                       dtype_out=eir.BF16, seed=4)
+    assert "skinny" in desc, desc
+
+
+def test_skinny_misaligned_long_operand(torch_cuda, oracle):
+    """The long operand one element off a 16-byte boundary: the launch reads
+    it element by element instead of in vectors, same result as aligned."""
+    torch = torch_cuda
+    expr, sizes = "mk,nk->mn", dict(m=11, k=24, n=70000)
+    left, right, out = parse_binary(expr)
+    loops = loops_for(expr, sizes)
+    rng = np.random.default_rng(9)
+    a = rng.uniform(-1, 1, tensor_numel(left, sizes)).astype(np.float32)
+    b = rng.uniform(-1, 1, tensor_numel(right, sizes)).astype(np.float32)
+    plan = eir.ContractionPlan(loops["dim_types"], loops["sizes"], loops["strides_left"],
+                               loops["strides_right"], loops["strides_out"])
+    desc = plan.describe()
+    assert "skinny" in desc and "kvec" in desc, desc
+    da = torch.from_numpy(a).cuda()
+    buf_b = torch.zeros(b.size + 1, device="cuda")
+    buf_b[1:] = torch.from_numpy(b).cuda()
+    db_al = torch.from_numpy(b).cuda()
+    o_mis = torch.zeros(tensor_numel(out, sizes), device="cuda")
+    o_al = torch.zeros_like(o_mis)
+    s = torch.cuda.current_stream()
+    plan.execute(da, buf_b[1:], o_mis, stream=s)
+    plan.execute(da, db_al, o_al, stream=s)
+    torch.cuda.synchronize()
+    plan.close()
+    assert torch.equal(o_mis, o_al), "vector and element loads sum differently"
+    ref = np.zeros(tensor_numel(out, sizes), dtype=np.float32)
+    oracle.contract(loops, a, b, ref)
+    assert rel_frobenius(ref, o_al.cpu().numpy()) <= TOL_FP32
+
+
+def test_skinny_switch_off(torch_cuda, oracle, monkeypatch):
+    """ETIR_NO_SKINNY leaves such shapes to the MFMA tiles (same results)."""
+    monkeypatch.setenv("ETIR_NO_SKINNY", "1")
+    _, desc = run_case(torch_cuda, oracle, "mk,nk->mn", dict(m=11, k=24, n=70000), seed=12)
+    assert "skinny" not in desc, desc
