@@ -51,6 +51,9 @@ def parse_args():
     p.add_argument("--no-mfma-ceiling", action="store_true",
                    help="skip the matrix-core rate and clock probe (einsum_ir_amd/bin/mfma_ceiling)")
     p.add_argument("--only", default="", help="comma list of configs to run (c1,c2,c3,c4,c5,mlp,samples)")
+    p.add_argument("--samples", default="",
+                   help="with samples: comma list of what to run (tccg and/or einsum_benchmark network names; "
+                        "default all)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also time a plain 512 MiB device copy (reference for the PMC byte counters)")
     p.add_argument("--settle", type=float, default=1.0,
@@ -114,14 +117,17 @@ def summarize_rocprof(dirs, timed, kernel_filter=""):
     the warm-up and then the timed steps) and over all of them.  Kernel
     durations come from run_kernel_trace.csv; counters from
     run_counter_collection.csv.  FETCH_SIZE / WRITE_SIZE (KiB per dispatch)
-    are scaled to bytes by what the same counter reads for the largest plain
-    device copy in the run (bench.py --calibrate-copy: 512 MiB each way)."""
+    are scaled to bytes by what the same counter reads for the run's first
+    plain device copy (bench.py --calibrate-copy: 512 MiB each way, before
+    any workload; later copies, such as the 1 GiB one of the permute rows,
+    are not the calibration)."""
     import glob
     import statistics
     pat = re.compile(kernel_filter) if kernel_filter else None
     out = []
     durations = {}
     counters = {}          # (kernel, grid) -> counter -> [values in dispatch order]
+    first_id = {}          # (kernel, grid) -> first dispatch id
     for d in dirs:
         for path in sorted(glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)):
             for r in _read_csv(path):
@@ -139,6 +145,7 @@ def summarize_rocprof(dirs, timed, kernel_filter=""):
             for k, cs in per.items():
                 for c, by_id in cs.items():
                     counters.setdefault(k, {})[c] = [by_id[i] for i in sorted(by_id)]
+                    first_id[k] = min(first_id.get(k, min(by_id)), min(by_id))
     if durations:
         out.append(f"# kernel durations (us): the last {timed} dispatches of each kernel and grid, and all of them")
         out.append(f"{'timed_avg':>10} {'timed_min':>10} {'timed_max':>10} {'all_avg':>10} {'calls':>6} "
@@ -156,10 +163,13 @@ def summarize_rocprof(dirs, timed, kernel_filter=""):
     if counters:
         scale = {}
         for c, expect_kib in (("FETCH_SIZE", 524288.0), ("WRITE_SIZE", 524288.0)):
-            copies = [(g, vals) for (n, g), cs in counters.items() for cc, vals in cs.items()
+            copies = [(first_id[(n, g)], vals) for (n, g), cs in counters.items() for cc, vals in cs.items()
                       if cc == c and "copyBuffer" in n]
             if copies:
-                g, vals = max(copies)
+                # the calibration's own dispatches come first (the copy kernel's
+                # grid does not depend on the size, so later copies share the group)
+                _, vals = min(copies, key=lambda x: x[0])
+                vals = vals[:5]
                 scale[c] = expect_kib / statistics.mean(vals)
                 out.append(f"# calibration: the 512 MiB device copy reads {c} = {statistics.mean(vals):.0f} KiB "
                            f"per dispatch; {c} is scaled by {scale[c]:.4f}")
@@ -387,25 +397,30 @@ def _expression_rate(torch, stream, expr, sizes_arg, path_arg, steps, warmup, se
     return n, per
 
 
-def bench_samples(torch, eir, stream):
+def bench_samples(torch, eir, stream, which=()):
     """The reference's sample workloads (tests/golden/einsum_samples.json):
     the 59 TCCG binary contractions and the four einsum_benchmark networks at
     full size, fp32, each through EinsumExpression along its recorded path.
     Rates use num_ops() (the reference harnesses' flop count)."""
     import math
     fx = json.load(open(os.path.join(ROOT, "tests", "golden", "einsum_samples.json")))
+    pick = lambda name: not which or name in which
     rates = []
-    for c in fx["tccg"]:
+    for c in (fx["tccg"] if pick("tccg") else []):
         n, per = _expression_rate(torch, stream, c["expr"], c["sizes"], c["path"], 10, 2,
                                   sum(map(ord, c["expr"])))
         rates.append((n / per * 1e-9, c["expr"]))
-    gm = math.exp(sum(math.log(r) for r, _ in rates) / len(rates))
-    lo, hi = min(rates), max(rates)
-    tccg = dict(cases=len(rates), unit="GFLOP/s", geomean=round(gm, 1),
-                frac_fp32_peak_geomean=round(gm / (PEAK_FP32_TFLOPS * 1e3), 4),
-                min=[round(lo[0], 1), lo[1]], max=[round(hi[0], 1), hi[1]])
+    tccg = None
+    if rates:
+        gm = math.exp(sum(math.log(r) for r, _ in rates) / len(rates))
+        lo, hi = min(rates), max(rates)
+        tccg = dict(cases=len(rates), unit="GFLOP/s", geomean=round(gm, 1),
+                    frac_fp32_peak_geomean=round(gm / (PEAK_FP32_TFLOPS * 1e3), 4),
+                    min=[round(lo[0], 1), lo[1]], max=[round(hi[0], 1), hi[1]])
     nets = {}
     for name, c in fx["einsum_benchmark"].items():
+        if not pick(name):
+            continue
         n, per = _expression_rate(torch, stream, c["expr"], c["sizes"], c["path"], None, 1, 11)
         nets[name] = dict(gflop=round(n * 1e-9, 2), ms_per_eval=round(per * 1e3, 3),
                           value=round(n / per * 1e-9, 1), unit="GFLOP/s",
@@ -704,8 +719,9 @@ def main():
         log(f"mlp: {mlp['per_launch']*1e6:.1f} us/eval")
 
     if run("samples"):
-        tccg, nets = bench_samples(torch, eir, stream)
-        extra["tccg_fp32"] = tccg
+        tccg, nets = bench_samples(torch, eir, stream, set(x for x in args.samples.split(",") if x))
+        if tccg is not None:
+            extra["tccg_fp32"] = tccg
         extra["einsum_benchmark_fp32"] = nets
         log(f"tccg: {tccg}")
         for name, r in nets.items():
