@@ -96,8 +96,22 @@ __global__ __launch_bounds__( 256 ) void contract_gemv_kernel( ContractArgs a ) 
 #pragma unroll
     for( int l_i = 0; l_i < 8; l_i++ ) l_v = fmaf( l_x[l_i], l_y[l_i], l_v );
   }
-  for( ; l_k < a.K; l_k++ ) {
-    l_v = fmaf( gemv_ld< T >( l_pa, koff_a( l_k ) ), gemv_ld< T >( l_pb, koff_b( l_k ) ), l_v );
+  // the last partial chunk the same way: loads of clamped (existing) k all
+  // in flight together, FMAs only for the k inside K, still ascending (a
+  // rolled tail loop waited for each k's loads in turn: K = 11 meant four
+  // round trips instead of two)
+  if( l_k < a.K ) {
+    float l_x[8], l_y[8];
+#pragma unroll
+    for( int l_i = 0; l_i < 8; l_i++ ) {
+      int32_t const l_kc = min( l_k + l_i, a.K - 1 );
+      l_x[l_i] = gemv_ld< T >( l_pa, koff_a( l_kc ) );
+      l_y[l_i] = gemv_ld< T >( l_pb, koff_b( l_kc ) );
+    }
+#pragma unroll
+    for( int l_i = 0; l_i < 8; l_i++ ) {
+      if( l_k + l_i < a.K ) l_v = fmaf( l_x[l_i], l_y[l_i], l_v );
+    }
   }
 
   if( l_read_out ) l_v = l_old + l_v;
@@ -189,11 +203,23 @@ __global__ __launch_bounds__( 256 ) void contract_gemv4_kernel( ContractArgs a )
 #pragma unroll
       for( int l_i = 0; l_i < 4; l_i++ ) l_v[l_i] = fmaf( l_x[l_j], l_y[l_j][l_i], l_v[l_i] );
   }
-  for( ; l_k < a.K; l_k++ ) {
-    float const l_x = gemv_ld< T >( l_pa, koff_a( l_k ) );
-    f4 const l_y = ld4( koff_b( l_k ) );
+  if( l_k < a.K ) {
+    // the last partial chunk: clamped loads in flight together, as above
+    float l_x[8];
+    f4    l_y[8];
 #pragma unroll
-    for( int l_i = 0; l_i < 4; l_i++ ) l_v[l_i] = fmaf( l_x, l_y[l_i], l_v[l_i] );
+    for( int l_j = 0; l_j < 8; l_j++ ) {
+      int32_t const l_kc = min( l_k + l_j, a.K - 1 );
+      l_x[l_j] = gemv_ld< T >( l_pa, koff_a( l_kc ) );
+      l_y[l_j] = ld4( koff_b( l_kc ) );
+    }
+#pragma unroll
+    for( int l_j = 0; l_j < 8; l_j++ ) {
+      if( l_k + l_j < a.K ) {
+#pragma unroll
+        for( int l_i = 0; l_i < 4; l_i++ ) l_v[l_i] = fmaf( l_x[l_j], l_y[l_j][l_i], l_v[l_i] );
+      }
+    }
   }
 
   float l_r[4];
