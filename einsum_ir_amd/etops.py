@@ -23,10 +23,11 @@ Differences from the tpp backend, by design:
     picks tiles itself);
   * level-1 (packing) strides are accepted and ignored: the kernels stage
     tiles through LDS instead of packing buffers;
-  * ``optimize`` returns the configuration with the same loops (nothing to
-    hand back: the GPU planner's choices live in the compiled plan) and every
-    exec type ``prim``; tpp's optimisation keys are accepted (and have no
-    effect), unknown keys are rejected as in the reference;
+  * ``optimize`` returns the loops as the GPU planner runs them (size-1 loops
+    dropped, contiguous loops of one type fused; exec type ``shared`` for a
+    contraction's C loops, which form the grid, ``prim`` otherwise) and no
+    packing level; tpp's optimisation keys are accepted (and have no effect),
+    unknown keys are rejected as in the reference;
   * DataType has the additive member ``bfloat16`` (bf16 tensors, fp32
     accumulation).
 """
@@ -506,10 +507,13 @@ class backend:
 def optimize(config: TensorOperationConfig,
              optimization_config: Optional[Dict[str, Union[int, bool]]] = None) -> TensorOperationConfig:
     """Optimizes a configuration (reference etops/__init__.py:436-514,
-    TensorOperation.cpp:486-604).  On the HIP backend the loops are returned
-    as given with every exec type ``prim``: the whole operation is one kernel
-    grid and the planner chooses fusion and tiles when the operation is set
-    up.  Keys other than the tpp backend's raise like the reference's."""
+    TensorOperation.cpp:486-604).  On the HIP backend the result is the loop
+    IR the GPU planner runs: size-1 loops dropped, loops of one type that are
+    contiguous in every tensor fused, exec type ``shared`` for the C loops of
+    a contraction (the kernel grid) and ``prim`` for the loops inside the
+    kernel (M, N, K; every loop of a permutation).  Tiles are chosen when the
+    operation is set up.  Keys other than the tpp backend's raise like the
+    reference's; their values have no effect."""
     actual = config.backend or "hip"
     if actual not in BACKENDS:
         raise ValueError(f"optimize: no backend {actual!r} here (only {BACKENDS})")
@@ -518,10 +522,41 @@ def optimize(config: TensorOperationConfig,
     if rejected:
         raise RuntimeError(f"optimize returned {ErrorType.invalid_optimization_config.name}: "
                            f"unknown key or non-integer value for {rejected}")
-    return dataclasses.replace(config, backend=actual,
-                               dim_types=tuple(config.dim_types), dim_sizes=tuple(config.dim_sizes),
-                               exec_types=(ExecType.prim,) * len(config.dim_types),
-                               strides=(tuple(tuple(t) for t in config.strides[0]),))
+    dim_types, dim_sizes, strides = _fuse_loops(config.dim_types, config.dim_sizes, config.strides[0])
+    binary = config.prim_main in (PrimType.gemm, PrimType.brgemm)
+    exec_types = tuple(ExecType.shared if binary and t == DimType.c else ExecType.prim for t in dim_types)
+    return dataclasses.replace(config, backend=actual, dim_types=dim_types, dim_sizes=dim_sizes,
+                               exec_types=exec_types, strides=(strides,))
+
+
+def _fuse_loops(dim_types, dim_sizes, strides):
+    """The loops as the GPU planner runs them: loops of size 1 dropped (one is
+    kept if nothing else is left), then any two loops of one type where the
+    outer one's stride equals the inner one's stride times its size in every
+    tensor merged into one loop of the product size, until none is left to
+    merge (the fusion step of reference ContractionOptimizer.cpp:76-111, for a
+    kernel that takes whole loop types at once, so no loop is split or
+    reordered).  Returns (dim_types, dim_sizes, strides per tensor)."""
+    loops = [[DimType(t), int(s), [int(st[i]) for st in strides]]
+             for i, (t, s) in enumerate(zip(dim_types, dim_sizes)) if int(s) != 1]
+    if not loops:
+        loops = [[DimType(dim_types[0]), int(dim_sizes[0]), [int(st[0]) for st in strides]]] if dim_sizes else []
+    merged = True
+    while merged:
+        merged = False
+        for o, outer in enumerate(loops):
+            for i, inner in enumerate(loops):
+                if i != o and inner[0] == outer[0] and \
+                        all(so == si * inner[1] for so, si in zip(outer[2], inner[2])):
+                    outer[1] *= inner[1]
+                    outer[2] = inner[2]
+                    del loops[i]
+                    merged = True
+                    break
+            if merged:
+                break
+    return (tuple(t for t, _, _ in loops), tuple(s for _, s, _ in loops),
+            tuple(tuple(lp[2][k] for lp in loops) for k in range(len(strides))))
 
 
 __all__ = ["TensorOperation", "TensorOperationConfig", "ConfigError", "DataType", "PrimType", "ExecType", "DimType",

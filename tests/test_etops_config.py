@@ -140,10 +140,72 @@ def test_json_rejects():
     assert e.value.rules == ("prim_last",)
 
 
+def _offsets(cfg):
+    """The multiset of (offset in each tensor) tuples over every point of the
+    config's iteration space: two configs with equal multisets multiply the
+    same element pairs and add each product into the same output element."""
+    import itertools
+    sizes, strides = cfg.dim_sizes, cfg.strides[0]
+    return sorted(tuple(sum(i * s for i, s in zip(idx, st)) for st in strides)
+                  for idx in itertools.product(*map(range, sizes)))
+
+
+def test_optimize_fuses_contiguous_loops():
+    # out[b][c][m1][m2][n], A[b][c][m1][m2][k1][k2], B[b][c][n][k1][k2], plus
+    # a size-1 loop x; b,c / m1,m2 / k1,k2 are contiguous in every tensor
+    sizes = dict(b=2, c=3, m1=4, x=1, m2=5, n=6, k1=7, k2=8)
+    d = etops.dim
+    types = (d.c, d.c, d.m, d.n, d.m, d.n, d.k, d.k)
+    a = dict(b=3360, c=1120, m1=280, x=0, m2=56, n=0, k1=8, k2=1)
+    b = dict(b=1008, c=336, m1=0, x=0, m2=0, n=56, k1=8, k2=1)
+    o = dict(b=360, c=120, m1=30, x=99, m2=6, n=1, k1=0, k2=0)
+    names = list(sizes)
+    cfg = _gemm(dim_types=types, exec_types=(etops.exec.seq,) * 8, dim_sizes=tuple(sizes.values()),
+                strides=(tuple(tuple(t[n] for n in names) for t in (a, b, o)),))
+    opt = etops.optimize(cfg)
+    assert opt.dim_types == (d.c, d.m, d.n, d.k)
+    assert opt.dim_sizes == (6, 20, 6, 56)
+    assert opt.exec_types == (etops.exec.shared, etops.exec.prim, etops.exec.prim, etops.exec.prim)
+    assert opt.strides == (((1120, 56, 0, 1), (336, 0, 56, 1), (120, 6, 1, 0)),)
+    assert _offsets(opt) == _offsets(cfg)
+    # the optimized config is valid and optimizes to itself
+    assert etops.optimize(opt) == opt
+
+
+def test_optimize_keeps_non_contiguous_loops():
+    # A's m1 stride padded (300, not 64 * 4): m1 and m2 stay apart
+    d = etops.dim
+    cfg = _gemm(dim_types=(d.m, d.m, d.n, d.k), exec_types=(etops.exec.prim,) * 4, dim_sizes=(3, 4, 5, 7),
+                strides=(((300, 64, 0, 1), (0, 0, 7, 1), (20, 5, 1, 0)),))
+    opt = etops.optimize(cfg)
+    assert opt.dim_sizes == (3, 4, 5, 7)
+    assert _offsets(opt) == _offsets(cfg)
+    # the same with A unpadded fuses m1, m2
+    cfg = _gemm(dim_types=(d.m, d.m, d.n, d.k), exec_types=(etops.exec.prim,) * 4, dim_sizes=(3, 4, 5, 7),
+                strides=(((28 * 4, 28, 0, 1), (0, 0, 7, 1), (20, 5, 1, 0)),))
+    opt = etops.optimize(cfg)
+    assert opt.dim_sizes == (12, 5, 7) and opt.strides[0][0] == (28, 0, 1)
+    assert _offsets(opt) == _offsets(cfg)
+
+
+def test_optimize_unary():
+    # out[c1][c2][c3] = in[c3][c1][c2]: c1,c2 contiguous in both, c3 not
+    d = etops.dim
+    cfg = etops.TensorOperationConfig(data_type=etops.float32, prim_first=etops.prim.none,
+                                      prim_main=etops.prim.copy, prim_last=etops.prim.none,
+                                      dim_types=(d.c,) * 3, exec_types=(etops.exec.seq,) * 3, dim_sizes=(3, 4, 5),
+                                      strides=(((4, 1, 12), (20, 5, 1)),))
+    opt = etops.optimize(cfg)
+    assert opt.dim_sizes == (12, 5) and opt.strides == (((1, 12), (5, 1)),)
+    assert opt.exec_types == (etops.exec.prim,) * 2
+    assert _offsets(opt) == _offsets(cfg)
+
+
 def test_optimize():
     cfg = _gemm(exec_types=(etops.exec.seq, etops.exec.shared, etops.exec.sfc))
     opt = etops.optimize(cfg)
     assert opt.backend == "hip"
+    # nothing to fuse: the loops come back as given, all inside the kernel
     assert opt.exec_types == (etops.exec.prim,) * 3
     assert opt.dim_sizes == cfg.dim_sizes and opt.dim_types == tuple(cfg.dim_types)
     assert opt.strides == (tuple(tuple(t) for t in cfg.strides[0]),)

@@ -193,3 +193,33 @@ def test_float64_contraction_and_setup_errors(torch_cuda, oracle):
                     cfg.exec_types, cfg.dim_sizes, cfg.strides) == etops.ErrorType.compilation_failed
     with pytest.raises(RuntimeError, match="execute before a successful setup"):
         op.execute(torch.zeros(1, device="cuda"), torch.zeros(1, device="cuda"), dout)
+
+
+def test_optimized_config_runs_the_same(torch_cuda, oracle):
+    """etops.optimize's fused loops (b,c / m1,m2 / k1,k2 contiguous in every
+    tensor, a size-1 loop dropped) give the same output bit for bit as the
+    config it came from, and both match the oracle."""
+    torch = torch_cuda
+    sizes = (2, 3, 40, 1, 5, 48, 7, 8)
+    types = (C, C, M, N, M, N, K, K)
+    sa = (3360 * 10, 1120 * 10, 280, 0, 56, 0, 8, 1)
+    sb = (1008 * 8, 336 * 8, 0, 0, 0, 56, 8, 1)
+    so = (360 * 80, 120 * 80, 30 * 8, 0, 6 * 8, 1, 0, 0)
+    cfg = _config(types, sizes, sa, sb, so)
+    opt = etops.optimize(cfg)
+    assert opt.dim_types == (C, M, N, K) and opt.dim_sizes == (6, 200, 48, 56), opt
+    rng = np.random.default_rng(5)
+    a = rng.uniform(-1, 1, _extent(sizes, sa)).astype(np.float32)
+    b = rng.uniform(-1, 1, _extent(sizes, sb)).astype(np.float32)
+    n_out = _extent(sizes, so)
+    da, db = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    outs = []
+    for c in (cfg, opt):
+        op = etops.TensorOperation(c)
+        dout = torch.full((n_out,), float("nan"), device="cuda")
+        op.execute(da, db, dout)
+        op.close()
+        outs.append(dout.cpu().numpy())
+    assert np.array_equal(outs[0], outs[1])
+    ref = _oracle(oracle, cfg, a, b, np.zeros(n_out, np.float32), oracle.ZERO, oracle.UNDEF)
+    assert rel_frobenius(ref, outs[1]) <= TOL_FP32
