@@ -444,20 +444,30 @@ def bench_mlp(torch, eir, stream, steps, warmup):
     ws = [(torch.rand(fo * fi, device="cuda", generator=g) * 2 - 1) / fi ** 0.5 for fi, fo in zip(widths, widths[1:])]
     bs = [(torch.rand(fo, device="cuda", generator=g) * 2 - 1) / fi ** 0.5 for fi, fo in zip(widths, widths[1:])]
     out = torch.empty(1152 * 10, device="cuda")
-    nodes = host.Nodes(sizes, aux, stream=stream)
-    prev = nodes.add_leaf([0, 1, 2, 3], x)
-    n_w = [nodes.add_leaf(i, w) for i, w in zip(ids_w, ws)]
-    for layer in range(5):
-        last = eir.RELU if layer < 4 else eir.UNDEFINED_KTYPE
-        prev = nodes.add_binary(ids_h[layer], prev, n_w[layer], tensor=out if layer == 4 else None,
-                                aux=bs[layer], first=eir.COPY, main=eir.MADD, last=last)
-    nodes.compile(prev)
-    for n in n_w:
-        nodes.store_and_lock_data(n)
+
+    def build(s):
+        nodes = host.Nodes(sizes, aux, stream=s)
+        prev = nodes.add_leaf([0, 1, 2, 3], x)
+        n_w = [nodes.add_leaf(i, w) for i, w in zip(ids_w, ws)]
+        for layer in range(5):
+            last = eir.RELU if layer < 4 else eir.UNDEFINED_KTYPE
+            prev = nodes.add_binary(ids_h[layer], prev, n_w[layer], tensor=out if layer == 4 else None,
+                                    aux=bs[layer], first=eir.COPY, main=eir.MADD, last=last)
+        nodes.compile(prev)
+        for n in n_w:
+            nodes.store_and_lock_data(n)
+        return nodes
+
+    nodes = build(stream)
     flops = nodes.num_ops()
     wall, per_eval = time_launches(torch, stream, nodes.eval_async, steps, warmup)
     nodes.close()
-    return dict(flops=flops, wall=wall, per_launch=per_eval)
+    # the same tree replayed as a recorded HIP graph (needs a stream of its own)
+    gs = torch.cuda.Stream()
+    nodes = build(gs)
+    _, per_eval_graph = time_launches(torch, gs, nodes.eval_graph_async, steps, warmup)
+    nodes.close()
+    return dict(flops=flops, wall=wall, per_launch=per_eval, per_launch_graph=per_eval_graph)
 
 
 def cpu_baseline_c3():
@@ -714,9 +724,10 @@ def main():
                                                  us_per_eval=round(mlp["per_launch"] * 1e6, 2),
                                                  frac_fp32_peak=round(gf / (PEAK_FP32_TFLOPS * 1e3), 4),
                                                  flops_per_eval=mlp["flops"],
+                                                 us_per_eval_graph=round(mlp["per_launch_graph"] * 1e6, 2),
                                                  path="EinsumNode tree, 5 contractions with bias COPY + ReLU, "
                                                       "weights locked")
-        log(f"mlp: {mlp['per_launch']*1e6:.1f} us/eval")
+        log(f"mlp: {mlp['per_launch']*1e6:.1f} us/eval, {mlp['per_launch_graph']*1e6:.1f} us/eval as graph replay")
 
     if run("samples"):
         tccg, nets = bench_samples(torch, eir, stream, set(x for x in args.samples.split(",") if x))

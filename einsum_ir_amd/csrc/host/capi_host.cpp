@@ -88,6 +88,15 @@ struct etir_nodes_s {
   backend::MemoryManager memory;
   void * stream = nullptr;
   int64_t root = -1;
+  // recorded evaluation of the root (etir_nodes_eval_graph*), dropped when
+  // the tree is compiled again or its locked data changes
+  etir_graph_t graph = nullptr;
+
+  void reset_graph() {
+    if( graph != nullptr ) etir_hip_graph_destroy( graph );
+    graph = nullptr;
+  }
+  ~etir_nodes_s() { reset_graph(); }
 };
 
 extern "C" {
@@ -424,6 +433,7 @@ int etir_nodes_add_binary( etir_nodes_t    handle,
 int etir_nodes_compile( etir_nodes_t handle, int64_t root ) {
   if( handle == nullptr ) return err_t::CALLED_BEFORE_COMPILATION;
   if( root < 0 || root >= (int64_t) handle->nodes.size() ) return err_t::INVALID_ID;
+  handle->reset_graph();
   try {
     handle->nodes[root].set_stream( handle->stream );
     err_t l_err = handle->nodes[root].compile();
@@ -439,12 +449,14 @@ int etir_nodes_compile( etir_nodes_t handle, int64_t root ) {
 int etir_nodes_store_and_lock_data( etir_nodes_t handle, int64_t node ) {
   if( handle == nullptr || handle->root < 0 ) return err_t::CALLED_BEFORE_COMPILATION;
   if( node < 0 || node >= (int64_t) handle->nodes.size() ) return err_t::INVALID_ID;
+  handle->reset_graph();
   return handle->nodes[node].store_and_lock_data();
 }
 
 int etir_nodes_unlock_data( etir_nodes_t handle, int64_t node ) {
   if( handle == nullptr || handle->root < 0 ) return err_t::CALLED_BEFORE_COMPILATION;
   if( node < 0 || node >= (int64_t) handle->nodes.size() ) return err_t::INVALID_ID;
+  handle->reset_graph();
   return handle->nodes[node].unlock_data();
 }
 
@@ -456,6 +468,35 @@ int etir_nodes_eval_async( etir_nodes_t handle ) {
 int etir_nodes_eval( etir_nodes_t handle ) {
   if( handle == nullptr || handle->root < 0 ) return err_t::CALLED_BEFORE_COMPILATION;
   return handle->nodes[ handle->root ].eval_sync();
+}
+
+int etir_nodes_eval_graph_async( etir_nodes_t handle ) {
+  if( handle == nullptr || handle->root < 0 ) return err_t::CALLED_BEFORE_COMPILATION;
+  if( handle->stream == nullptr ) return err_t::UNDEFINED_ERROR;
+  backend::EinsumNode & l_root = handle->nodes[ handle->root ];
+  if( handle->graph == nullptr ) {
+    // a recording keeps the pointers it saw: host tensors, staged through
+    // temporary device copies per evaluation, cannot take part
+    if( l_root.has_host_ext() ) return err_t::NO_DATA_PTR_PROVIDED;
+    if( etir_hip_graph_begin( handle->stream ) != ETIR_SUCCESS ) return err_t::UNDEFINED_ERROR;
+    err_t l_err = l_root.eval_one_stream_async();
+    if( l_err != err_t::SUCCESS ) {
+      etir_hip_graph_abort( handle->stream );
+      return l_err;
+    }
+    if( etir_hip_graph_end( handle->stream, &handle->graph ) != ETIR_SUCCESS ) {
+      handle->graph = nullptr;
+      return err_t::UNDEFINED_ERROR;
+    }
+  }
+  return etir_hip_graph_launch( handle->graph, handle->stream ) == ETIR_SUCCESS
+           ? err_t::SUCCESS : err_t::UNDEFINED_ERROR;
+}
+
+int etir_nodes_eval_graph( etir_nodes_t handle ) {
+  int l_err = etir_nodes_eval_graph_async( handle );
+  if( l_err != err_t::SUCCESS ) return l_err;
+  return etir_hip_synchronize( handle->stream ) == ETIR_SUCCESS ? err_t::SUCCESS : err_t::UNDEFINED_ERROR;
 }
 
 int64_t etir_nodes_num_ops( etir_nodes_t handle ) {

@@ -55,6 +55,8 @@ _SIGS = {
     "etir_nodes_unlock_data": (ctypes.c_int, [_vp, ctypes.c_int64]),
     "etir_nodes_eval": (ctypes.c_int, [_vp]),
     "etir_nodes_eval_async": (ctypes.c_int, [_vp]),
+    "etir_nodes_eval_graph": (ctypes.c_int, [_vp]),
+    "etir_nodes_eval_graph_async": (ctypes.c_int, [_vp]),
     "etir_nodes_num_ops": (ctypes.c_int64, [_vp]),
     "etir_nodes_destroy": (ctypes.c_int, [_vp]),
 }
@@ -303,6 +305,14 @@ class Nodes(_Handle):
 
     def eval_async(self):
         _check(host_lib().etir_nodes_eval_async(self._h))
+
+    def eval_graph(self):
+        """One evaluation as a replay of a recorded HIP graph (recorded on the
+        first call; needs a stream of its own); waits for it."""
+        _check(host_lib().etir_nodes_eval_graph(self._h))
+
+    def eval_graph_async(self):
+        _check(host_lib().etir_nodes_eval_graph_async(self._h))
 
     def num_ops(self):
         return int(host_lib().etir_nodes_num_ops(self._h))

@@ -150,6 +150,14 @@ int etir_nodes_unlock_data( etir_nodes_t handle, int64_t node );
 /* EinsumNode::eval of the compiled root: _eval waits, _eval_async does not. */
 int etir_nodes_eval( etir_nodes_t handle );
 int etir_nodes_eval_async( etir_nodes_t handle );
+/* The root's evaluation as a replay of a recorded HIP graph, recorded on the
+ * first call and again after compile, store_and_lock_data or unlock_data;
+ * the stream given at creation must not be NULL.  No counterpart in the
+ * reference (the same as etir_expression_eval_graph, for trees built node by
+ * node): one replay instead of EinsumNode::eval's per-call launches.
+ * _eval_graph waits for the replay, _eval_graph_async does not. */
+int etir_nodes_eval_graph( etir_nodes_t handle );
+int etir_nodes_eval_graph_async( etir_nodes_t handle );
 int64_t etir_nodes_num_ops( etir_nodes_t handle );
 int etir_nodes_destroy( etir_nodes_t handle );
 

@@ -121,3 +121,56 @@ def test_nodes_reject_bad_children(torch_cuda):
         nodes.add_binary([0, 1], 0, 1)
     assert err.value.code == eir.INVALID_ID
     nodes.close()
+
+
+def test_mlp_graph_replay(torch_cuda):
+    """etir_nodes_eval_graph: the tree recorded once and replayed; every
+    replay equals eval()'s output bit for bit, with eager evaluations and
+    synchronisations between replays; locking and unlocking the weights drops
+    the recording, and the next replay follows the new state."""
+    torch = torch_cuda
+    x, ws, bs = _params(9)
+    out = torch.zeros(BATCH * WIDTHS[-1], dtype=torch.float32, device="cuda")
+    s = torch.cuda.Stream()
+    nodes, n_w, t_w = _build(torch, x, ws, bs, out, stream=s)
+    torch.cuda.synchronize()
+    nodes.eval()
+    ref = out.cpu().numpy()
+    assert rel_frobenius(_reference(x, ws, bs), ref.reshape(BATCH, WIDTHS[-1])) <= TOL_FP32
+    for r in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        nodes.eval_graph()
+        assert np.array_equal(out.cpu().numpy(), ref), f"replay {r} differs from eval()"
+        nodes.eval()
+        assert np.array_equal(out.cpu().numpy(), ref)
+    # locked weights: device copies, so zeroing the external buffers after
+    # the lock changes nothing in the new recording's replays
+    for n in n_w:
+        nodes.store_and_lock_data(n)
+    for t in t_w:
+        t.zero_()
+    torch.cuda.synchronize()
+    for r in range(2):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        nodes.eval_graph()
+        assert np.array_equal(out.cpu().numpy(), ref), f"locked replay {r} differs"
+    # unlocked: the external (zeroed) weights are read again, output = b4
+    for n in n_w:
+        nodes.unlock_data(n)
+    out.fill_(float("nan"))
+    torch.cuda.synchronize()
+    nodes.eval_graph()
+    got = out.cpu().numpy().reshape(BATCH, WIDTHS[-1])
+    assert np.array_equal(got, np.broadcast_to(bs[4], got.shape))
+    nodes.close()
+
+
+def test_mlp_graph_needs_a_stream(torch_cuda):
+    x, ws, bs = _params(10)
+    out = torch_cuda.zeros(BATCH * WIDTHS[-1], dtype=torch_cuda.float32, device="cuda")
+    nodes, _, _ = _build(torch_cuda, x, ws, bs, out)
+    with pytest.raises(eir.EinsumIrError):
+        nodes.eval_graph()
+    nodes.close()
