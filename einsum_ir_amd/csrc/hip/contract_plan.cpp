@@ -41,6 +41,7 @@ int launch_contract_cpx( bool f64, int32_t ma, int32_t mb, bool kaff, ContractAr
                          uint32_t grid, hipStream_t stream );
 int launch_contract_bf16_dma( int32_t ma, int32_t mb, int32_t variant, ContractArgs const & a,
                               uint32_t grid, hipStream_t stream );
+int launch_contract_panel( ContractArgs const & a, hipStream_t stream );
 int launch_contract_kwave( int32_t waves, int32_t kw, ContractArgs const & a, uint32_t grid,
                            hipStream_t stream );
 int launch_contract_f32_dma( int32_t ma, int32_t mb, ContractArgs const & a, uint32_t grid, hipStream_t stream );
@@ -162,6 +163,7 @@ char const * tile_str( int32_t t ) {
     case TILE_F32_DMA_128x128: return "f32_dma_128x128x32";
     case TILE_GEMV:            return "gemv";
     case TILE_SKINNY:          return "skinny";
+    case TILE_PANEL:           return "panel";
     default:                return "?";
   }
 }
@@ -569,6 +571,43 @@ int plan_contraction_impl( int64_t            num_loops,
     if( l_sk_ok || l_forced ) plan.tile = TILE_SKINNY;
   }
 
+  // ------------------------------------- short K, one free side of 65-256
+  // With K <= 64 an MFMA tile lives for one load round trip and its stores
+  // (einsum_benchmark MERA root, M = 177147, N = 243, K = 50: 73 us on 128 x
+  // 128 tiles, 62 here): the short operand stays in LDS for the whole launch
+  // and persistent workgroups stream panels of the long side, each panel's
+  // stores issued between the next one's MFMAs.  fp32, no C dims, first
+  // touch ZERO, last touch none or RELU, the long operand affine along its
+  // side, at least four panels per CU (each workgroup pays about one panel
+  // of set-up: M = 16384 k x 243 x 50 at 2 / 4 panels per CU 22.7 / 32.1 us
+  // against 21.1 / 40.9 on the tiles).  ETIR_TILE=15 forces it where the
+  // shape allows (a long side of at least one panel), ETIR_NO_PANEL turns it
+  // off.
+  {
+    int64_t const l_sh = std::min( l_kern_m, l_kern_n );
+    int64_t const l_lo = std::max( l_kern_m, l_kern_n );
+    bool const l_res_a = l_kern_m <= l_kern_n;
+    std::vector< int64_t > const & l_tl = l_res_a ? l_tn_b : l_tm_a;
+    bool l_aff = true;
+    int64_t const l_st = l_tl.size() > 1 ? l_tl[1] : 0;
+    for( std::size_t l_i = 0; l_i < l_tl.size() && l_aff; l_i++ ) l_aff = ( l_tl[l_i] == int64_t( l_i ) * l_st );
+    l_aff = l_aff && l_st >= 0 && l_st <= std::numeric_limits< int32_t >::max();
+    int64_t l_mo = 0, l_no = 0;
+    for( int64_t l_v : l_tm_out ) l_mo = std::max( l_mo, l_v );
+    for( int64_t l_v : l_tn_out ) l_no = std::max( l_no, l_v );
+    bool const l_pn_shape = l_f32 && !l_cpx && plan.tile != TILE_GEMV && plan.tile != TILE_SKINNY
+                         && l_size_c == 1 && l_sh > 64 && l_sh <= 256 && l_size_k >= 1 && l_size_k <= 64
+                         && ktype_first_touch == ETIR_KTYPE_ZERO
+                         && ( ktype_last_touch == ETIR_KTYPE_UNDEFINED || ktype_last_touch == ETIR_KTYPE_RELU )
+                         && !plan.needs_aux && l_aff && 4 * ( l_mo + l_no + 1 ) <= int64_t( 0xffffff00u );
+    int64_t const l_pl = ( l_sh > 128 ) ? 64 : 128;
+    char const * l_env_t = std::getenv( "ETIR_TILE" );
+    bool const l_forced = l_pn_shape && l_lo >= l_pl && l_env_t != nullptr && std::atoi( l_env_t ) == TILE_PANEL;
+    bool const l_pn_ok = l_pn_shape && ( l_lo + l_pl - 1 ) / l_pl >= 4 * l_cus && l_env_t == nullptr
+                      && std::getenv( "ETIR_NO_PANEL" ) == nullptr;
+    if( l_pn_ok || l_forced ) plan.tile = TILE_PANEL;
+  }
+
   // ------------------------------------------- long K on few large tiles
   // The 64 x 64 tile fills the chip where fewer than 256 of the 128 x 128
   // tiles exist, but runs at about half the fp32 direct-to-LDS kernel's rate;
@@ -593,7 +632,7 @@ int plan_contraction_impl( int64_t            num_loops,
   // 90 on split K)
   {
     int64_t const l_t32 = n_tiles( TILE_F32_KWAVE_32x32 );
-    bool const l_kw_ok = l_f32 && plan.tile != TILE_GEMV && plan.tile != TILE_SKINNY && plan.mode_a == LOAD_VEC_K && plan.mode_b == LOAD_VEC_K && l_k_affine
+    bool const l_kw_ok = l_f32 && plan.tile != TILE_GEMV && plan.tile != TILE_SKINNY && plan.tile != TILE_PANEL && plan.mode_a == LOAD_VEC_K && plan.mode_b == LOAD_VEC_K && l_k_affine
                       && l_sk_a == 1 && l_sk_b == 1 && l_size_k % 16 == 0 && l_size_k >= 256
                       && l_size_k <= 4096 && n_tiles( plan.tile ) < l_cus && l_t32 >= l_cus / 2
                       && l_t32 <= 2 * l_cus
@@ -617,7 +656,7 @@ int plan_contraction_impl( int64_t            num_loops,
   // of them factored if needed) become C loops of a partial contraction that
   // writes one workspace slice per split, and split_reduce sums the slices.
   if( allow_split && !l_f64 && !l_cpx && l_size_k >= 512 && plan.tile != TILE_F32_KWAVE_32x32
-      && plan.tile != TILE_GEMV && plan.tile != TILE_SKINNY ) {
+      && plan.tile != TILE_GEMV && plan.tile != TILE_SKINNY && plan.tile != TILE_PANEL ) {
     int64_t const l_tiles = n_tiles( plan.tile );
     if( l_tiles > 0 && l_tiles < l_cus ) {
       // at least 128 k per split; aim for two workgroups per CU
@@ -943,6 +982,13 @@ int plan_contraction_impl( int64_t            num_loops,
     a.out_nt = ( l_run >= 32 && ( l_run % 32 == 0 || l_run == l_tn_out.size() ) ) ? 1 : 0;
     if( char const * l_env = std::getenv( "ETIR_OUT_NT" ) ) a.out_nt = std::atoi( l_env ) != 0 ? 1 : 0;
   }
+  if( plan.tile == TILE_PANEL ) {
+    int64_t l_mo = 0, l_no = 0;
+    for( int64_t l_v : l_tm_out ) l_mo = std::max( l_mo, l_v );
+    for( int64_t l_v : l_tn_out ) l_no = std::max( l_no, l_v );
+    a.out_bytes  = uint32_t( 4 * ( l_mo + l_no + 1 ) );
+    a.panel_grid = int32_t( l_cus );
+  }
   if(    plan.tile == TILE_BF16_DMA_256x256 && plan.dma_variant == 3 && a.M % 256 == 0 && a.N % 256 == 0
       && a.out_off32 && a.out_nt && !a.out_bf16 && a.first_touch == ETIR_KTYPE_ZERO
       && a.last_touch == ETIR_KTYPE_UNDEFINED ) {
@@ -1096,6 +1142,9 @@ int launch_contraction( ContractionPlan const & plan,
       break;
     case TILE_SKINNY:
       l_err = launch_contract_skinny( plan.dtype_in == ETIR_BF16, a, stream );
+      break;
+    case TILE_PANEL:
+      l_err = launch_contract_panel( a, stream );
       break;
     default: return fail( ETIR_COMPILATION_FAILED, "contraction: unknown tile configuration" );
   }

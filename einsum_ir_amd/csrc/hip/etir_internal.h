@@ -227,7 +227,8 @@ enum TileCfg : int32_t {
   TILE_F32_KWAVE_32x32  = 11, // K split over the waves of one workgroup (contract_kwave.hip)
   TILE_F32_DMA_128x128  = 12, // fp32 direct-to-LDS kernel (contract_f32_dma.hip)
   TILE_GEMV             = 13, // M == 1 or N == 1: one thread per output element (contract_gemv.hip)
-  TILE_SKINNY           = 14  // one free side of 2-64: one thread per long index (contract_skinny.hip)
+  TILE_SKINNY           = 14, // one free side of 2-64: one thread per long index (contract_skinny.hip)
+  TILE_PANEL            = 15  // short K, one free side of 65-256 resident in LDS (contract_panel.hip)
 };
 
 struct ContractArgs {
@@ -277,6 +278,11 @@ struct ContractArgs {
   // K, every row offset a multiple of 4 elements and K % 4 == 0, so a thread
   // reads its K range in 4-element vectors
   int32_t skinny_kvec;
+  // panel kernel: bytes from the output's base to the end of its last
+  // element (stores at or past it are dropped by the buffer range check) and
+  // the number of persistent workgroups
+  uint32_t out_bytes;
+  int32_t  panel_grid;
 };
 
 struct ContractionPlan {
