@@ -148,6 +148,7 @@ int etir_hip_plan_describe( etir_plan_t plan, char * buf, int64_t len ) {
     if( p.mode == etir::PermMode::TRANSPOSE && p.tr_shape != 0 ) {
       l_s += p.tr_shape == 1 ? " tile=128x32" : p.tr_shape == 2 ? " tile=32x128"
            : p.tr_shape == 3 ? " tile=128x64 v16" : " tile=128x32 v16";
+      if( p.args.o1_size > 0 ) l_s += " fold=" + std::to_string( p.args.o1_size ) + "x" + std::to_string( p.args.size_o / p.args.o1_size );
     }
     if( p.mode == etir::PermMode::ROWS ) {
       l_s += " row=" + std::to_string( p.rows_len ) + "/" + std::to_string( p.rows_vw )

@@ -102,6 +102,13 @@ struct PermArgs {
   int32_t  slot_pi;   // REG4: LDS pitch (16-byte slots) of i and of c
   int32_t  slot_pc;
   int32_t  nt_store;  // TRANSPOSE: streaming (non-temporal) output stores
+  // TRANSPOSE, 2-byte 16-byte-read tile: o1_size > 0 folds the output's
+  // next dim (output stride o1_size, input stride s_in_o2) into o, which then
+  // runs over o1 + o1_size * o2 (size_o = o1_size * that dim's size);
+  // o1_magic = ceil(2^32 / o1_size), so o / o1_size = umulhi(o, o1_magic)
+  int32_t  o1_size;
+  uint32_t o1_magic;
+  int64_t  s_in_o2;
   // ROWS: rows of the shared unit-stride dim (g chunks of the kernel's vector
   // width each); x continues the input's run, y the output's; tiles of
   // rows_ex x rows_ey rows, parked in LDS at rows_pitch chunks per x

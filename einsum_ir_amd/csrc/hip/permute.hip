@@ -127,7 +127,12 @@ __device__ inline int64_t grid_digit( uint32_t & io_rest, int64_t i_size ) {
 // column reads of the write phase step one bank per row.  VEC false (no
 // vector alignment, a.vec_ok 0): every access is one element (a separate
 // instantiation: the run-time choice inside one kernel cost 10 %).
-template< typename T, int TI, int TO, bool VEC >
+// FOLD: o is the output's unit-stride dim and the one after it together
+// (a.o1_size > 0), contiguous in the output, two strides in the input, so an
+// output dim that is not a multiple of the tile still fills it (bf16
+// abcd->bdac 36,48,36,512: o runs over c and a, 1296 elements, instead of
+// 36 of every 64).
+template< typename T, int TI, int TO, bool VEC, bool FOLD >
 __global__ __launch_bounds__( kThreads )
 void perm_transpose16_kernel( PermArgs a ) {
   static_assert( sizeof( T ) == 2, "16-byte reads of 8 elements" );
@@ -166,17 +171,26 @@ void perm_transpose16_kernel( PermArgs a ) {
   for( int l_p = 0; l_p < RP; l_p++ ) {
     int64_t const l_o = l_o0 + l_r + ( kThreads / RT ) * l_p;
     int64_t const l_i = l_i0 + VR * l_c;
+    int64_t l_row;                          // input offset of row o
+    if constexpr( FOLD ) {
+      uint32_t const l_o2 = __umulhi( uint32_t( l_o ), a.o1_magic );
+      uint32_t const l_o1 = uint32_t( l_o ) - l_o2 * uint32_t( a.o1_size );
+      l_row = int64_t( l_o1 ) * a.s_in_o + int64_t( l_o2 ) * a.s_in_o2;
+    }
+    else {
+      l_row = l_o * a.s_in_o;
+    }
 #pragma unroll
     for( int l_e = 0; l_e < VR; l_e++ ) l_v[l_p].v[l_e] = T( 0 );
     if constexpr( VEC ) {
       if( l_o < a.size_o && l_i < a.size_i ) {
-        l_v[l_p] = *reinterpret_cast< VecN< T, VR > const * >( l_in + l_o * a.s_in_o + l_i );
+        l_v[l_p] = *reinterpret_cast< VecN< T, VR > const * >( l_in + l_row + l_i );
       }
     }
     else {
 #pragma unroll
       for( int l_e = 0; l_e < VR; l_e++ ) {
-        if( l_o < a.size_o && l_i + l_e < a.size_i ) l_v[l_p].v[l_e] = l_in[l_o * a.s_in_o + l_i + l_e];
+        if( l_o < a.size_o && l_i + l_e < a.size_i ) l_v[l_p].v[l_e] = l_in[l_row + l_i + l_e];
       }
     }
   }
@@ -834,8 +848,14 @@ int launch_typed( PermutePlan const & p,
     if( p.tr_shape == 3 || p.tr_shape == 4 ) {
       if constexpr( sizeof( T ) == 2 ) {
         auto go = [&]( auto to_c, auto vec_c ) {
-          hipLaunchKernelGGL( ( perm_transpose16_kernel< T, 128, decltype( to_c )::value, decltype( vec_c )::value > ),
-                              l_g, dim3( kThreads ), 0, stream, a );
+          if( a.o1_size > 0 ) {
+            hipLaunchKernelGGL( ( perm_transpose16_kernel< T, 128, decltype( to_c )::value, decltype( vec_c )::value,
+                                                           true > ), l_g, dim3( kThreads ), 0, stream, a );
+          }
+          else {
+            hipLaunchKernelGGL( ( perm_transpose16_kernel< T, 128, decltype( to_c )::value, decltype( vec_c )::value,
+                                                           false > ), l_g, dim3( kThreads ), 0, stream, a );
+          }
         };
         std::integral_constant< int, 64 > const l_to64{};
         std::integral_constant< int, 32 > const l_to32{};
@@ -1364,6 +1384,31 @@ int plan_permute( int64_t         num_dims,
     return true;
   };
   auto all_div4 = [&]( int skip0, int skip1 ) { return all_div( 4, skip0, skip1 ); };
+  // 2-byte transpose with 16-byte reads: input rows in groups of 8 elements,
+  // output rows in groups of 4, every other stride a multiple of those
+  auto v16_ok = [&]( int di, int dof ) {
+    if(    plan.elem_bytes != 2 || plan.size[di] % 8 != 0 || plan.s_in[dof] % 8 != 0 || plan.size[dof] % 4 != 0
+        || plan.s_out[di] % 4 != 0 ) {
+      return false;
+    }
+    for( int l_di = 0; l_di < l_n; l_di++ ) {
+      if( l_di != di && plan.s_in[l_di] % 8 != 0 ) return false;
+      if( l_di != dof && plan.s_out[l_di] % 4 != 0 ) return false;
+    }
+    return true;
+  };
+  // the output dim that continues the output's run after dim dof (output
+  // stride = dof's size), not the input's unit-stride dim di; -1 if none
+  auto fold_dim = [&]( int di, int dof ) {
+    int l_f = -1;
+    for( int l_di = 0; l_di < l_n; l_di++ ) {
+      if(    l_di != di && l_di != dof && plan.s_out[l_di] == plan.size[dof]
+          && plan.size[dof] * plan.size[l_di] < ( int64_t( 1 ) << 26 ) ) {
+        l_f = l_di;
+      }
+    }
+    return l_f;
+  };
 
   if( ktype == ETIR_KTYPE_ZERO ) {
     plan.mode = PermMode::FILL;
@@ -1392,7 +1437,17 @@ int plan_permute( int64_t         num_dims,
   int64_t const l_vb = (    plan.elem_bytes == 2 && l_dim_i >= 0 && l_dim_o >= 0
                          && plan.size[l_dim_i] % 8 == 0 && plan.size[l_dim_o] % 8 == 0 ) ? 8 : 4;
   int64_t const l_scale = plan.elem_bytes == 2 ? 2 : 1;
-  int64_t const l_short = kReg4MaxShort * l_scale;
+  // 2-byte elements whose output unit-stride dim (above 16) the 16-byte
+  // transpose can fold with the output's next dim (below) take that
+  // transpose rather than REG4 (bf16 abcd->dcba 32,32,128,128: 66.9 against
+  // 70.0 % of HBM peak; 24,32,128,128: 25.8 against 71.5 %)
+  // (an input unit-stride dim of at least a tile side: shorter ones take the
+  // tiled kernel below when not REG4)
+  bool const l_fold16 = plan.elem_bytes == 2 && l_dim_i >= 0 && l_dim_o >= 0 && l_dim_i != l_dim_o
+                     && plan.size[l_dim_i] >= kTile && plan.size[l_dim_o] > kReg4MaxShort
+                     && v16_ok( l_dim_i, l_dim_o )
+                     && fold_dim( l_dim_i, l_dim_o ) >= 0;
+  int64_t const l_short = l_fold16 ? kReg4MaxShort : kReg4MaxShort * l_scale;
   int64_t const l_both = 32 * l_scale;
 
   // a long input unit-stride dim with a short output one: split it into an
@@ -1603,14 +1658,23 @@ int plan_permute( int64_t         num_dims,
     // 2-byte elements whose input rows allow 8-element vectors (and output
     // rows 4-element ones): the 16-byte-read transpose, 128 x 64 unless
     // 128 x 32 fills strictly more of its padded tile grid
-    bool l_v16 = plan.elem_bytes == 2 && a.size_i % 8 == 0 && a.s_in_o % 8 == 0 && a.size_o % 4 == 0
-              && a.s_out_i % 4 == 0;
-    for( int l_di = 0; l_di < l_n; l_di++ ) {
-      if( l_di != l_dim_i && plan.s_in[l_di] % 8 != 0 ) l_v16 = false;
-      if( l_di != l_dim_o && plan.s_out[l_di] % 4 != 0 ) l_v16 = false;
+    bool const l_v16 = v16_ok( l_dim_i, l_dim_o );
+    // an output unit-stride dim that leaves 64-wide tiles part empty: the
+    // output's next dim, if it continues the output's run, is folded into o
+    // (not the input's unit dim: that one is i), and the tile is 128 x 64,
+    // whose output rows are whole 128-byte lines (bf16 abcd->bdac
+    // 36,48,36,512: 51.6 % of HBM peak on 128 x 32 tiles of o = c, 64.7 %
+    // folded on 128 x 32, 71.0 % folded on 128 x 64)
+    int const l_dim_o2 = ( l_v16 && a.size_o % 64 != 0 ) ? fold_dim( l_dim_i, l_dim_o ) : -1;
+    a.o1_size = 0;
+    if( l_dim_o2 >= 0 ) {
+      a.o1_size  = int32_t( a.size_o );
+      a.o1_magic = uint32_t( ( ( uint64_t( 1 ) << 32 ) + uint64_t( a.size_o ) - 1 ) / uint64_t( a.size_o ) );
+      a.s_in_o2  = plan.s_in[l_dim_o2];
+      a.size_o  *= plan.size[l_dim_o2];
     }
     if( l_v16 ) {
-      plan.tr_shape = ( util( 128, 32 ) > util( 128, 64 ) ) ? 4 : 3;
+      plan.tr_shape = ( l_dim_o2 < 0 && util( 128, 32 ) > util( 128, 64 ) ) ? 4 : 3;
       l_ti = 128;
       l_to = ( plan.tr_shape == 3 ) ? 64 : 32;
     }
@@ -1619,7 +1683,7 @@ int plan_permute( int64_t         num_dims,
     a.num_batch = 0;
     a.num_batch_total = 1;
     for( int l_di = 0; l_di < l_n; l_di++ ) {
-      if( l_di == l_dim_i || l_di == l_dim_o ) continue;
+      if( l_di == l_dim_i || l_di == l_dim_o || l_di == l_dim_o2 ) continue;
       a.batch_size[a.num_batch]  = plan.size[l_di];
       a.batch_s_in[a.num_batch]  = plan.s_in[l_di];
       a.batch_s_out[a.num_batch] = plan.s_out[l_di];

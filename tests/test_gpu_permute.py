@@ -172,12 +172,27 @@ def test_permute_transpose_shapes(torch_cuda, oracle, expr, sizes, tile, dtype, 
 
 # bf16 transposes with 16-byte reads (input rows in groups of 8 elements,
 # output rows in groups of 4): 128 x 64 tiles, or 128 x 32 where those fill
-# more of their padded grid; ragged extents on both sides
+# more of their padded grid; ragged extents on both sides.  An output
+# unit-stride dim that is not a multiple of 64 is folded with the output's
+# next dim when that one continues the output's run (fold=o1xo2, 128 x 64)
 TR16_CASES = [
-    ("abcd->bdac", dict(a=36, b=5, c=36, d=512), "tile=128x64 v16"),
-    ("abcd->bdac", dict(a=7, b=3, c=72, d=256), "tile=128x32 v16"),     # o = 72: 72/96 of 32-row tiles
-    ("abcd->dbca", dict(a=64, b=3, c=5, d=200), "tile=128x64 v16"),     # i = 200: 200 of 256
-    ("abc->cba", dict(a=100, b=3, c=136), "tile=128x64 v16"),           # o = 100: 100 of 128
+    # o = c (36) folded with a (36): 1296-element o rows
+    ("abcd->bdac", dict(a=36, b=5, c=36, d=512), "tile=128x64 v16 fold=36x36"),
+    # o = c (72) folded with a (7): 504 o rows
+    ("abcd->bdac", dict(a=7, b=3, c=72, d=256), "tile=128x64 v16 fold=72x7"),
+    # o = a (64): no fold; i = 200: 200 of 256
+    ("abcd->dbca", dict(a=64, b=3, c=5, d=200), "tile=128x64 v16"),
+    # o = a (100) folded with b (3)
+    ("abc->cba", dict(a=100, b=3, c=136), "tile=128x64 v16 fold=100x3"),
+    # o = c (44) folded with a (7), ragged on both sides (i = 200)
+    ("abcd->bdac", dict(a=7, b=3, c=44, d=200), "fold=44x7"),
+    # o = a (40) folded with b (9), c a batch dim
+    ("abcd->dcba", dict(a=40, b=9, c=5, d=136), "fold=40x9"),
+    # o = a (24, above 16): the folded transpose rather than register blocks
+    ("abcd->dcba", dict(a=24, b=32, c=5, d=128), "tile=128x64 v16 fold=24x32"),
+    # no next output dim continues o's run (the input's unit dim d follows o):
+    # 128 x 32 where it fills more of its grid
+    ("abc->bca", dict(a=72, b=6, c=256), "tile=128x32 v16"),
 ]
 
 
@@ -203,7 +218,7 @@ def test_permute_transpose16_unaligned(torch_cuda, oracle, offset):
     ref = o0[offset:].copy()
     oracle.permute(u["sizes"], u["strides_in"], u["strides_out"], x[offset:].copy(), ref, dtype=eir.BF16)
     plan = eir.PermutePlan(u["sizes"], u["strides_in"], u["strides_out"], dtype=eir.BF16)
-    assert "tile=128x64 v16" in plan.describe(), plan.describe()
+    assert "v16 fold=36x36" in plan.describe(), plan.describe()
     dx, do = _to_dev(torch, x), _to_dev(torch, o0)
     plan.execute(dx[offset:], do[offset:], stream=torch.cuda.current_stream())
     torch.cuda.synchronize()
