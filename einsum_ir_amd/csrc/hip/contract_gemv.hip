@@ -39,6 +39,24 @@ __device__ inline float gemv_ld< uint16_t >( uint16_t const * p, int64_t off ) {
   return kern::bf16_to_f32( p[off] );
 }
 
+// The long operand and the output are each touched once per launch: their
+// loads and stores are non-temporal, so they stream past the caches instead
+// of evicting the short operand and each other (lm_batch's C=128 M=1
+// N=65536 K=11 node, 403 MB: 73.6 us with ordinary accesses, 70.2 with
+// non-temporal loads, 69.8 with non-temporal stores, 63.6 with both)
+template< typename T >
+__device__ inline float gemv_ld_nt( T const * p, int64_t off );
+template<>
+__device__ inline float gemv_ld_nt< float >( float const * p, int64_t off ) {
+  return __builtin_nontemporal_load( p + off );
+}
+template<>
+__device__ inline float gemv_ld_nt< uint16_t >( uint16_t const * p, int64_t off ) {
+  return kern::bf16_to_f32( __builtin_nontemporal_load( p + off ) );
+}
+__device__ inline void gemv_st_nt( float * p, float v ) { __builtin_nontemporal_store( v, p ); }
+__device__ inline void gemv_st_nt( uint16_t * p, uint16_t v ) { __builtin_nontemporal_store( v, p ); }
+
 template< typename T, bool KAFF >
 __global__ __launch_bounds__( 256 ) void contract_gemv_kernel( ContractArgs a ) {
   uint64_t const l_total = uint64_t( a.C ) * uint64_t( a.M ) * uint64_t( a.N );
@@ -91,7 +109,7 @@ __global__ __launch_bounds__( 256 ) void contract_gemv_kernel( ContractArgs a ) 
 #pragma unroll
     for( int l_i = 0; l_i < 8; l_i++ ) {
       l_x[l_i] = gemv_ld< T >( l_pa, koff_a( l_k + l_i ) );
-      l_y[l_i] = gemv_ld< T >( l_pb, koff_b( l_k + l_i ) );
+      l_y[l_i] = gemv_ld_nt< T >( l_pb, koff_b( l_k + l_i ) );
     }
 #pragma unroll
     for( int l_i = 0; l_i < 8; l_i++ ) l_v = fmaf( l_x[l_i], l_y[l_i], l_v );
@@ -106,7 +124,7 @@ __global__ __launch_bounds__( 256 ) void contract_gemv_kernel( ContractArgs a ) 
     for( int l_i = 0; l_i < 8; l_i++ ) {
       int32_t const l_kc = min( l_k + l_i, a.K - 1 );
       l_x[l_i] = gemv_ld< T >( l_pa, koff_a( l_kc ) );
-      l_y[l_i] = gemv_ld< T >( l_pb, koff_b( l_kc ) );
+      l_y[l_i] = gemv_ld_nt< T >( l_pb, koff_b( l_kc ) );
     }
 #pragma unroll
     for( int l_i = 0; l_i < 8; l_i++ ) {
@@ -118,8 +136,8 @@ __global__ __launch_bounds__( 256 ) void contract_gemv_kernel( ContractArgs a ) 
   if( l_aux_first ) l_v = l_aux + l_v;
   if( a.last_touch == ETIR_KTYPE_RELU ) l_v = fmaxf( l_v, 0.0f );
   else if( a.last_touch == ETIR_KTYPE_ADD ) l_v = l_v + l_aux;
-  if( a.out_bf16 ) reinterpret_cast< uint16_t * >( a.out )[l_off] = kern::f32_to_bf16_rne( l_v );
-  else             reinterpret_cast< float * >( a.out )[l_off] = l_v;
+  if( a.out_bf16 ) gemv_st_nt( reinterpret_cast< uint16_t * >( a.out ) + l_off, kern::f32_to_bf16_rne( l_v ) );
+  else             gemv_st_nt( reinterpret_cast< float * >( a.out ) + l_off, l_v );
 }
 
 // Kernel M == 1 with the long operand B and the output unit-stride along N
@@ -131,7 +149,6 @@ __global__ __launch_bounds__( 256 ) void contract_gemv_kernel( ContractArgs a ) 
 template< typename T, bool KAFF >
 __global__ __launch_bounds__( 256 ) void contract_gemv4_kernel( ContractArgs a ) {
   typedef float f4 __attribute__( ( ext_vector_type( 4 ) ) );
-  typedef V4< T > TV;
   int32_t const l_n4 = a.N / 4;
   uint64_t const l_total = uint64_t( a.C ) * uint64_t( l_n4 );
   uint64_t const l_e = uint64_t( blockIdx.x ) * 256 + threadIdx.x;
@@ -180,11 +197,18 @@ __global__ __launch_bounds__( 256 ) void contract_gemv4_kernel( ContractArgs a )
   T const * l_pb = reinterpret_cast< T const * >( a.b ) + a.tc_b[l_c] + l_n;
   auto koff_a = [&]( int32_t k ) -> int64_t { return KAFF ? int64_t( k ) * a.sk_a : int64_t( a.tk_a[k] ); };
   auto koff_b = [&]( int32_t k ) -> int64_t { return KAFF ? int64_t( k ) * a.sk_b : int64_t( a.tk_b[k] ); };
+  // one non-temporal vector of 4 elements of B (16 bytes fp32, 8 bytes bf16)
+  typedef uint16_t u16x4 __attribute__( ( ext_vector_type( 4 ) ) );
   auto ld4 = [&]( int64_t off ) {
-    TV const l_t = *reinterpret_cast< TV const * >( l_pb + off );
     f4 l_r;
+    if constexpr( sizeof( T ) == 4 ) {
+      l_r = __builtin_nontemporal_load( reinterpret_cast< f4 const * >( l_pb + off ) );
+    }
+    else {
+      u16x4 const l_t = __builtin_nontemporal_load( reinterpret_cast< u16x4 const * >( l_pb + off ) );
 #pragma unroll
-    for( int l_i = 0; l_i < 4; l_i++ ) l_r[l_i] = gemv_ld< T >( l_t.v, l_i );
+      for( int l_i = 0; l_i < 4; l_i++ ) l_r[l_i] = kern::bf16_to_f32( l_t[l_i] );
+    }
     return l_r;
   };
 
@@ -233,13 +257,14 @@ __global__ __launch_bounds__( 256 ) void contract_gemv4_kernel( ContractArgs a )
     l_r[l_i] = l_w;
   }
   if( a.out_bf16 ) {
-    V4< uint16_t > l_o;
+    u16x4 l_o;
 #pragma unroll
-    for( int l_i = 0; l_i < 4; l_i++ ) l_o.v[l_i] = kern::f32_to_bf16_rne( l_r[l_i] );
-    *reinterpret_cast< V4< uint16_t > * >( reinterpret_cast< uint16_t * >( a.out ) + l_off ) = l_o;
+    for( int l_i = 0; l_i < 4; l_i++ ) l_o[l_i] = kern::f32_to_bf16_rne( l_r[l_i] );
+    __builtin_nontemporal_store( l_o, reinterpret_cast< u16x4 * >( reinterpret_cast< uint16_t * >( a.out ) + l_off ) );
   }
   else {
-    *reinterpret_cast< f4 * >( reinterpret_cast< float * >( a.out ) + l_off ) = f4{ l_r[0], l_r[1], l_r[2], l_r[3] };
+    __builtin_nontemporal_store( f4{ l_r[0], l_r[1], l_r[2], l_r[3] },
+                                 reinterpret_cast< f4 * >( reinterpret_cast< float * >( a.out ) + l_off ) );
   }
 }
 
