@@ -50,7 +50,7 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-mfma-ceiling", action="store_true",
                    help="skip the matrix-core rate and clock probe (einsum_ir_amd/bin/mfma_ceiling)")
-    p.add_argument("--only", default="", help="comma list of configs to run (c1,c2,c3,c4,c5,mlp,samples)")
+    p.add_argument("--only", default="", help="comma list of configs to run (c1,c2,c3,c4,c5,mlp,nodes,samples)")
     p.add_argument("--samples", default="",
                    help="with samples: comma list of what to run (tccg and/or einsum_benchmark network names; "
                         "default all)")
@@ -470,6 +470,46 @@ def bench_mlp(torch, eir, stream, steps, warmup):
     return dict(flops=flops, wall=wall, per_launch=per_eval, per_launch_graph=per_eval_graph)
 
 
+# single tree nodes timed alone, each the shape one kernel family was tuned on:
+# (name, expression, sizes, what bounds it)
+NODES = [
+    # einsum_benchmark lm_batch's largest matrix-vector node (403 MB, HBM-bound)
+    ("lm_batch_gemv_C128_M1_N65536_K11", "ck,ckn->cn", dict(c=128, k=11, n=65536), "hbm"),
+    # einsum_benchmark MERA's root on the short-K panel kernel (its operands'
+    # and output's layouts as the tree lays them out are einsum_ir_amd's own;
+    # this is the plain [m][n] layout of the same sizes)
+    ("mera_root_M177147_N243_K50", "mk,nk->mn", dict(m=177147, k=50, n=243), "mfma"),
+]
+
+
+def bench_nodes(torch, eir, stream, steps, warmup):
+    """Single contraction nodes timed alone (inputs resident, back-to-back
+    launches): rate against the HBM peak (algorithmic bytes: inputs + output)
+    or the fp32 MFMA peak (2 C M N K flops)."""
+    rows = []
+    for name, expr, sizes, bound in NODES:
+        lp = eir.binary_loops(expr, sizes)
+        plan = eir.ContractionPlan(lp["dim_types"], lp["sizes"], lp["strides_left"], lp["strides_right"],
+                                   lp["strides_out"])
+        ins, out = expr.split("->")
+        numel = lambda t: int(__import__("math").prod(sizes[d] for d in t))
+        l_t, r_t = ins.split(",")
+        a = torch.rand(numel(l_t), device="cuda")
+        b = torch.rand(numel(r_t), device="cuda")
+        o = torch.empty(numel(out), device="cuda")
+        _, per = time_launches(torch, stream, lambda: plan.execute(a, b, o, stream=stream), steps, warmup)
+        byt = 4 * (numel(l_t) + numel(r_t) + numel(out))
+        row = dict(node=name, expr=expr, sizes=sizes, us_per_launch=round(per * 1e6, 2), kernel=plan.describe(),
+                   bytes_per_launch=byt, gbs=round(byt / per * 1e-9, 1), flops_per_launch=plan.flops,
+                   gflops=round(plan.flops / per * 1e-9, 1))
+        row["frac_peak"] = round(row["gbs"] / PEAK_HBM_GBS if bound == "hbm" else row["gflops"] / (PEAK_FP32_TFLOPS * 1e3), 4)
+        row["bound"] = bound
+        rows.append(row)
+        plan.close()
+        del a, b, o
+    return rows
+
+
 def cpu_baseline_c3():
     """CPU restatement of the reference algorithm on a bounded sample of config 3:
     one batch (z=1), a=16 of 64 (M = 16*64 = 1024), all of N = 4096 and K = 1024."""
@@ -697,6 +737,11 @@ def main():
                                           frac_fp32_peak=round(gf / (PEAK_FP32_TFLOPS * 1e3), 4),
                                           kernel=c1["desc"])
         log(f"c1: {c1['desc']}  {c1['per_launch']*1e6:.2f} us/launch")
+    if run("nodes"):
+        nodes = bench_nodes(torch, eir, stream, max(args.steps, 50), args.warmup)
+        extra["single_nodes"] = nodes
+        log("nodes: " + ", ".join(f"{r['node']} {r['us_per_launch']:.1f} us ({r['frac_peak']*100:.1f} % of the "
+                                  f"{r['bound']} peak)" for r in nodes))
     if run("c4"):
         c4 = bench_c4(torch, eir, stream, max(5, args.steps // 5), min(args.warmup, 2), settle=args.settle)
         gf = c4["flops"] / c4["per_launch"] * 1e-9
