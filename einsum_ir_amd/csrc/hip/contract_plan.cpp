@@ -963,6 +963,24 @@ int plan_contraction_impl( int64_t            num_loops,
     a.skinny_kvec = ( plan.tile == TILE_SKINNY && l_k_affine && ( l_size_k <= 1 || l_skl == 1 ) && l_size_k % 4 == 0
                       && all_multiple( l_tl, 4 ) && all_multiple( l_tcl, 4 ) ) ? 1 : 0;
     if( a.skinny_kvec ) plan.desc += " kvec";
+    // the output as [long][short] with the short side unit-stride (short
+    // offsets s, long offsets i * S): a workgroup's outputs are one block,
+    // written in address order through LDS; only where the output is
+    // written, not read (no accumulation, no aux)
+    std::vector< int64_t > const & l_tlo = l_short_a ? l_tn_out : l_tm_out;
+    std::vector< int64_t > const & l_tso = l_short_a ? l_tm_out : l_tn_out;
+    a.skinny_blk = 0;
+    if( plan.tile == TILE_SKINNY && ktype_first_touch == ETIR_KTYPE_ZERO && !plan.needs_aux
+        && ( ktype_last_touch == ETIR_KTYPE_UNDEFINED || ktype_last_touch == ETIR_KTYPE_RELU )
+        && affine_stride( l_tso ) == 1 ) {
+      int64_t const l_s = int64_t( l_tso.size() );
+      bool l_ok = true;
+      for( std::size_t l_i = 0; l_ok && l_i < l_tlo.size(); l_i++ ) l_ok = ( l_tlo[l_i] == int64_t( l_i ) * l_s );
+      if( l_ok ) {
+        a.skinny_blk = 1;
+        plan.desc += " blk";
+      }
+    }
   }
   if( l_cpx ) {
     a.cpx_a   = l_x[0].s[l_sa];

@@ -51,7 +51,12 @@ constexpr int kSkChunk   = 32;    // k per LDS chunk of the short operand
 template< typename T, int SMAX, bool SHORT_A, bool KAFF, bool KVEC >
 __global__ __launch_bounds__( kSkThreads ) void contract_skinny_kernel( ContractArgs a ) {
   constexpr int KC = kSkChunk;
-  __shared__ float s_op[KC][SMAX];
+  // the short operand's chunk [KC][SMAX]; after the K loop, the block
+  // store's staging [SC][kSkThreads + 1]
+  constexpr int SC  = SMAX < 16 ? SMAX : 16;
+  constexpr int RAW = KC * SMAX > SC * ( kSkThreads + 1 ) ? KC * SMAX : SC * ( kSkThreads + 1 );
+  __shared__ float s_raw[RAW];
+  float ( *s_op )[SMAX] = reinterpret_cast< float ( * )[SMAX] >( s_raw );
   // the short side's output and aux offsets, read from LDS in the epilogue:
   // a global table read between the stores would wait for every store
   // before it (one vector-memory counter for loads and stores)
@@ -144,6 +149,43 @@ __global__ __launch_bounds__( kSkThreads ) void contract_skinny_kernel( Contract
       }
     } );
     __syncthreads();
+  }
+
+  if( a.skinny_blk ) {
+    // the output as [long][short], the short side unit-stride: the
+    // workgroup's outputs are one block of (i1 - i0) * S elements, written in
+    // chunks of SC short indices, each chunk in address order (runs of SC
+    // elements S apart).  Element e of a chunk is long row t = e / ns, short
+    // index sl = e - t * ns, with t = (e * ceil(2^16 / ns)) >> 16 (exact for
+    // e < 4096 = 256 * 16, ns <= 16; 24-bit multiplies, full rate)
+    constexpr uint32_t LD = kSkThreads + 1;      // LDS row stride: odd, successive short indices on other banks
+    int32_t const  l_i0 = int32_t( blockIdx.x ) * kSkThreads;
+    uint32_t const l_nl = uint32_t( min( l_i0 + kSkThreads, l_nlong ) - l_i0 );
+    int64_t const  l_ob = a.tc_out[l_c] + int64_t( l_i0 ) * l_nshrt;
+    kern::static_for< SMAX / SC >( [&]( auto cc ) __attribute__( ( always_inline ) ) {
+      constexpr int l_s0 = decltype( cc )::value * SC;
+      if( l_s0 >= l_nshrt ) return;
+#pragma unroll
+      for( int l_j = 0; l_j < SC; l_j++ ) {
+        float l_v = l_acc[l_s0 + l_j];
+        if( a.last_touch == ETIR_KTYPE_RELU ) l_v = fmaxf( l_v, 0.0f );
+        s_raw[uint32_t( l_j ) * LD + threadIdx.x] = l_v;
+      }
+      __syncthreads();
+      uint32_t const l_ns = uint32_t( min( SC, l_nshrt - l_s0 ) );
+      uint32_t const l_m  = ( 65536u + l_ns - 1 ) / l_ns;
+      uint32_t const l_n  = l_nl * l_ns;
+      for( uint32_t l_e = threadIdx.x; l_e < l_n; l_e += kSkThreads ) {
+        uint32_t const l_t  = __umul24( l_e, l_m ) >> 16;
+        uint32_t const l_sl = l_e - __umul24( l_t, l_ns );
+        float const l_v = s_raw[l_sl * LD + l_t];
+        int64_t const l_off = l_ob + int64_t( __umul24( l_t, uint32_t( l_nshrt ) ) ) + l_s0 + l_sl;
+        if( a.out_bf16 ) reinterpret_cast< uint16_t * >( a.out )[l_off] = kern::f32_to_bf16_rne( l_v );
+        else             reinterpret_cast< float * >( a.out )[l_off] = l_v;
+      }
+      __syncthreads();
+    } );
+    return;
   }
   if( !l_in ) return;
 

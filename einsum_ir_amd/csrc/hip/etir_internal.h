@@ -285,6 +285,10 @@ struct ContractArgs {
   // K, every row offset a multiple of 4 elements and K % 4 == 0, so a thread
   // reads its K range in 4-element vectors
   int32_t skinny_kvec;
+  // one-short-side kernel: the output is [long][short] with the short side
+  // unit-stride, so a workgroup's outputs form one block that it writes in
+  // address order through LDS
+  int32_t skinny_blk;
   // panel kernel: bytes from the output's base to the end of its last
   // element (stores at or past it are dropped by the buffer range check) and
   // the number of persistent workgroups

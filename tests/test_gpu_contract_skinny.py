@@ -107,3 +107,71 @@ def test_skinny_switch_off(torch_cuda, oracle, monkeypatch):
     monkeypatch.setenv("ETIR_NO_SKINNY", "1")
     _, desc = run_case(torch_cuda, oracle, "mk,nk->mn", dict(m=11, k=24, n=70000), seed=12)
     assert "skinny" not in desc, desc
+
+
+# outputs laid out as [long][short] with the short side unit-stride: the
+# workgroup writes its outputs as one block through LDS (" blk")
+BLOCK_SHAPES = [
+    # short kernel N of 9 (one chunk of 9), long operand in K vectors
+    ("mk,nk->mn", dict(m=70000, k=40, n=9)),
+    # short kernel M of 45 (SMAX 64: chunks of 16, 16, 13), output [n][m]
+    ("mk,kn->nm", dict(m=45, k=11, n=70000)),
+    # a C dim: one block per workgroup per C index
+    ("zmk,znk->zmn", dict(z=3, m=30000, k=6, n=12)),
+    # short side over two output dims, ragged last workgroup (70001 rows)
+    ("mk,kst->mst", dict(m=70001, k=5, s=4, t=5)),
+    # short side 64 (four full chunks)
+    ("mk,nk->mn", dict(m=70000, k=20, n=64)),
+]
+
+
+@pytest.mark.parametrize("expr,sizes", BLOCK_SHAPES)
+def test_skinny_block_store(torch_cuda, oracle, monkeypatch, expr, sizes):
+    monkeypatch.delenv("ETIR_TILE", raising=False)
+    _, desc = run_case(torch_cuda, oracle, expr, sizes, seed=sum(sizes.values()) % 1000)
+    assert "skinny" in desc and " blk" in desc, desc
+
+
+def test_skinny_block_store_relu_bf16(torch_cuda, oracle):
+    _, desc = run_case(torch_cuda, oracle, "mk,kn->nm", dict(m=45, k=11, n=70000), last=eir.RELU, seed=21)
+    assert " blk" in desc, desc
+    _, desc = run_case(torch_cuda, oracle, "mk,kn->nm", dict(m=45, k=11, n=70000), dtype=eir.BF16,
+                       dtype_out=eir.BF16, seed=22)
+    assert " blk" in desc, desc
+
+
+def test_skinny_block_store_only_for_its_layout(torch_cuda, oracle):
+    """Accumulation into the output reads it per element, and a short side
+    that is not the output's unit-stride run (the MERA chain's
+    [long / 10][short][long % 10]) has no block: the planner keeps the
+    per-thread stores there (same results)."""
+    _, desc = run_case(torch_cuda, oracle, "mk,kn->nm", dict(m=45, k=11, n=70000), first=eir.ADD, seed=23)
+    assert "skinny" in desc and " blk" not in desc, desc
+    _, desc = run_case(torch_cuda, oracle, "akr,ks->asr", dict(a=7000, k=11, r=10, s=45), seed=25)
+    assert "skinny" in desc and " blk" not in desc, desc
+
+
+def test_skinny_block_store_writes_nothing_past_the_output(torch_cuda, oracle):
+    """The last workgroup's block ends with the output: a guard region after
+    the output keeps its bit pattern."""
+    torch = torch_cuda
+    expr, sizes = "mk,nk->mn", dict(m=64 * 1030 + 17, k=9, n=13)
+    left, right, out = parse_binary(expr)
+    loops = loops_for(expr, sizes)
+    rng = np.random.default_rng(24)
+    a = rng.uniform(-1, 1, tensor_numel(left, sizes)).astype(np.float32)
+    b = rng.uniform(-1, 1, tensor_numel(right, sizes)).astype(np.float32)
+    n_out = tensor_numel(out, sizes)
+    plan = eir.ContractionPlan(loops["dim_types"], loops["sizes"], loops["strides_left"],
+                               loops["strides_right"], loops["strides_out"])
+    assert " blk" in plan.describe(), plan.describe()
+    guard = 64 * 1024
+    buf = torch.full((n_out + guard,), float("nan"), device="cuda")
+    plan.execute(torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda(), buf, stream=torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    plan.close()
+    got = buf.cpu().numpy()
+    assert np.isnan(got[n_out:]).all(), "a store landed past the output"
+    ref = np.zeros(n_out, dtype=np.float32)
+    oracle.contract(loops, a, b, ref)
+    assert rel_frobenius(ref, got[:n_out]) <= TOL_FP32
