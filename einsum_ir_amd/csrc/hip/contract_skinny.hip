@@ -25,6 +25,8 @@
 #include "etir_internal.h"
 #include "contract_kernel.h"
 
+#include <numeric>
+
 namespace etir {
 
 namespace {
@@ -84,21 +86,28 @@ __global__ __launch_bounds__( kSkThreads ) void contract_skinny_kernel( Contract
 #pragma unroll
   for( int l_s = 0; l_s < SMAX; l_s++ ) l_acc[l_s] = 0.0f;
 
-  // staging of the short operand: thread t always takes short index t % SMAX
-  // (SMAX divides the workgroup) and k = t / SMAX + i * (threads / SMAX) of
-  // each chunk, so its row offset is read once, and the NI loads of a chunk
+  // staging of the short operand: element e = t + 256 q (q < NI) of a chunk
+  // is (k, s) = (e / SMAX, e % SMAX), so consecutive threads write
+  // consecutive LDS words.  Thread t's short indices repeat with period
+  // P = SMAX / gcd(256, SMAX) in q (1 where SMAX divides the workgroup, 3 for
+  // SMAX 48), so it reads P row offsets once, and the NI loads of a chunk
   // are independent of each other and of the long operand's
   constexpr int NI = SMAX * KC / kSkThreads;
-  static_assert( kSkThreads % SMAX == 0 && NI >= 1, "skinny: SMAX must divide the workgroup" );
-  int const  l_st  = int( threadIdx.x ) % SMAX;
-  int const  l_kt  = int( threadIdx.x ) / SMAX;
-  bool const l_sok = l_st < l_nshrt;
-  int64_t const l_srow = int64_t( l_ts[l_sok ? l_st : 0] );
+  constexpr int P  = SMAX / std::gcd( kSkThreads, SMAX );
+  static_assert( ( SMAX * KC ) % kSkThreads == 0 && NI >= 1 && NI % P == 0, "skinny: SMAX x KC must fill the workgroup" );
+  int32_t l_ss[P];
+  int64_t l_srow[P];
+#pragma unroll
+  for( int l_p = 0; l_p < P; l_p++ ) {
+    l_ss[l_p]   = ( int32_t( threadIdx.x ) + kSkThreads * l_p ) % SMAX;
+    l_srow[l_p] = int64_t( l_ts[l_ss[l_p] < l_nshrt ? l_ss[l_p] : 0] );
+  }
   if( threadIdx.x < SMAX ) {
     int32_t const * l_tso = SHORT_A ? a.tm_out : a.tn_out;
     int32_t const * l_tsa = SHORT_A ? a.tm_aux : a.tn_aux;
-    s_oo[threadIdx.x] = l_sok ? l_tso[l_st] : 0;
-    s_ao[threadIdx.x] = ( l_sok && a.aux != nullptr ) ? l_tsa[l_st] : 0;
+    bool const l_sok = int32_t( threadIdx.x ) < l_nshrt;
+    s_oo[threadIdx.x] = l_sok ? l_tso[threadIdx.x] : 0;
+    s_ao[threadIdx.x] = ( l_sok && a.aux != nullptr ) ? l_tsa[threadIdx.x] : 0;
   }
   __syncthreads();
 
@@ -107,8 +116,9 @@ __global__ __launch_bounds__( kSkThreads ) void contract_skinny_kernel( Contract
     float l_sv[NI];
 #pragma unroll
     for( int l_q = 0; l_q < NI; l_q++ ) {
-      int32_t const l_k = l_k0 + l_kt + l_q * ( kSkThreads / SMAX );
-      l_sv[l_q] = ( l_sok && l_k < a.K ) ? sk_ld< T >( l_ps, l_srow + koff_s( l_k ) ) : 0.0f;
+      int32_t const l_k = l_k0 + ( int32_t( threadIdx.x ) + kSkThreads * l_q ) / SMAX;
+      l_sv[l_q] = ( l_ss[l_q % P] < l_nshrt && l_k < a.K ) ? sk_ld< T >( l_ps, l_srow[l_q % P] + koff_s( l_k ) )
+                                                            : 0.0f;
     }
     // this thread's long-operand values of the chunk, all loads in flight together
     float l_x[KC];
@@ -134,7 +144,7 @@ __global__ __launch_bounds__( kSkThreads ) void contract_skinny_kernel( Contract
       }
     }
 #pragma unroll
-    for( int l_q = 0; l_q < NI; l_q++ ) s_op[l_kt + l_q * ( kSkThreads / SMAX )][l_st] = l_sv[l_q];
+    for( int l_q = 0; l_q < NI; l_q++ ) s_raw[int( threadIdx.x ) + kSkThreads * l_q] = l_sv[l_q];
     __syncthreads();
     int32_t const l_kn = min( int32_t( KC ), a.K - l_k0 );
     // compile-time loops (accumulators and long-operand values stay in
@@ -263,6 +273,7 @@ int launch_contract_skinny( bool bf16_in, ContractArgs const & a, hipStream_t st
     if(      l_nshrt <= 8 )  pick_side( t_c, std::integral_constant< int, 8 >() );
     else if( l_nshrt <= 16 ) pick_side( t_c, std::integral_constant< int, 16 >() );
     else if( l_nshrt <= 32 ) pick_side( t_c, std::integral_constant< int, 32 >() );
+    else if( l_nshrt <= 48 ) pick_side( t_c, std::integral_constant< int, 48 >() );
     else                     pick_side( t_c, std::integral_constant< int, 64 >() );
   };
   if( bf16_in ) pick_smax( BF16() );

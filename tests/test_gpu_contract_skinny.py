@@ -21,6 +21,10 @@ DEFAULT_SHAPES = [
     ("km,kn->mn", dict(k=11, m=5, n=80000), ""),
     # short side 45 with K <= 64, the MERA shape
     ("mk,kn->mn", dict(m=45, k=11, n=70000), ""),
+    # short sides of 33-48 (SMAX 48: the staging's short indices repeat
+    # every 3 elements of a thread), K over two chunks
+    ("km,kn->mn", dict(k=40, m=33, n=70000), ""),
+    ("mk,nk->mn", dict(m=70000, k=52, n=48), "kvec"),
     # K over several 32-k chunks with a tail, K % 4 != 0: no vectors
     ("mk,nk->mn", dict(m=16, k=102, n=70000), ""),
     # a C dim (grid rows)
