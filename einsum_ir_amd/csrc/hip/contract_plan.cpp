@@ -705,10 +705,30 @@ int plan_contraction_impl( int64_t            num_loops,
           break;
         }
       }
-      // extent of the output (elements) over its C, M and N loops
-      int64_t l_span = 1;
+      // extent of the output (elements) over its C, M and N loops; the
+      // workspace slices lie l_span apart, the extent rounded up to 64
+      // elements (16-byte aligned slices)
+      int64_t l_ext = 1;
       for( auto const * l_set : { &l_c, &l_m, &l_n } ) {
-        for( Loop const & l_x : *l_set ) l_span += ( l_x.size - 1 ) * l_x.s[T_OUT];
+        for( Loop const & l_x : *l_set ) l_ext += ( l_x.size - 1 ) * l_x.s[T_OUT];
+      }
+      int64_t const l_span = ( l_ext + 63 ) / 64 * 64;
+      // dense output: its loops, by output stride, each stride the product
+      // of the sizes below it (then the offsets are exactly 0 .. l_ext - 1)
+      int64_t l_dense = 0;
+      {
+        std::vector< std::pair< int64_t, int64_t > > l_ds;
+        for( auto const * l_set : { &l_c, &l_m, &l_n } ) {
+          for( Loop const & l_x : *l_set ) if( l_x.size > 1 ) l_ds.push_back( { l_x.s[T_OUT], l_x.size } );
+        }
+        std::sort( l_ds.begin(), l_ds.end() );
+        int64_t l_pack = 1;
+        bool l_ok = true;
+        for( auto const & l_d : l_ds ) {
+          l_ok = l_ok && ( l_d.first == l_pack );
+          l_pack *= l_d.second;
+        }
+        if( l_ok && l_pack == l_ext ) l_dense = l_ext;
       }
       int64_t const l_ws_bytes = 4 * l_sf * l_span;
       if( l_sf >= 2 && l_size_k / l_sf >= 128 && l_ws_bytes <= ( int64_t( 1 ) << 29 ) ) {
@@ -758,6 +778,7 @@ int plan_contraction_impl( int64_t            num_loops,
         }
         plan.split    = (int32_t) l_sf;
         plan.out_span = l_span;
+        plan.out_dense = plan.needs_aux ? 0 : l_dense;
         plan.partial  = l_part;
         plan.C = l_size_c;
         plan.M = l_part->M;
@@ -771,7 +792,7 @@ int plan_contraction_impl( int64_t            num_loops,
         plan.bytes = l_esz * l_size_c * ( l_size_m + l_size_n ) * l_size_k
                    + l_esz_o * l_size_c * l_size_m * l_size_n;
         plan.desc = "split-K S=" + std::to_string( l_sf ) + " K'=" + std::to_string( l_size_k / l_sf )
-                  + " | " + l_part->desc + " | reduce";
+                  + " | " + l_part->desc + " | reduce" + ( plan.out_dense > 0 ? " flat" : "" );
         return ETIR_SUCCESS;
       }
     }
@@ -1078,6 +1099,9 @@ int launch_contraction( ContractionPlan const & plan,
     r.tn_out = p.tn_out;
     r.tn_aux = p.tn_aux;
     r.span = plan.out_span;
+    r.n_flat = plan.out_dense;
+    r.flat_vec = ( r.n_flat > 0 && r.span % 4 == 0
+                   && reinterpret_cast< uintptr_t >( out ) % uintptr_t( plan.dtype_out == ETIR_BF16 ? 8 : 16 ) == 0 ) ? 1 : 0;
     r.C = (int32_t) plan.C;
     r.M = p.M;
     r.N = p.N;

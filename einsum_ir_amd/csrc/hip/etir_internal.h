@@ -322,10 +322,14 @@ struct ContractionPlan {
   ContractArgs args{};          // table pointers + sizes; tensor pointers set at execute
   // split K: the contraction runs as `partial` -- the split K loops turned
   // into C loops that write one slice each of the workspace (laid out like
-  // the output, `out_span` elements per slice) -- followed by split_reduce,
-  // which sums the slices in a fixed order and applies the touch kernels
+  // the output, `out_span` elements apart: the output's extent rounded up to
+  // 64) -- followed by split_reduce, which sums the slices in a fixed order
+  // and applies the touch kernels.  out_dense: the output's C, M and N
+  // offsets are exactly 0 .. out_dense - 1 (a dense tensor), so the
+  // reduction runs over that range as flat arrays (0: not dense)
   int32_t split = 1;
   int64_t out_span = 0;
+  int64_t out_dense = 0;
   void *  d_ws = nullptr;
   std::shared_ptr< ContractionPlan > partial;
   // tables and workspace live in a caller's region (DevicePlacement), not in
@@ -375,6 +379,8 @@ struct SplitReduceArgs {
   int32_t const * tn_out;
   int32_t const * tn_aux;
   int64_t span;
+  int64_t n_flat;     // > 0: out[o] = touch( sum_s ws[s * span + o] ) for o < n_flat, no tables
+  int32_t flat_vec;   // n_flat > 0: 4 elements per thread (span % 4 == 0, output aligned to 4 elements)
   int32_t C, M, N, S;
   int32_t first_touch;
   int32_t last_touch;

@@ -8,6 +8,7 @@
 // 84-163: ZERO/COPY/ADD first touch, RELU/ADD last touch, aux broadcasts via
 // zero strides).  One thread per output element; consecutive threads take
 // consecutive kernel-N indices, the output's unit-stride index when it has one.
+// A dense output without an aux tensor takes the flat kernel below instead.
 #include "etir_internal.h"
 #include "contract_kernel.h"
 
@@ -77,9 +78,83 @@ __global__ __launch_bounds__( 256 ) void split_reduce_kernel( SplitReduceArgs a 
   else             reinterpret_cast< float * >( a.out )[l_off] = l_v;
 }
 
+// A dense output (its offsets exactly 0 .. n_flat - 1): the slices and the
+// output as flat arrays, VEC consecutive elements per thread (16-byte loads
+// of fp32 slices), no offset tables and no index division.  Same ascending
+// slice order and touch kernels as above, per element.
+template< int VEC >
+__global__ __launch_bounds__( 256 ) void split_reduce_flat_kernel( SplitReduceArgs a ) {
+  typedef float FV __attribute__( ( ext_vector_type( VEC ) ) );
+  int64_t const l_o = ( int64_t( blockIdx.x ) * 256 + threadIdx.x ) * VEC;
+  if( l_o >= a.n_flat ) return;
+  bool const l_read_out = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_UNDEFINED );
+  // the last thread may hold fewer than VEC elements: element by element
+  int const l_n = int( min( int64_t( VEC ), a.n_flat - l_o ) );
+  FV l_old = FV( 0.0f );
+  if( l_read_out ) {
+#pragma unroll
+    for( int l_j = 0; l_j < VEC; l_j++ ) {
+      if( l_j < l_n ) {
+        l_old[l_j] = a.out_bf16 ? kern::bf16_to_f32( reinterpret_cast< uint16_t const * >( a.out )[l_o + l_j] )
+                                : reinterpret_cast< float const * >( a.out )[l_o + l_j];
+      }
+    }
+  }
+  FV l_v = FV( 0.0f );
+  float const * l_p = a.ws + l_o;
+  for( int32_t l_s = 0; l_s < a.S; l_s += 8 ) {
+    FV l_x[8];
+#pragma unroll
+    for( int l_i = 0; l_i < 8; l_i++ ) {
+      l_x[l_i] = FV( 0.0f );
+      if( l_s + l_i < a.S ) {
+        float const * l_q = l_p + int64_t( l_s + l_i ) * a.span;
+        if( VEC > 1 && l_n == VEC ) l_x[l_i] = *reinterpret_cast< FV const * >( l_q );
+        else {
+#pragma unroll
+          for( int l_j = 0; l_j < VEC; l_j++ ) if( l_j < l_n ) l_x[l_i][l_j] = l_q[l_j];
+        }
+      }
+    }
+#pragma unroll
+    for( int l_i = 0; l_i < 8; l_i++ ) {
+      if( l_s + l_i < a.S ) l_v += l_x[l_i];
+    }
+  }
+#pragma unroll
+  for( int l_j = 0; l_j < VEC; l_j++ ) {
+    float l_e = l_v[l_j];
+    if( l_read_out ) l_e = l_old[l_j] + l_e;
+    if( a.last_touch == ETIR_KTYPE_RELU ) l_e = fmaxf( l_e, 0.0f );
+    l_v[l_j] = l_e;
+  }
+  if( a.out_bf16 ) {
+    uint16_t * l_out = reinterpret_cast< uint16_t * >( a.out ) + l_o;
+#pragma unroll
+    for( int l_j = 0; l_j < VEC; l_j++ ) if( l_j < l_n ) l_out[l_j] = kern::f32_to_bf16_rne( l_v[l_j] );
+  }
+  else {
+    float * l_out = reinterpret_cast< float * >( a.out ) + l_o;
+    if( VEC > 1 && l_n == VEC ) *reinterpret_cast< FV * >( l_out ) = l_v;
+    else {
+#pragma unroll
+      for( int l_j = 0; l_j < VEC; l_j++ ) if( l_j < l_n ) l_out[l_j] = l_v[l_j];
+    }
+  }
+}
+
 }  // namespace
 
 int launch_split_reduce( SplitReduceArgs const & a, hipStream_t stream ) {
+  if( a.n_flat > 0 ) {
+    if( a.aux != nullptr ) return fail( ETIR_UNDEFINED_ERROR, "split reduce: flat reduction with an aux tensor" );
+    int64_t const l_vec = a.flat_vec ? 4 : 1;
+    int64_t const l_blocks = ( a.n_flat + 256 * l_vec - 1 ) / ( 256 * l_vec );
+    if( l_blocks > 0x7fffffffLL ) return fail( ETIR_UNDEFINED_ERROR, "split reduce: grid too large" );
+    if( a.flat_vec ) hipLaunchKernelGGL( split_reduce_flat_kernel< 4 >, dim3( (uint32_t) l_blocks ), dim3( 256 ), 0, stream, a );
+    else             hipLaunchKernelGGL( split_reduce_flat_kernel< 1 >, dim3( (uint32_t) l_blocks ), dim3( 256 ), 0, stream, a );
+    return ETIR_SUCCESS;
+  }
   int64_t const l_total = int64_t( a.C ) * a.M * a.N;
   if( l_total == 0 ) return ETIR_SUCCESS;
   int64_t const l_blocks = ( l_total + 255 ) / 256;

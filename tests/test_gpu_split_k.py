@@ -22,12 +22,66 @@ def _split_of(desc):
 def test_split_touch_kernels(torch_cuda, oracle, first, last):
     _, desc = run_case(torch_cuda, oracle, "mk,kn->mn", dict(m=64, k=4096, n=96), first=first, last=last)
     assert _split_of(desc) > 1, desc
+    # a dense output without an aux tensor is reduced as flat arrays
+    needs_aux = first in (eir.COPY, eir.ADD) or last == eir.ADD
+    assert ("reduce flat" in desc) == (not needs_aux), desc
+
+
+@pytest.mark.parametrize("expr,sizes", [
+    # 6111 outputs: the last thread of the 4-wide flat reduction holds 3
+    ("mk,kn->mn", dict(m=63, k=4096, n=97)),
+    # the output's dims in another order than the kernel's M and N (dense all
+    # the same: the flat reduction does not need the element order)
+    ("akb,kn->nab", dict(a=7, k=4096, b=9, n=33)),
+])
+def test_split_flat_reduction(torch_cuda, oracle, expr, sizes):
+    _, desc = run_case(torch_cuda, oracle, expr, sizes, seed=61)
+    assert _split_of(desc) > 1 and "reduce flat" in desc, desc
+    _, desc = run_case(torch_cuda, oracle, expr, sizes, last=eir.RELU, seed=62)
+    assert "reduce flat" in desc, desc
+
+
+def test_split_padded_output_takes_the_table_reduction(torch_cuda, oracle):
+    """An output with a gap between its rows is not dense: the reduction
+    walks the offset tables (and leaves the gap alone); the values agree with
+    the flat reduction of the same contraction into a dense output."""
+    torch = torch_cuda
+    from tests.helpers import loops_for
+    m, k, n, pad = 64, 4096, 96, 5
+    loops = loops_for("mk,kn->mn", dict(m=m, k=k, n=n))
+    rng = np.random.default_rng(63)
+    a = torch.from_numpy(rng.uniform(-1, 1, m * k).astype(np.float32)).cuda()
+    b = torch.from_numpy(rng.uniform(-1, 1, k * n).astype(np.float32)).cuda()
+    outs = {}
+    for row in (n, n + pad):
+        strides_out = list(loops["strides_out"])
+        for i, s_ in enumerate(strides_out):
+            if s_ == n:
+                strides_out[i] = row
+        plan = eir.ContractionPlan(loops["dim_types"], loops["sizes"], loops["strides_left"],
+                                   loops["strides_right"], strides_out)
+        desc = plan.describe()
+        buf = torch.full((m * row,), float("nan"), device="cuda")
+        plan.execute(a, b, buf, stream=torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        plan.close()
+        assert _split_of(desc) > 1, desc
+        assert ("reduce flat" in desc) == (row == n), desc
+        got = buf.cpu().numpy().reshape(m, row)
+        if row > n:
+            assert np.isnan(got[:, n:]).all(), "the reduction wrote into the gap"
+        outs[row] = got[:, :n]
+    ref = np.zeros(m * n, dtype=np.float32)
+    oracle.contract(loops, a.cpu().numpy(), b.cpu().numpy(), ref)
+    for got in outs.values():
+        assert np.linalg.norm(got.ravel() - ref) / np.linalg.norm(ref) <= 1e-5
+    assert np.linalg.norm(outs[n] - outs[n + pad]) / np.linalg.norm(outs[n]) <= 1e-6
 
 
 def test_split_bf16_inputs_and_output(torch_cuda, oracle):
     _, desc = run_case(torch_cuda, oracle, "km,nk->mn", dict(k=2048, m=96, n=64), dtype=eir.BF16,
                        dtype_out=eir.BF16)
-    assert _split_of(desc) > 1, desc
+    assert _split_of(desc) > 1 and "reduce flat" in desc, desc
 
 
 def test_split_multi_loop_k(torch_cuda, oracle):
