@@ -730,6 +730,31 @@ int plan_contraction_impl( int64_t            num_loops,
         }
         if( l_ok && l_pack == l_ext ) l_dense = l_ext;
       }
+      // with an aux tensor: every loop either matches the output's stride in
+      // the aux tensor or is broadcast (aux stride 0), the broadcast loops
+      // outermost in the output; then the aux offset is o % (the extent of
+      // the others)
+      int64_t l_dense_aux = 0;
+      if( l_dense > 0 && plan.needs_aux ) {
+        int64_t l_inner = 1;
+        int64_t l_bmin = std::numeric_limits< int64_t >::max();
+        int64_t l_kmax = 0;
+        bool l_ok = true;
+        for( auto const * l_set : { &l_c, &l_m, &l_n } ) {
+          for( Loop const & l_x : *l_set ) {
+            if( l_x.size <= 1 ) continue;
+            if( l_x.s[T_AUX] == 0 ) l_bmin = std::min( l_bmin, l_x.s[T_OUT] );
+            else {
+              l_ok = l_ok && ( l_x.s[T_AUX] == l_x.s[T_OUT] );
+              l_inner *= l_x.size;
+              l_kmax = std::max( l_kmax, l_x.s[T_OUT] );
+            }
+          }
+        }
+        if( l_ok && ( l_bmin == std::numeric_limits< int64_t >::max() || l_bmin == l_inner ) && l_kmax < l_inner ) {
+          l_dense_aux = l_inner;
+        }
+      }
       int64_t const l_ws_bytes = 4 * l_sf * l_span;
       if( l_sf >= 2 && l_size_k / l_sf >= 128 && l_ws_bytes <= ( int64_t( 1 ) << 29 ) ) {
         // loop arrays of the partial contraction
@@ -778,7 +803,8 @@ int plan_contraction_impl( int64_t            num_loops,
         }
         plan.split    = (int32_t) l_sf;
         plan.out_span = l_span;
-        plan.out_dense = plan.needs_aux ? 0 : l_dense;
+        plan.out_dense     = ( !plan.needs_aux || l_dense_aux > 0 ) ? l_dense : 0;
+        plan.out_dense_aux = plan.needs_aux ? l_dense_aux : 0;
         plan.partial  = l_part;
         plan.C = l_size_c;
         plan.M = l_part->M;
@@ -1100,6 +1126,7 @@ int launch_contraction( ContractionPlan const & plan,
     r.tn_aux = p.tn_aux;
     r.span = plan.out_span;
     r.n_flat = plan.out_dense;
+    r.flat_aux = plan.out_dense_aux;
     r.flat_vec = ( r.n_flat > 0 && r.span % 4 == 0
                    && reinterpret_cast< uintptr_t >( out ) % uintptr_t( plan.dtype_out == ETIR_BF16 ? 8 : 16 ) == 0 ) ? 1 : 0;
     r.C = (int32_t) plan.C;

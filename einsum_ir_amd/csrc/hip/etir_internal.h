@@ -330,6 +330,10 @@ struct ContractionPlan {
   int32_t split = 1;
   int64_t out_span = 0;
   int64_t out_dense = 0;
+  // out_dense with an aux tensor: the aux offset of output offset o is
+  // o % out_dense_aux (the aux broadcasts over the output's outermost loops
+  // and matches its strides on the others)
+  int64_t out_dense_aux = 0;
   void *  d_ws = nullptr;
   std::shared_ptr< ContractionPlan > partial;
   // tables and workspace live in a caller's region (DevicePlacement), not in
@@ -380,6 +384,7 @@ struct SplitReduceArgs {
   int32_t const * tn_aux;
   int64_t span;
   int64_t n_flat;     // > 0: out[o] = touch( sum_s ws[s * span + o] ) for o < n_flat, no tables
+  int64_t flat_aux;   // n_flat > 0 with an aux tensor: its offset for output offset o is o % flat_aux
   int32_t flat_vec;   // n_flat > 0: 4 elements per thread (span % 4 == 0, output aligned to 4 elements)
   int32_t C, M, N, S;
   int32_t first_touch;

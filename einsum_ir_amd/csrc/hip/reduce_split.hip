@@ -8,7 +8,8 @@
 // 84-163: ZERO/COPY/ADD first touch, RELU/ADD last touch, aux broadcasts via
 // zero strides).  One thread per output element; consecutive threads take
 // consecutive kernel-N indices, the output's unit-stride index when it has one.
-// A dense output without an aux tensor takes the flat kernel below instead.
+// A dense output takes the flat kernel below instead (with an aux tensor,
+// where that broadcasts over the output's outermost loops only).
 #include "etir_internal.h"
 #include "contract_kernel.h"
 
@@ -80,16 +81,30 @@ __global__ __launch_bounds__( 256 ) void split_reduce_kernel( SplitReduceArgs a 
 
 // A dense output (its offsets exactly 0 .. n_flat - 1): the slices and the
 // output as flat arrays, VEC consecutive elements per thread (16-byte loads
-// of fp32 slices), no offset tables and no index division.  Same ascending
-// slice order and touch kernels as above, per element.
+// of fp32 slices), no offset tables and no index division; an aux tensor
+// that broadcasts over the output's outermost loops is read at o % flat_aux.
+// Same ascending slice order and touch kernels as above, per element.
 template< int VEC >
 __global__ __launch_bounds__( 256 ) void split_reduce_flat_kernel( SplitReduceArgs a ) {
   typedef float FV __attribute__( ( ext_vector_type( VEC ) ) );
   int64_t const l_o = ( int64_t( blockIdx.x ) * 256 + threadIdx.x ) * VEC;
   if( l_o >= a.n_flat ) return;
-  bool const l_read_out = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_UNDEFINED );
+  bool const l_read_out  = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_UNDEFINED );
+  bool const l_aux_first = ( a.first_touch == ETIR_KTYPE_ADD || a.first_touch == ETIR_KTYPE_COPY );
+  bool const l_need_aux  = ( a.aux != nullptr ) && ( l_aux_first || a.last_touch == ETIR_KTYPE_ADD );
   // the last thread may hold fewer than VEC elements: element by element
   int const l_n = int( min( int64_t( VEC ), a.n_flat - l_o ) );
+  FV l_aux = FV( 0.0f );
+  if( l_need_aux ) {
+#pragma unroll
+    for( int l_j = 0; l_j < VEC; l_j++ ) {
+      if( l_j < l_n ) {
+        int64_t const l_ao = ( l_o + l_j ) % a.flat_aux;
+        l_aux[l_j] = a.out_bf16 ? kern::bf16_to_f32( reinterpret_cast< uint16_t const * >( a.aux )[l_ao] )
+                                : reinterpret_cast< float const * >( a.aux )[l_ao];
+      }
+    }
+  }
   FV l_old = FV( 0.0f );
   if( l_read_out ) {
 #pragma unroll
@@ -125,7 +140,9 @@ __global__ __launch_bounds__( 256 ) void split_reduce_flat_kernel( SplitReduceAr
   for( int l_j = 0; l_j < VEC; l_j++ ) {
     float l_e = l_v[l_j];
     if( l_read_out ) l_e = l_old[l_j] + l_e;
+    if( l_aux_first ) l_e = l_aux[l_j] + l_e;
     if( a.last_touch == ETIR_KTYPE_RELU ) l_e = fmaxf( l_e, 0.0f );
+    else if( a.last_touch == ETIR_KTYPE_ADD ) l_e = l_e + l_aux[l_j];
     l_v[l_j] = l_e;
   }
   if( a.out_bf16 ) {
@@ -147,7 +164,9 @@ __global__ __launch_bounds__( 256 ) void split_reduce_flat_kernel( SplitReduceAr
 
 int launch_split_reduce( SplitReduceArgs const & a, hipStream_t stream ) {
   if( a.n_flat > 0 ) {
-    if( a.aux != nullptr ) return fail( ETIR_UNDEFINED_ERROR, "split reduce: flat reduction with an aux tensor" );
+    if( a.aux != nullptr && a.flat_aux <= 0 ) {
+      return fail( ETIR_UNDEFINED_ERROR, "split reduce: flat reduction with an aux tensor but no aux period" );
+    }
     int64_t const l_vec = a.flat_vec ? 4 : 1;
     int64_t const l_blocks = ( a.n_flat + 256 * l_vec - 1 ) / ( 256 * l_vec );
     if( l_blocks > 0x7fffffffLL ) return fail( ETIR_UNDEFINED_ERROR, "split reduce: grid too large" );

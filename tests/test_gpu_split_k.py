@@ -22,9 +22,23 @@ def _split_of(desc):
 def test_split_touch_kernels(torch_cuda, oracle, first, last):
     _, desc = run_case(torch_cuda, oracle, "mk,kn->mn", dict(m=64, k=4096, n=96), first=first, last=last)
     assert _split_of(desc) > 1, desc
-    # a dense output without an aux tensor is reduced as flat arrays
-    needs_aux = first in (eir.COPY, eir.ADD) or last == eir.ADD
-    assert ("reduce flat" in desc) == (not needs_aux), desc
+    # a dense output (with an aux tensor of its own layout) is reduced as
+    # flat arrays
+    assert "reduce flat" in desc, desc
+
+
+@pytest.mark.parametrize("aux_outer,flat", [
+    # a bias over n, broadcast over the outermost dim m: aux offset o % n
+    (dict(m=1, n=96), True),
+    # broadcast over the innermost dim n: the table reduction
+    (dict(m=64, n=1), False),
+])
+@pytest.mark.parametrize("first,last", [(eir.COPY, eir.RELU), (eir.ZERO, eir.ADD), (eir.ADD, eir.UNDEFINED_KTYPE)])
+def test_split_broadcast_aux(torch_cuda, oracle, aux_outer, flat, first, last):
+    _, desc = run_case(torch_cuda, oracle, "mk,kn->mn", dict(m=64, k=4096, n=96), first=first, last=last,
+                       aux_outer=aux_outer, seed=64)
+    assert _split_of(desc) > 1, desc
+    assert ("reduce flat" in desc) == flat, desc
 
 
 @pytest.mark.parametrize("expr,sizes", [
