@@ -370,6 +370,15 @@ einsum_ir::err_t einsum_ir::backend::BinaryPrimitives::reorder_gpu( bool        
       if( l_ext_k % 2 == 0 )              l_mn_inner = false;
       else if( l_ext_mn[l_s] % 2 == 0 )   l_mn_inner = true;
     }
+    // one short side (2-64) against a long one: the one-short-side kernel
+    // reads the long child coalesced along the long side, so that child takes
+    // its own dims innermost, and the node that produces it writes long runs
+    // of its output instead of K-length ones (einsum_benchmark MERA: the
+    // M = 252, N = 39600 node wrote 6-element runs for its K = 24 consumer)
+    if(    std::min( l_ext_mn[0], l_ext_mn[1] ) >= 2 && std::min( l_ext_mn[0], l_ext_mn[1] ) <= 64
+        && l_ext_mn[l_s] >= 16384 && l_ext_mn[l_s] > l_ext_mn[1 - l_s] ) {
+      l_mn_inner = true;
+    }
 
     std::vector< int64_t > l_c, l_mn, l_x;
     for( dim_t l_ty : { dim_t::C, l_own[l_s] } ) {
