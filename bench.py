@@ -479,6 +479,11 @@ NODES = [
     # and output's layouts as the tree lays them out are einsum_ir_amd's own;
     # this is the plain [m][n] layout of the same sizes)
     ("mera_root_M177147_N243_K50", "mk,nk->mn", dict(m=177147, k=50, n=243), "mfma"),
+    # the one-short-side kernel: MERA's M = 11, N = 415800, K = 24 node
+    # (HBM-bound), and an output laid out [long][short] (short side 13,
+    # unit-stride), written as one block per workgroup
+    ("mera_skinny_M11_N415800_K24", "mk,nk->mn", dict(m=11, k=24, n=415800), "hbm"),
+    ("skinny_block_store_M400000_N13_K24", "mk,nk->mn", dict(m=400000, k=24, n=13), "hbm"),
 ]
 
 
