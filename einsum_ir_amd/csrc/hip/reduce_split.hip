@@ -96,10 +96,13 @@ __global__ __launch_bounds__( 256 ) void split_reduce_flat_kernel( SplitReduceAr
   int const l_n = int( min( int64_t( VEC ), a.n_flat - l_o ) );
   FV l_aux = FV( 0.0f );
   if( l_need_aux ) {
+    // one 64-bit division per thread: the next elements' aux offsets wrap at
+    // most once per element
+    int64_t l_ao = l_o % a.flat_aux;
 #pragma unroll
     for( int l_j = 0; l_j < VEC; l_j++ ) {
+      if( l_j > 0 && ++l_ao == a.flat_aux ) l_ao = 0;
       if( l_j < l_n ) {
-        int64_t const l_ao = ( l_o + l_j ) % a.flat_aux;
         l_aux[l_j] = a.out_bf16 ? kern::bf16_to_f32( reinterpret_cast< uint16_t const * >( a.aux )[l_ao] )
                                 : reinterpret_cast< float const * >( a.aux )[l_ao];
       }
