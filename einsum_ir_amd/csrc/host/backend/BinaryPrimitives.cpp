@@ -340,6 +340,19 @@ einsum_ir::err_t einsum_ir::backend::BinaryPrimitives::reorder_gpu( bool        
     }
     else if( l_gathered < i_min_bytes_permute ) l_keep[l_s] = 3;
   }
+  // one short side (2-64) against a long one: the one-short-side kernel
+  // reads the short operand once per workgroup through its offset tables, so
+  // a short leaf keeps its layout whatever its gathers (a permute of it is a
+  // launch on the tree's path: einsum_benchmark MERA, 1 KB, 5 us), and the
+  // long child takes its K order (K stays one affine index in both)
+  int64_t const l_short_ext = std::min( l_ext_mn[0], l_ext_mn[1] );
+  int const l_short = ( l_ext_mn[0] <= l_ext_mn[1] ) ? 0 : 1;
+  // (not with C dims: those nodes can take the tiles, C fastest, whose
+  // operand layouts the K order would change; TCCG efbadx,cfx->abcdex 7.7 ->
+  // 6.5 TFLOP/s)
+  bool const l_has_c = std::find( l_t_out.begin(), l_t_out.end(), dim_t::C ) != l_t_out.end();
+  bool const l_skinny_node = !l_has_c && l_short_ext >= 2 && l_short_ext <= 64 && l_ext_mn[1 - l_short] >= 16384;
+  if( l_skinny_node && l_fixed[l_short] && l_nd[l_short] > 0 && l_keep[l_short] == 0 ) l_keep[l_short] = 3;
   // two K-read children must agree on the innermost K dim
   if(    l_keep[0] == 2 && l_keep[1] == 2
       && io_dim_ids_left[i_num_dims_left - 1] != io_dim_ids_right[i_num_dims_right - 1] ) {
@@ -349,6 +362,7 @@ einsum_ir::err_t einsum_ir::backend::BinaryPrimitives::reorder_gpu( bool        
   // shared K order: that of a child read along K as it is, else the left's
   int l_k_src = 0;
   if( l_keep[0] != 2 && l_keep[1] == 2 ) l_k_src = 1;
+  if( l_skinny_node && l_keep[l_short] != 0 && l_keep[1 - l_short] == 0 ) l_k_src = l_short;
   std::vector< int64_t > l_k_order;
   for( int64_t l_d = 0; l_d < l_nd[l_k_src]; l_d++ ) {
     if( l_t[l_k_src][l_d] == dim_t::K ) l_k_order.push_back( l_ids[l_k_src][l_d] );
