@@ -1547,8 +1547,11 @@ int plan_permute( int64_t         num_dims,
     // LDS slot pitches: simulate both phases' 16-byte accesses (eight lanes
     // per LDS cycle, a slot covers 4 of the 64 four-byte banks; fp64's
     // 32-byte slots are counted as 16-byte ones) and take the padding with
-    // the fewest conflicts
-    {
+    // the fewest conflicts among those whose tile fits the 64 KiB a
+    // workgroup gets; where none does (several passes over c with a long i
+    // run: bf16 acdb with a 128-wide input run, four passes, about 130 KiB)
+    // the planner takes one pass
+    auto pick_slots = [&]() -> bool {
       int32_t const l_nig = int32_t( a.size_i / l_vb ), l_nog = int32_t( a.size_o / l_vb );
       int32_t const l_si = int32_t( a.size_i );
       int32_t const l_cw = a.c_chunk / plan.reg4_cpt, l_ct = a.c_chunk;
@@ -1558,6 +1561,7 @@ int plan_permute( int64_t         num_dims,
       for( int32_t l_padi = 0; l_padi < 4; l_padi++ ) {
         for( int32_t l_padc = 0; l_padc < 16; l_padc++ ) {
           int32_t const l_pi = l_nog + l_padi, l_pc = l_si * l_pi + l_padc;
+          if( int64_t( a.c_chunk ) * l_pc * l_vb * plan.elem_bytes > 65536 ) continue;
           int64_t l_cost = 0;
           auto group_cost = [&]( std::vector< int32_t > const & slots ) {
             for( std::size_t l_g = 0; l_g < slots.size(); l_g += 8 ) {
@@ -1596,6 +1600,13 @@ int plan_permute( int64_t         num_dims,
           }
         }
       }
+      return l_best >= 0;
+    };
+    if( !pick_slots() && plan.reg4_cpt > 1 ) {
+      plan.reg4_cpt = 1;
+      plan.reg4_threads = l_blocks_c <= 64 ? 64 : ( l_blocks_c <= 128 ? 128 : kThreads );
+      a.c_chunk = (int32_t) std::max< int64_t >( 1, plan.reg4_threads / l_blocks_c );
+      if( !pick_slots() ) return fail( ETIR_COMPILATION_FAILED, "permute: REG4 tile does not fit LDS" );
     }
     a.num_batch = 0;
     a.num_batch_total = 1;

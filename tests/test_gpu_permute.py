@@ -4,6 +4,8 @@ Mirrors the reference's unary tests (reference src/backend/UnaryTpp.test.torch.c
 src/basic/unary/UnaryBackendTpp.test.torch.cpp: transposes of up to 9 dims
 checked with at::equal) with seeded inputs and the CPU oracle as checker.
 """
+import re
+
 import numpy as np
 import pytest
 
@@ -377,6 +379,15 @@ def test_permute_reg4_passes(torch_cuda, oracle, monkeypatch, cpt):
     for expr, sizes in REG4_CASES[:3]:
         desc = _check(torch_cuda, oracle, expr, sizes, seed=int(cpt))
         assert f"t=256x{cpt}" in desc, desc
+
+
+def test_permute_reg4_passes_beyond_the_lds_limit(torch_cuda, oracle, monkeypatch):
+    """A pass count whose LDS tile would exceed 64 KiB (bf16 acdb, a 128-wide
+    input run: four passes would need about 130 KiB) is not taken: one pass,
+    same bytes."""
+    monkeypatch.setenv("ETIR_PERM_REG4_CPT", "4")
+    desc = _check(torch_cuda, oracle, "abcd->acdb", dict(a=8, b=16, c=64, d=128), dtype=eir.BF16, seed=44)
+    assert "reg4" in desc and re.search(r"t=\d+x1\b", desc), desc
 
 
 @pytest.mark.parametrize("threads", ["64", "128", "256", "512"])
