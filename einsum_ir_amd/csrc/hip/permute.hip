@@ -1516,7 +1516,14 @@ int plan_permute( int64_t         num_dims,
     // or four passes of 256 threads over c (longer runs of (c, i), measured
     // slower too)
     int64_t const l_blocks_c = ( a.size_i / l_vb ) * ( a.size_o / l_vb );
-    plan.reg4_threads = l_blocks_c <= 64 ? 64 : ( l_blocks_c <= 128 ? 128 : kThreads );
+    int32_t const l_threads_small = l_blocks_c <= 64 ? 64 : ( l_blocks_c <= 128 ? 128 : kThreads );
+    plan.reg4_threads = l_threads_small;
+    // 2-byte elements with a 16-wide output run and an input run of 64 or
+    // more: 512-thread workgroups (eight times the c values per workgroup)
+    // measured faster on every such shape (bf16 acdb 128x16x64x128: 61 -> 76
+    // % of HBM peak; five more, i of 64 to 256: 60-62 -> 74-77 %); an output
+    // run of 8 or 32, a short input run, and fp32 gain nothing or lose
+    if( plan.elem_bytes == 2 && a.size_o == 16 && a.size_i >= 64 && l_blocks_c <= 512 ) plan.reg4_threads = 512;
     plan.reg4_cpt = 1;
     if( char const * l_env = std::getenv( "ETIR_PERM_REG4_THREADS" ) ) {
       int const l_t = std::atoi( l_env );
@@ -1550,7 +1557,7 @@ int plan_permute( int64_t         num_dims,
     // the fewest conflicts among those whose tile fits the 64 KiB a
     // workgroup gets; where none does (several passes over c with a long i
     // run: bf16 acdb with a 128-wide input run, four passes, about 130 KiB)
-    // the planner takes one pass
+    // the planner takes one pass of the smallest workgroup
     auto pick_slots = [&]() -> bool {
       int32_t const l_nig = int32_t( a.size_i / l_vb ), l_nog = int32_t( a.size_o / l_vb );
       int32_t const l_si = int32_t( a.size_i );
@@ -1602,9 +1609,10 @@ int plan_permute( int64_t         num_dims,
       }
       return l_best >= 0;
     };
-    if( !pick_slots() && plan.reg4_cpt > 1 ) {
+    if( !pick_slots() ) {
       plan.reg4_cpt = 1;
-      plan.reg4_threads = l_blocks_c <= 64 ? 64 : ( l_blocks_c <= 128 ? 128 : kThreads );
+      plan.reg4_threads = l_threads_small;
+      plan.reg4_direct = false;
       a.c_chunk = (int32_t) std::max< int64_t >( 1, plan.reg4_threads / l_blocks_c );
       if( !pick_slots() ) return fail( ETIR_COMPILATION_FAILED, "permute: REG4 tile does not fit LDS" );
     }
